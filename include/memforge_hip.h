@@ -1,0 +1,219 @@
+/*
+ * memforge_hip.h -- C ABI of libmemforge_hip.so, the gfx950 (MI355X) device
+ * library behind MemForge's continuous-batching data path.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes,
+ * enqueues its kernels on `stream` (a hipStream_t, NULL for the default
+ * stream) and returns an int status: MF_OK (0) or a negative MF_ERR_* code.
+ * Nothing here allocates device memory or synchronises the stream; scratch
+ * space is passed in by the caller. Strides are in ELEMENTS, and the last
+ * (head_dim) axis of every K/V/Q tensor must be contiguous.
+ *
+ * Pool addressing (shared by every entry point that touches the KV pool):
+ * a slot index s = block * block_size + offset names one token of one
+ * physical block, and element (s, head, d) of one layer lives at
+ *     layer_base + block * pool_stride_block + offset * pool_stride_slot
+ *                + head * pool_stride_head + d.
+ * That covers both layouts the reference uses: PagedKVPool's
+ * (layers, blocks, slots, kv_heads, head_dim) and PagedKVCache's
+ * (blocks, heads, slots, head_dim).
+ */
+#ifndef MEMFORGE_HIP_H
+#define MEMFORGE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mf_stream_t; /* a hipStream_t */
+
+/* Element types. */
+enum { MF_F32 = 0, MF_F16 = 1, MF_BF16 = 2 };
+
+/* Status codes. */
+enum {
+    MF_OK = 0,
+    MF_ERR_ARG = -1,         /* bad size, stride, pointer or dtype */
+    MF_ERR_UNSUPPORTED = -2, /* head_dim / dtype combination not built */
+    MF_ERR_WORKSPACE = -3,   /* caller-supplied scratch is too small */
+    MF_ERR_HIP = -4          /* a HIP launch failed; see mf_last_hip_error */
+};
+
+/* Library version string and the last HIP error code seen by this thread. */
+const char* mf_version(void);
+int mf_last_hip_error(void);
+const char* mf_status_string(int status);
+
+/* ------------------------------------------------------------------ KV write
+ * Scatter `num_tokens` new key/value rows into one layer of the pool through
+ * slot_mapping (int64, one slot per row; a negative slot skips the row).
+ * Source row t, head h starts at src + t*src_stride_t + h*src_stride_h (the
+ * same strides for k_src and v_src). Converts src_dtype -> pool_dtype with
+ * round-to-nearest-even, so the result is bit-identical to torch's
+ * `.to(pool dtype)` followed by `index_copy_`.
+ * Replaces paged_gather.scatter_kv (memforge_ml/kernels/paged_gather.py:92-117),
+ * PagedKVPool.write / write_flat (memforge_ml/runtime/kv_pool.py:134-149,
+ * 181-192) and PagedKVCache.write_kv (memforge_ml/models/paged_attention.py:45-67).
+ */
+int mf_kv_write(const void* k_src, const void* v_src, int src_dtype,
+                int64_t src_stride_t, int64_t src_stride_h,
+                const int64_t* slot_mapping, int64_t num_tokens,
+                void* k_pool, void* v_pool, int pool_dtype,
+                int64_t pool_stride_block, int64_t pool_stride_slot,
+                int64_t pool_stride_head, int block_size, int num_heads,
+                int head_dim, mf_stream_t stream);
+
+/* ----------------------------------------------------------------- KV gather
+ * The inverse of mf_kv_write: copy pool slots slot_mapping[0..num_tokens) of
+ * one layer into dst rows (dst + t*dst_stride_t + h*dst_stride_h), converting
+ * pool_dtype -> dst_dtype.
+ * Replaces paged_gather.gather_kv (memforge_ml/kernels/paged_gather.py:58-89),
+ * PagedKVPool.gather / gather_flat (memforge_ml/runtime/kv_pool.py:151-179)
+ * and PagedKVCache.read_kv (memforge_ml/models/paged_attention.py:69-97).
+ */
+int mf_kv_gather(const void* k_pool, const void* v_pool, int pool_dtype,
+                 int64_t pool_stride_block, int64_t pool_stride_slot,
+                 int64_t pool_stride_head, int block_size,
+                 const int64_t* slot_mapping, int64_t num_tokens,
+                 void* k_dst, void* v_dst, int dst_dtype,
+                 int64_t dst_stride_t, int64_t dst_stride_h, int num_heads,
+                 int head_dim, mf_stream_t stream);
+
+/* --------------------------------------------------------------- ragged pack
+ * Build one step's packed token batch on the device from the scheduler's step
+ * output. `entries` (device, int32, B rows of MF_ENTRY_INTS) describes each
+ * sequence contributing tokens this step, in plan order:
+ *   [0] q_len      query tokens this step (chunk length, 1 for a decode,
+ *                  k+1 for a speculative verify row)
+ *   [1] start_pos  absolute position of the first of them
+ *   [2] kv_len     keys attention may read for this entry
+ *   [3] table_off  offset of its block table in `tables`
+ *   [4] table_len  entries in its block table
+ *   [5] token_off  offset of its q_len token ids in `tokens`
+ * Outputs (device): token_ids[T] and positions[T] (int64, the model's
+ * input_ids / position_ids), seq_slot[T] (entry index per row), slot_mapping[T]
+ * (int64, table[p / bs] * bs + p % bs), cu_seqlens[B+1], kv_lens[B] and the
+ * padded block_tables[B][max_blocks] (unused entries 0). T = sum of q_len.
+ * status (device, int32[4], written by this call) reports malformed input:
+ *   status[0] bit flags: MF_PACK_TABLE_OVERFLOW, MF_PACK_NEGATIVE_POSITION,
+ *             MF_PACK_DUPLICATE_SLOT, MF_PACK_BAD_ENTRY
+ *   status[1] first row needing a block past its table (or -1)
+ *   status[2] first row whose slot another row also writes (or -1)
+ *   status[3] first malformed entry (or -1)
+ * Duplicate detection runs when slot_bitmap is non-NULL: a device bitmap of
+ * num_slots bits that must be all-zero on entry and is all-zero again on exit.
+ * Replaces the engine's per-step packing (memforge_ml/runtime/
+ * continuous_engine.py:782-905, 1104-1131; batched_speculative.py:696-701) and
+ * VarlenPackedCache._build_write_index (memforge_ml/runtime/varlen_cache.py:161-191).
+ */
+#define MF_ENTRY_INTS 6
+#define MF_PACK_TABLE_OVERFLOW 1
+#define MF_PACK_NEGATIVE_POSITION 2
+#define MF_PACK_DUPLICATE_SLOT 4
+#define MF_PACK_BAD_ENTRY 8
+int mf_ragged_pack(const int32_t* entries, int num_entries,
+                   const int32_t* tables, const int32_t* tokens,
+                   int block_size, int max_blocks, int64_t total_tokens,
+                   int64_t* token_ids, int64_t* positions, int32_t* seq_slot,
+                   int64_t* slot_mapping, int32_t* cu_seqlens, int32_t* kv_lens,
+                   int32_t* block_tables, uint32_t* slot_bitmap,
+                   int64_t num_slots, int32_t* status, mf_stream_t stream);
+
+/* ----------------------------------------------------------- paged attention
+ * Varlen paged attention: one code path for decode, chunked prefill and the
+ * (k+1)-query speculative verify. Packed query rows of sequence s are
+ * cu_seqlens[s] .. cu_seqlens[s+1]-1 (through row_map[] when non-NULL, which
+ * maps packed index -> physical row of q/out/positions). Row r of sequence s
+ * attends, for every query head, to the keys of s at positions
+ * 0 .. positions[r] (inclusive) that are < kv_lens[s], with grouped-query
+ * heads (query head qh reads kv head qh / (num_q_heads / num_kv_heads)).
+ * Keys below pool_lens[s] (all keys when pool_lens is NULL) are read from the
+ * pool through block_tables[s][key / block_size]; keys at or above it are the
+ * in-flight rows of the same sequence's new tokens (new_k/new_v row
+ * cu_seqlens[s] + key - pool_lens[s], through row_map), which is how a verify
+ * pass attends to candidates it has not written to the pool. Softmax
+ * accumulates in fp32; out is written in `dtype` (the q/K/V dtype).
+ * Work is described by a plan from mf_attention_plan (device copy of its
+ * items/merges); `partials` is fp32 scratch of at least the planned size.
+ * Passing the plan's items with num_merges = 0, then a second call with no
+ * items and only the merges, runs the same work as one call in two launches
+ * (used to time the attention and merge kernels apart).
+ * Replaces paged_attention_varlen / _materialised (memforge_ml/kernels/
+ * varlen_attention.py:78-235, 291-395), paged_attention_blockwise
+ * (memforge_ml/kernels/block_attention.py:51-145), PagedAttention.forward
+ * (memforge_ml/models/paged_attention.py:108-141) and the Triton
+ * paged_decode_attention (memforge_ml/kernels/triton_paged_decode.py:129-176).
+ */
+int mf_paged_attention(const void* q, int64_t q_stride_row, int64_t q_stride_head,
+                       void* out, int64_t out_stride_row, int64_t out_stride_head,
+                       int dtype, const void* k_pool, const void* v_pool,
+                       int64_t pool_stride_block, int64_t pool_stride_slot,
+                       int64_t pool_stride_head, int block_size,
+                       const int32_t* block_tables, int64_t block_table_stride,
+                       const int32_t* cu_seqlens, const int32_t* kv_lens,
+                       const int64_t* positions, const int32_t* row_map,
+                       const int32_t* pool_lens, const void* new_k, const void* new_v,
+                       int64_t new_stride_row, int64_t new_stride_head,
+                       int num_q_heads, int num_kv_heads, int head_dim, float scale,
+                       const int32_t* plan_items, int64_t num_items_narrow,
+                       int64_t num_items_wide, const int32_t* plan_merges,
+                       int64_t num_merges, float* partials, int64_t partials_floats,
+                       mf_stream_t stream);
+
+/* Host-side planner for mf_paged_attention. Inputs are HOST arrays:
+ * cu_seqlens[B+1] and kv_lens[B]. Splits every (sequence, kv head, column
+ * tile) over key partitions of `partition_tiles` 16-key tiles (0 = chosen
+ * from the total work) and writes MF_PLAN_ITEM_INTS ints per work item to
+ * items (narrow items -- one 16-column tile -- first, then wide ones) and
+ * MF_PLAN_MERGE_INTS ints per split-K merge to merges. counts receives
+ * [num_items_narrow, num_items_wide, num_merges, partials_floats].
+ * A plan is valid for the dtype and head_dim it was made for.
+ * Returns MF_ERR_WORKSPACE if a capacity is too small (counts still holds
+ * the required sizes). */
+#define MF_PLAN_ITEM_INTS 8
+#define MF_PLAN_MERGE_INTS 8
+int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const int32_t* kv_lens,
+                      int num_q_heads, int num_kv_heads, int head_dim, int dtype,
+                      int partition_tiles, int32_t* items, int64_t items_capacity,
+                      int32_t* merges, int64_t merges_capacity, int64_t* counts);
+
+/* ----------------------------------------------------- rejection verify
+ * Speculative rejection sampling for B rows of K draft candidates, with the
+ * randomness supplied by the caller. For row b and i < K: p = target
+ * probability and q = draft probability of draft_tokens[b][i]; accept iff
+ * (double)u_accept[b][i] <= min(1, p / (q + 1e-9)) in double precision. The
+ * first rejection resamples from normalise(max(p_vec - q_vec, 0)) (or from
+ * the target distribution when that residual sums to 0) and stops the row;
+ * if all K are accepted a bonus token is drawn from target position K. A draw
+ * from distribution w is argmax_i(w_i / exp_noise[b][i]) (first index on
+ * ties), which is torch.multinomial(w, 1) given the same Exp(1) noise.
+ * Target probabilities are softmax(target_logits[b][i][:V] / temperature) in
+ * fp32, or a one-hot argmax when temperature <= 0; target logits wider than the
+ * draft vocabulary V are clipped to V first.
+ * Outputs: out_tokens[b][0..out_count[b]) (at most K+1), out_is_draft likewise,
+ * out_num_accepted[b] draft tokens accepted.
+ * workspace: at least mf_spec_verify_workspace_size(B, K) bytes.
+ * Replaces RejectionSampler.verify_tokens / sample_from_probs
+ * (memforge_ml/speculative/rejection_sampler.py:12-83) and resolve_round /
+ * _probs_from_logits (memforge_ml/runtime/batched_speculative.py:112-124, 731-777).
+ */
+int64_t mf_spec_verify_workspace_size(int num_rows, int num_draft);
+int mf_spec_verify(int num_rows, int num_draft, int vocab,
+                   const int32_t* draft_tokens,
+                   const float* draft_probs, int64_t dp_stride_row, int64_t dp_stride_pos,
+                   const void* target_logits, int target_dtype,
+                   int64_t tl_stride_row, int64_t tl_stride_pos,
+                   float temperature, const float* u_accept,
+                   const float* exp_noise, int64_t noise_stride_row,
+                   int32_t* out_tokens, uint8_t* out_is_draft, int32_t* out_count,
+                   int32_t* out_num_accepted, void* workspace, int64_t workspace_bytes,
+                   mf_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEMFORGE_HIP_H */

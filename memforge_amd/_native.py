@@ -1,0 +1,390 @@
+"""ctypes binding of ``libmemforge_hip.so`` (the C ABI in ``include/memforge_hip.h``).
+
+This module is the only place Python touches the device library. Every
+function takes torch tensors that already live on the GPU, passes their data
+pointers and element strides to the C entry point on torch's current stream,
+and raises if the library is missing, a tensor is on the wrong device, or the
+entry point returns an error status. There is no fallback path: the data path
+runs on the MI355X or not at all.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libmemforge_hip.so")
+
+MF_F32, MF_F16, MF_BF16 = 0, 1, 2
+DTYPE_CODES = {torch.float32: MF_F32, torch.float16: MF_F16, torch.bfloat16: MF_BF16}
+
+PLAN_ITEM_INTS = 8
+PLAN_MERGE_INTS = 8
+ENTRY_INTS = 6
+
+PACK_TABLE_OVERFLOW = 1
+PACK_NEGATIVE_POSITION = 2
+PACK_DUPLICATE_SLOT = 4
+PACK_BAD_ENTRY = 8
+
+_c_int, _c_i64, _c_f32, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+
+_SIGNATURES = {
+    "mf_version": (ctypes.c_char_p, []),
+    "mf_last_hip_error": (_c_int, []),
+    "mf_status_string": (ctypes.c_char_p, [_c_int]),
+    "mf_kv_write": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_int,
+                             _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp]),
+    "mf_kv_gather": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _vp, _c_i64,
+                              _vp, _vp, _c_int, _c_i64, _c_i64, _c_int, _c_int, _vp]),
+    "mf_ragged_pack": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_i64, _vp, _vp, _vp,
+                                _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),
+    "mf_paged_attention": (_c_int, [
+        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
+        _c_int, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int,
+        _c_int, _c_f32, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp]),
+    "mf_attention_plan": (_c_int, [_c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                   _vp, _c_i64, _vp, _c_i64, _vp]),
+    "mf_spec_verify_workspace_size": (_c_i64, [_c_int, _c_int]),
+    "mf_spec_verify": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _c_i64, _c_i64, _vp, _c_int,
+                                _c_i64, _c_i64, _c_f32, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp,
+                                _vp, _c_i64, _vp]),
+}
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def exported_symbols() -> Tuple[str, ...]:
+    return tuple(_SIGNATURES)
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded device library; raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH.name} is not built; run `python -m memforge_amd._build` "
+                "(memforge_amd has no CPU fallback)"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _LIB = handle
+    return _LIB
+
+
+class MemforgeHipError(RuntimeError):
+    """A device entry point rejected its arguments or failed to launch."""
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        L = lib()
+        msg = L.mf_status_string(status).decode()
+        raise MemforgeHipError(f"{what}: {msg} (status {status}, hip error {L.mf_last_hip_error()})")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def require_device(*tensors: Optional[torch.Tensor]) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError(
+                f"memforge_amd runs on the GPU; got a tensor on {t.device} "
+                "(there is no CPU path)"
+            )
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}; expected float32, float16 or bfloat16") from None
+
+
+# --------------------------------------------------------------- pool views
+
+@dataclass(frozen=True)
+class PoolView:
+    """One layer of a paged K or V pool as the C ABI addresses it."""
+
+    k: torch.Tensor  # tensor whose data_ptr is the layer base
+    v: torch.Tensor
+    stride_block: int
+    stride_slot: int
+    stride_head: int
+    block_size: int
+    num_heads: int
+    head_dim: int
+
+    @staticmethod
+    def from_bshd(k: torch.Tensor, v: torch.Tensor) -> "PoolView":
+        """``(blocks, slots, heads, dim)`` -- one layer of PagedKVPool."""
+        if k.shape != v.shape or k.stride() != v.stride() or k.dtype != v.dtype:
+            raise ValueError("K and V pools must share shape, strides and dtype")
+        if k.stride(-1) != 1:
+            raise ValueError("pool head_dim axis must be contiguous")
+        n, bs, h, d = k.shape
+        return PoolView(k, v, k.stride(0), k.stride(1), k.stride(2), bs, h, d)
+
+    @staticmethod
+    def from_bhsd(k: torch.Tensor, v: torch.Tensor) -> "PoolView":
+        """``(blocks, heads, slots, dim)`` -- PagedKVCache's per-head layout."""
+        if k.shape != v.shape or k.stride() != v.stride() or k.dtype != v.dtype:
+            raise ValueError("K and V pools must share shape, strides and dtype")
+        if k.stride(-1) != 1:
+            raise ValueError("pool head_dim axis must be contiguous")
+        n, h, bs, d = k.shape
+        return PoolView(k, v, k.stride(0), k.stride(2), k.stride(1), bs, h, d)
+
+
+def _rows_ok(t: torch.Tensor, name: str) -> None:
+    if t.dim() != 3:
+        raise ValueError(f"{name} must be a (tokens, heads, head_dim) view, got {tuple(t.shape)}")
+    if t.stride(-1) != 1 and t.shape[-1] > 1:
+        raise ValueError(f"{name} head_dim axis must be contiguous")
+
+
+# ----------------------------------------------------------- KV write/gather
+
+def kv_write(k_rows: torch.Tensor, v_rows: torch.Tensor, slots: torch.Tensor, pool: PoolView) -> None:
+    """Scatter (T, H, D) rows into pool slots ``slots`` (int64, device)."""
+    _rows_ok(k_rows, "k_rows")
+    _rows_ok(v_rows, "v_rows")
+    if k_rows.stride() != v_rows.stride():
+        v_rows = v_rows.contiguous()
+        k_rows = k_rows.contiguous()
+    require_device(k_rows, v_rows, slots, pool.k)
+    if slots.dtype != torch.int64 or not slots.is_contiguous():
+        slots = slots.to(torch.int64).contiguous()
+    T, H, D = k_rows.shape
+    if H != pool.num_heads or D != pool.head_dim or slots.numel() != T:
+        raise ValueError(
+            f"rows {tuple(k_rows.shape)} / {slots.numel()} slots do not match a pool of "
+            f"{pool.num_heads} heads x {pool.head_dim}"
+        )
+    _check(lib().mf_kv_write(
+        _ptr(k_rows), _ptr(v_rows), dtype_code(k_rows.dtype), k_rows.stride(0), k_rows.stride(1),
+        _ptr(slots), T, _ptr(pool.k), _ptr(pool.v), dtype_code(pool.k.dtype),
+        pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size, H, D, _stream(),
+    ), "mf_kv_write")
+
+
+def kv_gather(pool: PoolView, slots: torch.Tensor, k_rows: torch.Tensor, v_rows: torch.Tensor) -> None:
+    """Copy pool slots ``slots`` into preallocated (T, H, D) rows."""
+    _rows_ok(k_rows, "k_rows")
+    _rows_ok(v_rows, "v_rows")
+    if k_rows.stride() != v_rows.stride():
+        raise ValueError("k_rows and v_rows must share strides")
+    require_device(k_rows, v_rows, slots, pool.k)
+    if slots.dtype != torch.int64 or not slots.is_contiguous():
+        slots = slots.to(torch.int64).contiguous()
+    T, H, D = k_rows.shape
+    _check(lib().mf_kv_gather(
+        _ptr(pool.k), _ptr(pool.v), dtype_code(pool.k.dtype), pool.stride_block, pool.stride_slot,
+        pool.stride_head, pool.block_size, _ptr(slots), T, _ptr(k_rows), _ptr(v_rows),
+        dtype_code(k_rows.dtype), k_rows.stride(0), k_rows.stride(1), H, D, _stream(),
+    ), "mf_kv_gather")
+
+
+# ---------------------------------------------------------------- attention
+
+@dataclass
+class AttentionPlan:
+    """Work list for one mf_paged_attention call (valid for its dtype/head_dim)."""
+
+    items: torch.Tensor      # int32 device, (n_items, 8)
+    merges: torch.Tensor     # int32 device, (n_merges, 8)
+    n_narrow: int
+    n_wide: int
+    n_merges: int
+    partials_floats: int
+    items_host: np.ndarray
+    merges_host: np.ndarray
+
+
+def plan_attention(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int,
+                   num_kv_heads: int, head_dim: int, dtype: torch.dtype, device,
+                   partition_tiles: int = 0) -> AttentionPlan:
+    cu = np.ascontiguousarray(np.asarray(cu_seqlens, dtype=np.int32))
+    kv = np.ascontiguousarray(np.asarray(kv_lens, dtype=np.int32))
+    B = kv.shape[0]
+    if cu.shape[0] != B + 1:
+        raise ValueError("cu_seqlens must have one more entry than kv_lens")
+    counts = np.zeros(4, dtype=np.int64)
+    L = lib()
+    args = (B, cu.ctypes.data, kv.ctypes.data, num_q_heads, num_kv_heads, head_dim,
+            dtype_code(dtype), partition_tiles)
+    st = L.mf_attention_plan(*args, None, 0, None, 0, counts.ctypes.data)
+    if st not in (0, -3):
+        _check(st, "mf_attention_plan")
+    n_items = int(counts[0] + counts[1])
+    n_merges = int(counts[2])
+    items = np.zeros((max(n_items, 1), PLAN_ITEM_INTS), dtype=np.int32)
+    merges = np.zeros((max(n_merges, 1), PLAN_MERGE_INTS), dtype=np.int32)
+    _check(L.mf_attention_plan(*args, items.ctypes.data, n_items, merges.ctypes.data, n_merges,
+                               counts.ctypes.data), "mf_attention_plan")
+    dev_items = torch.from_numpy(items).to(device, non_blocking=False)
+    dev_merges = torch.from_numpy(merges).to(device, non_blocking=False)
+    return AttentionPlan(dev_items, dev_merges, int(counts[0]), int(counts[1]), n_merges,
+                         int(counts[3]), items[:n_items], merges[:n_merges])
+
+
+class Workspace:
+    """Grow-only fp32 scratch for split-K partials, one per device."""
+
+    def __init__(self) -> None:
+        self._buf: Optional[torch.Tensor] = None
+
+    def get(self, floats: int, device) -> Optional[torch.Tensor]:
+        if floats <= 0:
+            return None
+        if self._buf is None or self._buf.numel() < floats or self._buf.device != torch.device(device):
+            self._buf = torch.empty(max(floats, 1 << 16), dtype=torch.float32, device=device)
+        return self._buf
+
+
+_WORKSPACE = Workspace()
+
+
+def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView,
+                    block_tables: torch.Tensor, cu_seqlens: torch.Tensor, kv_lens: torch.Tensor,
+                    positions: torch.Tensor, plan: AttentionPlan, scale: float,
+                    num_kv_heads: int, row_map: Optional[torch.Tensor] = None,
+                    pool_lens: Optional[torch.Tensor] = None,
+                    new_k_rows: Optional[torch.Tensor] = None,
+                    new_v_rows: Optional[torch.Tensor] = None,
+                    partials: Optional[torch.Tensor] = None) -> None:
+    """Varlen paged attention into ``out_rows`` ((rows, Hq, D) views, device)."""
+    _rows_ok(q_rows, "q_rows")
+    _rows_ok(out_rows, "out_rows")
+    require_device(q_rows, out_rows, pool.k, block_tables, cu_seqlens, kv_lens, positions)
+    if q_rows.dtype != pool.k.dtype or out_rows.dtype != pool.k.dtype:
+        raise TypeError("query, output and pool must share a dtype")
+    for name, t, dt in (("block_tables", block_tables, torch.int32), ("cu_seqlens", cu_seqlens, torch.int32),
+                        ("kv_lens", kv_lens, torch.int32), ("positions", positions, torch.int64)):
+        if t.dtype != dt or not t.is_contiguous():
+            raise TypeError(f"{name} must be a contiguous {dt} tensor")
+    Hq, D = q_rows.shape[1], q_rows.shape[2]
+    if partials is None:
+        partials = _WORKSPACE.get(plan.partials_floats, q_rows.device)
+    nk = new_k_rows if new_k_rows is not None else None
+    nv = new_v_rows if new_v_rows is not None else None
+    if pool_lens is not None:
+        if nk is None or nv is None:
+            raise ValueError("pool_lens needs the in-flight new_k_rows/new_v_rows")
+        require_device(pool_lens, nk, nv)
+        if nk.stride() != nv.stride():
+            raise ValueError("in-flight K and V rows must share strides")
+    bt_stride = block_tables.shape[1] if block_tables.dim() == 2 else 0
+    _check(lib().mf_paged_attention(
+        _ptr(q_rows), q_rows.stride(0), q_rows.stride(1),
+        _ptr(out_rows), out_rows.stride(0), out_rows.stride(1),
+        dtype_code(q_rows.dtype), _ptr(pool.k), _ptr(pool.v),
+        pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size,
+        _ptr(block_tables), bt_stride, _ptr(cu_seqlens), _ptr(kv_lens), _ptr(positions),
+        _ptr(row_map), _ptr(pool_lens), _ptr(nk), _ptr(nv),
+        nk.stride(0) if nk is not None else 0, nk.stride(1) if nk is not None else 0,
+        Hq, num_kv_heads, D, float(scale),
+        _ptr(plan.items), plan.n_narrow, plan.n_wide, _ptr(plan.merges), plan.n_merges,
+        _ptr(partials), partials.numel() if partials is not None else 0, _stream(),
+    ), "mf_paged_attention")
+
+
+# -------------------------------------------------------------- ragged pack
+
+@dataclass
+class PackedStep:
+    token_ids: torch.Tensor     # int64 [T]
+    positions: torch.Tensor     # int64 [T]
+    seq_slot: torch.Tensor      # int32 [T]
+    slot_mapping: torch.Tensor  # int64 [T]
+    cu_seqlens: torch.Tensor    # int32 [B+1]
+    kv_lens: torch.Tensor       # int32 [B]
+    block_tables: torch.Tensor  # int32 [B, max_blocks]
+    status: torch.Tensor        # int32 [4]
+
+
+def ragged_pack(entries: torch.Tensor, tables: torch.Tensor, tokens: torch.Tensor,
+                total_tokens: int, block_size: int, max_blocks: int,
+                slot_bitmap: Optional[torch.Tensor] = None, num_slots: int = 0) -> PackedStep:
+    """Run mf_ragged_pack on device descriptors (int32 tensors already on the GPU)."""
+    require_device(entries, tables, tokens)
+    dev = entries.device
+    B = entries.shape[0]
+    out = PackedStep(
+        token_ids=torch.empty(total_tokens, dtype=torch.int64, device=dev),
+        positions=torch.empty(total_tokens, dtype=torch.int64, device=dev),
+        seq_slot=torch.empty(total_tokens, dtype=torch.int32, device=dev),
+        slot_mapping=torch.empty(total_tokens, dtype=torch.int64, device=dev),
+        cu_seqlens=torch.empty(B + 1, dtype=torch.int32, device=dev),
+        kv_lens=torch.empty(B, dtype=torch.int32, device=dev),
+        block_tables=torch.empty((B, max_blocks), dtype=torch.int32, device=dev),
+        status=torch.empty(4, dtype=torch.int32, device=dev),
+    )
+    _check(lib().mf_ragged_pack(
+        _ptr(entries), B, _ptr(tables), _ptr(tokens), block_size, max_blocks, total_tokens,
+        _ptr(out.token_ids), _ptr(out.positions), _ptr(out.seq_slot), _ptr(out.slot_mapping),
+        _ptr(out.cu_seqlens), _ptr(out.kv_lens), _ptr(out.block_tables), _ptr(slot_bitmap),
+        num_slots, _ptr(out.status), _stream(),
+    ), "mf_ragged_pack")
+    return out
+
+
+# --------------------------------------------------------- rejection verify
+
+@dataclass
+class VerifyResult:
+    tokens: torch.Tensor        # int32 [B, K+1]
+    is_draft: torch.Tensor      # uint8 [B, K+1]
+    count: torch.Tensor         # int32 [B]
+    num_accepted: torch.Tensor  # int32 [B]
+
+
+def spec_verify(draft_tokens: torch.Tensor, draft_probs: torch.Tensor, target_logits: torch.Tensor,
+                temperature: float, u_accept: torch.Tensor, exp_noise: torch.Tensor) -> VerifyResult:
+    """Batched rejection sampling. Shapes: draft_tokens (B, K) int32,
+    draft_probs (B, K, V) fp32, target_logits (B, K+1, >=V), u_accept (B, K) fp32,
+    exp_noise (B, V) fp32."""
+    require_device(draft_tokens, draft_probs, target_logits, u_accept, exp_noise)
+    B, K = draft_tokens.shape
+    V = draft_probs.shape[-1] if K > 0 else exp_noise.shape[-1]
+    if target_logits.shape[0] != B or target_logits.shape[1] != K + 1 or target_logits.shape[2] < V:
+        raise ValueError(f"target logits {tuple(target_logits.shape)} do not cover ({B}, {K + 1}, {V})")
+    if target_logits.stride(-1) != 1 or draft_probs.stride(-1) != 1 or exp_noise.stride(-1) != 1:
+        raise ValueError("vocabulary axes must be contiguous")
+    draft_tokens = draft_tokens.to(torch.int32).contiguous()
+    u_accept = u_accept.to(torch.float32).contiguous()
+    dev = target_logits.device
+    res = VerifyResult(
+        tokens=torch.zeros((B, K + 1), dtype=torch.int32, device=dev),
+        is_draft=torch.zeros((B, K + 1), dtype=torch.uint8, device=dev),
+        count=torch.empty(B, dtype=torch.int32, device=dev),
+        num_accepted=torch.empty(B, dtype=torch.int32, device=dev),
+    )
+    L = lib()
+    ws_bytes = int(L.mf_spec_verify_workspace_size(B, K))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _check(L.mf_spec_verify(
+        B, K, V, _ptr(draft_tokens), _ptr(draft_probs),
+        draft_probs.stride(0) if K > 0 else 0, draft_probs.stride(1) if K > 0 else 0,
+        _ptr(target_logits), dtype_code(target_logits.dtype), target_logits.stride(0),
+        target_logits.stride(1), float(temperature), _ptr(u_accept), _ptr(exp_noise),
+        exp_noise.stride(0), _ptr(res.tokens), _ptr(res.is_draft), _ptr(res.count),
+        _ptr(res.num_accepted), _ptr(ws), ws_bytes, _stream(),
+    ), "mf_spec_verify")
+    return res

@@ -1,0 +1,216 @@
+// KV write (slot_mapping scatter) and KV gather for the paged pool.
+//
+// One thread moves one chunk of VW consecutive head_dim elements of one
+// (token, head) pair for both K and V, so a wave covers whole 16-byte runs of
+// the pool row and the HBM traffic is exactly the bytes moved. The copy is a
+// pure permutation plus an optional dtype conversion (round to nearest even),
+// which makes it bit-identical to torch's index_copy_ / index_select of the
+// same data (memforge_ml/kernels/paged_gather.py:58-117).
+#include "mf_common.h"
+
+namespace mf {
+namespace {
+
+// Loads N bytes (N in {2,4,8,16,32}) into 32-bit words.
+template <int N>
+__device__ __forceinline__ void load_words(const char* p, uint32_t* w) {
+    if constexpr (N == 2) {
+        w[0] = *(const uint16_t*)p;
+    } else if constexpr (N == 4) {
+        w[0] = *(const uint32_t*)p;
+    } else if constexpr (N == 8) {
+        uint2 v = *(const uint2*)p;
+        w[0] = v.x; w[1] = v.y;
+    } else if constexpr (N == 16) {
+        uint4 v = *(const uint4*)p;
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else {
+        static_assert(N == 32, "chunk size");
+        uint4 a = *(const uint4*)p;
+        uint4 b = *(const uint4*)(p + 16);
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+        w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void store_words(char* p, const uint32_t* w) {
+    if constexpr (N == 2) {
+        *(uint16_t*)p = (uint16_t)w[0];
+    } else if constexpr (N == 4) {
+        *(uint32_t*)p = w[0];
+    } else if constexpr (N == 8) {
+        *(uint2*)p = make_uint2(w[0], w[1]);
+    } else if constexpr (N == 16) {
+        *(uint4*)p = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        static_assert(N == 32, "chunk size");
+        *(uint4*)p = make_uint4(w[0], w[1], w[2], w[3]);
+        *(uint4*)(p + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+    }
+}
+
+template <int ES>
+__device__ __forceinline__ uint32_t get_elem(const uint32_t* w, int e) {
+    if constexpr (ES == 4) return w[e];
+    else return (w[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+}
+template <int ES>
+__device__ __forceinline__ void set_elem(uint32_t* w, int e, uint32_t v) {
+    if constexpr (ES == 4) {
+        w[e] = v;
+    } else {
+        const int sh = (e & 1) * 16;
+        w[e >> 1] = (w[e >> 1] & ~(0xffffu << sh)) | (v << sh);
+    }
+}
+
+// Copies VW elements from `src` (dtype SDT) to `dst` (dtype DDT).
+template <int SDT, int DDT, int VW>
+__device__ __forceinline__ void copy_chunk(const char* src, char* dst) {
+    constexpr int SES = SDT == MF_F32 ? 4 : 2;
+    constexpr int DES = DDT == MF_F32 ? 4 : 2;
+    uint32_t in[(VW * SES + 3) / 4];
+    load_words<VW * SES>(src, in);
+    if constexpr (SDT == DDT) {
+        store_words<VW * DES>(dst, in);
+    } else {
+        uint32_t out[(VW * DES + 3) / 4] = {};
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+            const float f = bits_to_f32<SDT>(get_elem<SES>(in, e));
+            set_elem<DES>(out, e, f32_to_bits<DDT>(f));
+        }
+        store_words<VW * DES>(dst, out);
+    }
+}
+
+struct CopyArgs {
+    const char* row_k;   // contiguous-row side (source of a write, dest of a gather)
+    const char* row_v;
+    int64_t row_st, row_sh;  // elements
+    char* pool_k;
+    char* pool_v;
+    int64_t p_sb, p_ss, p_sh;  // elements
+    const int64_t* slots;
+    int64_t num_tokens;
+    int block_size, num_heads, head_dim;
+};
+
+// GATHER=false: rows -> pool (write). GATHER=true: pool -> rows (gather).
+template <int RDT, int PDT, int VW, bool GATHER>
+__global__ __launch_bounds__(256) void kv_copy_kernel(CopyArgs a) {
+    constexpr int RES = RDT == MF_F32 ? 4 : 2;
+    constexpr int PES = PDT == MF_F32 ? 4 : 2;
+    const int chunks = a.head_dim / VW;
+    const int64_t per_tok = (int64_t)a.num_heads * chunks;
+    const int64_t total = a.num_tokens * per_tok;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = idx / per_tok;
+        const int rem = (int)(idx - t * per_tok);
+        const int h = rem / chunks;
+        const int c = rem - h * chunks;
+        const int64_t slot = a.slots[t];
+        if (slot < 0) continue;
+        const int64_t blk = slot / a.block_size;
+        const int64_t off = slot - blk * a.block_size;
+        const int64_t pe = blk * a.p_sb + off * a.p_ss + (int64_t)h * a.p_sh + (int64_t)c * VW;
+        const int64_t re = t * a.row_st + (int64_t)h * a.row_sh + (int64_t)c * VW;
+        if constexpr (!GATHER) {
+            copy_chunk<RDT, PDT, VW>(a.row_k + re * RES, a.pool_k + pe * PES);
+            copy_chunk<RDT, PDT, VW>(a.row_v + re * RES, a.pool_v + pe * PES);
+        } else {
+            copy_chunk<PDT, RDT, VW>(a.pool_k + pe * PES, (char*)a.row_k + re * RES);
+            copy_chunk<PDT, RDT, VW>(a.pool_v + pe * PES, (char*)a.row_v + re * RES);
+        }
+    }
+}
+
+template <int RDT, int PDT, bool GATHER>
+int launch_copy(const CopyArgs& a, hipStream_t stream) {
+    // Widest chunk that keeps every access aligned: all strides and both base
+    // pointers must be multiples of the chunk.
+    auto aligned = [&](int vw) {
+        if (a.head_dim % vw) return false;
+        const int64_t strides[] = {a.row_st, a.row_sh, a.p_sb, a.p_ss, a.p_sh};
+        for (int64_t s : strides)
+            if (s % vw) return false;
+        const uintptr_t rb = (uintptr_t)vw * (RDT == MF_F32 ? 4 : 2);
+        const uintptr_t pb = (uintptr_t)vw * (PDT == MF_F32 ? 4 : 2);
+        return ((uintptr_t)a.row_k % rb == 0) && ((uintptr_t)a.row_v % rb == 0) &&
+               ((uintptr_t)a.pool_k % pb == 0) && ((uintptr_t)a.pool_v % pb == 0);
+    };
+    const int64_t total_base = a.num_tokens * a.num_heads;
+    auto grid_for = [&](int vw) {
+        const int64_t threads = total_base * (a.head_dim / vw);
+        int64_t blocks = (threads + 255) / 256;
+        if (blocks > 65536) blocks = 65536;
+        if (blocks < 1) blocks = 1;
+        return (unsigned)blocks;
+    };
+    if (aligned(8)) {
+        hipLaunchKernelGGL((kv_copy_kernel<RDT, PDT, 8, GATHER>), dim3(grid_for(8)), dim3(256), 0, stream, a);
+    } else if (aligned(4)) {
+        hipLaunchKernelGGL((kv_copy_kernel<RDT, PDT, 4, GATHER>), dim3(grid_for(4)), dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((kv_copy_kernel<RDT, PDT, 1, GATHER>), dim3(grid_for(1)), dim3(256), 0, stream, a);
+    }
+    return check_launch();
+}
+
+template <bool GATHER>
+int dispatch_copy(int rdt, int pdt, const CopyArgs& a, hipStream_t stream) {
+#define MF_COPY_CASE(R, P) \
+    if (rdt == R && pdt == P) return launch_copy<R, P, GATHER>(a, stream);
+    MF_COPY_CASE(MF_F32, MF_F32)
+    MF_COPY_CASE(MF_F32, MF_F16)
+    MF_COPY_CASE(MF_F32, MF_BF16)
+    MF_COPY_CASE(MF_F16, MF_F32)
+    MF_COPY_CASE(MF_F16, MF_F16)
+    MF_COPY_CASE(MF_F16, MF_BF16)
+    MF_COPY_CASE(MF_BF16, MF_F32)
+    MF_COPY_CASE(MF_BF16, MF_F16)
+    MF_COPY_CASE(MF_BF16, MF_BF16)
+#undef MF_COPY_CASE
+    return MF_ERR_ARG;
+}
+
+bool copy_args_ok(const CopyArgs& a, int rdt, int pdt) {
+    if (!dtype_ok(rdt) || !dtype_ok(pdt)) return false;
+    if (a.num_tokens < 0 || a.block_size <= 0 || a.num_heads <= 0 || a.head_dim <= 0) return false;
+    if (a.num_tokens > 0 && (!a.row_k || !a.row_v || !a.pool_k || !a.pool_v || !a.slots)) return false;
+    return true;
+}
+
+}  // namespace
+}  // namespace mf
+
+extern "C" int mf_kv_write(const void* k_src, const void* v_src, int src_dtype,
+                           int64_t src_stride_t, int64_t src_stride_h,
+                           const int64_t* slot_mapping, int64_t num_tokens, void* k_pool,
+                           void* v_pool, int pool_dtype, int64_t pool_stride_block,
+                           int64_t pool_stride_slot, int64_t pool_stride_head, int block_size,
+                           int num_heads, int head_dim, mf_stream_t stream) {
+    mf::CopyArgs a{(const char*)k_src, (const char*)v_src, src_stride_t, src_stride_h,
+                   (char*)k_pool, (char*)v_pool, pool_stride_block, pool_stride_slot,
+                   pool_stride_head, slot_mapping, num_tokens, block_size, num_heads, head_dim};
+    if (!mf::copy_args_ok(a, src_dtype, pool_dtype)) return MF_ERR_ARG;
+    if (num_tokens == 0) return MF_OK;
+    return mf::dispatch_copy<false>(src_dtype, pool_dtype, a, (hipStream_t)stream);
+}
+
+extern "C" int mf_kv_gather(const void* k_pool, const void* v_pool, int pool_dtype,
+                            int64_t pool_stride_block, int64_t pool_stride_slot,
+                            int64_t pool_stride_head, int block_size,
+                            const int64_t* slot_mapping, int64_t num_tokens, void* k_dst,
+                            void* v_dst, int dst_dtype, int64_t dst_stride_t,
+                            int64_t dst_stride_h, int num_heads, int head_dim,
+                            mf_stream_t stream) {
+    mf::CopyArgs a{(const char*)k_dst, (const char*)v_dst, dst_stride_t, dst_stride_h,
+                   (char*)k_pool, (char*)v_pool, pool_stride_block, pool_stride_slot,
+                   pool_stride_head, slot_mapping, num_tokens, block_size, num_heads, head_dim};
+    if (!mf::copy_args_ok(a, dst_dtype, pool_dtype)) return MF_ERR_ARG;
+    if (num_tokens == 0) return MF_OK;
+    return mf::dispatch_copy<true>(dst_dtype, pool_dtype, a, (hipStream_t)stream);
+}

@@ -1,0 +1,734 @@
+// Varlen paged attention for gfx950: one code path for decode, chunked
+// prefill and the (k+1)-query speculative verify.
+//
+// Work decomposition. A "column" is one (query row, query head) pair; the G
+// query heads that share a KV head are adjacent columns, so a decode row of a
+// GQA group-5 model is 5 columns and a 5-token verify row of a group-3 model is
+// 15. One wave owns a work item = (sequence, kv head, up to NT tiles of 16
+// columns, a range of 16-key tiles), reads every K/V tile of that range exactly
+// once and shares it across all of its columns.
+//
+// Per 16-key tile the wave computes S^T = K Q^T with MFMA (A = K rows straight
+// from the pool, B = the Q fragment kept in registers), applies the per-column
+// causal rule key <= position(row), runs the online softmax with the column
+// max reduced across the four 16-lane groups by xor shuffles, and accumulates
+// O^T = V^T P^T with a second MFMA whose B operand is the exponentiated S^T
+// tile exactly as the first MFMA left it in registers. V arrives with
+// fully coalesced 16-token x 16-byte row loads and is transposed into the MFMA
+// A layout with byte permutes; no LDS is used at all.
+//
+// Long contexts are split into key partitions (the plan decides); partial
+// (max, sum, unnormalised output) triples go to fp32 scratch and a merge
+// kernel combines them with the log-sum-exp rule.
+#include <algorithm>
+#include <cmath>
+
+#include "mf_common.h"
+
+namespace mf {
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+
+constexpr int kWaves = 4;  // waves per workgroup; each wave runs its own item
+
+// 16-column tiles one wave carries for multi-tile (prefill / wide verify)
+// items: as many as fit in registers without spilling.
+__host__ __device__ constexpr int wide_tiles(int dt, int dp) {
+    return dt == MF_F32 ? (dp >= 128 ? 2 : 4) : (dp >= 256 ? 1 : 4);
+}
+
+struct AttnArgs {
+    const char* q;
+    int64_t q_sr, q_sh;
+    char* out;
+    int64_t o_sr, o_sh;
+    const char* k_pool;
+    const char* v_pool;
+    int64_t p_sb, p_ss, p_sh;
+    int block_size;
+    const int32_t* block_tables;
+    int64_t bt_stride;
+    const int32_t* cu_seqlens;
+    const int32_t* kv_lens;
+    const int64_t* positions;
+    const int32_t* row_map;
+    const int32_t* pool_lens;
+    const char* new_k;
+    const char* new_v;
+    int64_t n_sr, n_sh;
+    int G;
+    int head_dim;
+    float scale_log2;
+    const int32_t* items;
+    int num_items;
+    float* partials;
+    int part_dstride;  // floats per column of a partial slot's output block
+};
+
+// ------------------------------------------------------------- MFMA wrappers
+// S^T tile: 16 keys x 16 columns, contraction over one 16-byte chunk of
+// head_dim per lane (8 x 16-bit or 4 x fp32 elements).
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_qk(uint4 a, uint4 b, f32x4 c) {
+    if constexpr (DT == MF_BF16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    } else if constexpr (DT == MF_F16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    } else {
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.x), __uint_as_float(b.x), c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.y), __uint_as_float(b.y), c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.z), __uint_as_float(b.z), c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.w), __uint_as_float(b.w), c, 0, 0, 0);
+        return c;
+    }
+}
+
+// O^T tile: 16 head_dim rows x 16 columns, contraction over 16 keys
+// (4 per lane) for 16-bit types.
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_pv16(uint2 a, uint2 b, f32x4 c) {
+    if constexpr (DT == MF_BF16) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                         __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                     __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+    }
+}
+
+// ---------------------------------------------------------- memory helpers
+template <int N>
+__device__ __forceinline__ void ld_words(const char* p, uint32_t* w) {
+    if constexpr (N == 4) {
+        w[0] = *(const uint32_t*)p;
+    } else if constexpr (N == 8) {
+        const uint2 v = *(const uint2*)p;
+        w[0] = v.x; w[1] = v.y;
+    } else {
+        static_assert(N % 16 == 0, "chunk");
+#pragma unroll
+        for (int k = 0; k < N / 16; ++k) {
+            const uint4 v = *(const uint4*)(p + 16 * k);
+            w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
+        }
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void st_words(char* p, const uint32_t* w) {
+    if constexpr (N == 4) {
+        *(uint32_t*)p = w[0];
+    } else if constexpr (N == 8) {
+        *(uint2*)p = make_uint2(w[0], w[1]);
+    } else {
+        static_assert(N % 16 == 0, "chunk");
+#pragma unroll
+        for (int k = 0; k < N / 16; ++k)
+            *(uint4*)(p + 16 * k) = make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
+    }
+}
+
+// Writes the lane's contiguous chunk of 4*VCH output elements (value e is
+// vals[e]) in dtype DT.
+template <int DT, int VCH>
+__device__ __forceinline__ void store_out_chunk(char* p, const float* vals) {
+    constexpr int NE = 4 * VCH;
+    if constexpr (DT == MF_F32) {
+        uint32_t w[NE];
+#pragma unroll
+        for (int e = 0; e < NE; ++e) w[e] = __float_as_uint(vals[e]);
+        st_words<NE * 4>(p, w);
+    } else {
+        uint32_t w[NE / 2];
+#pragma unroll
+        for (int e = 0; e < NE / 2; ++e)
+            w[e] = f32_to_bits<DT>(vals[2 * e]) | (f32_to_bits<DT>(vals[2 * e + 1]) << 16);
+        st_words<NE * 2>(p, w);
+    }
+}
+
+// -------------------------------------------------------------- main kernel
+template <int DT, int DP, int NT, bool FAST>
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+    constexpr int ES = DT == MF_F32 ? 4 : 2;
+    constexpr int EPL = 16 / ES;      // elements per 16-byte chunk
+    constexpr int NL = DP * ES / 64;  // 16-byte K/Q chunks per lane
+    constexpr int VCH = DP / 16;      // V elements per lane per key (= d tiles)
+    constexpr int VB = VCH * ES;      // bytes of one lane's V chunk
+    constexpr int VWD = VB / 4;       // 32-bit words of one lane's V chunk
+    static_assert(NL >= 1 && VWD >= 1, "head_dim too small for this dtype");
+    constexpr float kNegInf = -__builtin_huge_valf();
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int item = blockIdx.x * kWaves + wave;
+    if (item >= a.num_items) return;
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;  // 16-lane group: MFMA k-group / output row group
+    const int j = lane & 15;  // MFMA column (query column) and A-row (key) index
+
+    const int32_t* it = a.items + (int64_t)item * MF_PLAN_ITEM_INTS;
+    const int s = it[0], h = it[1], c0 = it[2], nct = it[3];
+    const int kt0 = it[4], kt1 = it[5], pslot = it[6];
+    const int row0 = a.cu_seqlens[s];
+    const int ncols = (a.cu_seqlens[s + 1] - row0) * a.G;
+    const int kv_len = a.kv_lens[s];
+    const int pool_len = (FAST || a.pool_lens == nullptr) ? kv_len : a.pool_lens[s];
+    const int D = a.head_dim;
+
+    // ---- columns owned by this lane (one per tile)
+    int prow[NT], qhead[NT], qpos[NT];
+    int maxpos = -1;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int cidx = (c0 + nt) * 16 + j;
+        const bool valid = nt < nct && cidx < ncols;
+        int r = 0, gq = 0, pr = row0, pos = -1;
+        if (valid) {
+            r = cidx / a.G;
+            gq = cidx - r * a.G;
+            pr = row0 + r;
+            if (a.row_map) pr = a.row_map[pr];
+            pos = (int)a.positions[pr];
+        }
+        prow[nt] = pr;
+        qhead[nt] = h * a.G + gq;
+        qpos[nt] = pos;
+        maxpos = max(maxpos, pos);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) maxpos = max(maxpos, __shfl_xor(maxpos, off, 64));
+    // Tiles past the last key any column may see are never read.
+    int kt_end = min(kt1, (min(maxpos, kv_len - 1) >> 4) + 1);
+    if (maxpos < 0 || kv_len <= 0) kt_end = kt0;
+    kt_end = __builtin_amdgcn_readfirstlane(kt_end);
+
+    // ---- Q fragments (MFMA B operand of S^T = K Q^T): lane (g, j) holds
+    // column j's head_dim chunk (c*4 + g) for c < NL.
+    uint4 qf[NT][NL];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+        for (int c = 0; c < NL; ++c) {
+            const int d0 = (c * 4 + g) * EPL;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (qpos[nt] >= 0 && d0 < D)
+                v = *(const uint4*)(a.q + ((int64_t)prow[nt] * a.q_sr + (int64_t)qhead[nt] * a.q_sh + d0) * ES);
+            qf[nt][c] = v;
+        }
+    }
+
+    float m[NT], l[NT];
+    f32x4 acc[NT][VCH];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        m[nt] = kNegInf;
+        l[nt] = 0.f;
+#pragma unroll
+        for (int c = 0; c < VCH; ++c) acc[nt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // General path: address of key `key`'s row for this kv head, or null.
+    auto key_row = [&](const char* pool, const char* inflight, int key) -> const char* {
+        if (key >= kv_len) return nullptr;
+        if (key < pool_len) {
+            const int blk = key / a.block_size;
+            const int off = key - blk * a.block_size;
+            const int phys = a.block_tables[(int64_t)s * a.bt_stride + blk];
+            return pool + ((int64_t)phys * a.p_sb + (int64_t)off * a.p_ss + (int64_t)h * a.p_sh) * ES;
+        }
+        int nr = row0 + (key - pool_len);
+        if (a.row_map) nr = a.row_map[nr];
+        return inflight + ((int64_t)nr * a.n_sr + (int64_t)h * a.n_sh) * ES;
+    };
+
+    // K: lane (g, j) loads key j's head_dim chunks (c*4 + g).
+    // V: lane (g, j) loads keys 4g..4g+3, head_dim elements [j*VCH, j*VCH+VCH).
+    auto load_tile = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
+        if constexpr (FAST) {
+            const int phys = a.block_tables[(int64_t)s * a.bt_stride + kt];
+            const int64_t base = (int64_t)phys * a.p_sb + (int64_t)h * a.p_sh;
+            const char* kp = a.k_pool + (base + (int64_t)j * a.p_ss) * ES;
+#pragma unroll
+            for (int c = 0; c < NL; ++c) {
+                const int d0 = (c * 4 + g) * EPL;
+                kf[c] = d0 < D ? *(const uint4*)(kp + (int64_t)d0 * ES) : make_uint4(0, 0, 0, 0);
+            }
+            const char* vp = a.v_pool + (base + (int64_t)j * VCH) * ES;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (j * VCH < D) {
+                    ld_words<VB>(vp + (int64_t)(4 * g + r) * a.p_ss * ES, vf[r]);
+                } else {
+#pragma unroll
+                    for (int w = 0; w < VWD; ++w) vf[r][w] = 0;
+                }
+            }
+        } else {
+            const char* kp = key_row(a.k_pool, a.new_k, kt * 16 + j);
+#pragma unroll
+            for (int c = 0; c < NL; ++c) {
+                const int d0 = (c * 4 + g) * EPL;
+                kf[c] = (kp && d0 < D) ? *(const uint4*)(kp + (int64_t)d0 * ES) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const char* vp = key_row(a.v_pool, a.new_v, kt * 16 + 4 * g + r);
+                if (vp && j * VCH < D) {
+                    ld_words<VB>(vp + (int64_t)j * VCH * ES, vf[r]);
+                } else {
+#pragma unroll
+                    for (int w = 0; w < VWD; ++w) vf[r][w] = 0;
+                }
+            }
+        }
+    };
+
+    auto process = [&](int kt, const uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
+        if constexpr (FAST) {
+            // Slots past the context in the last block may hold anything,
+            // NaN included; p = 0 there, but 0 * NaN is NaN, so clear them.
+            if ((kt + 1) * 16 > kv_len) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (kt * 16 + 4 * g + r >= kv_len) {
+#pragma unroll
+                        for (int w = 0; w < VWD; ++w) vf[r][w] = 0;
+                    }
+            }
+        }
+        uint2 p16[NT];
+        float p32[NT][4];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            if (nt < nct) {
+                f32x4 st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < NL; ++c) st = mfma_qk<DT>(kf[c], qf[nt][c], st);
+                // lane (g, j) now holds S^T[keys 4g..4g+3][column j]
+                float sv[4];
+                float bm = kNegInf;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = kt * 16 + 4 * g + r;
+                    const bool vis = key <= qpos[nt] && key < kv_len;
+                    sv[r] = vis ? st[r] * a.scale_log2 : kNegInf;
+                    bm = fmaxf(bm, sv[r]);
+                }
+                bm = fmaxf(bm, shfl_xor_f(bm, 16));
+                bm = fmaxf(bm, shfl_xor_f(bm, 32));
+                const float mn = fmaxf(m[nt], bm);
+                const float mu = mn == kNegInf ? 0.f : mn;
+                const float alpha = exp2f(m[nt] - mu);
+                float p[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) p[r] = exp2f(sv[r] - mu);
+                l[nt] = l[nt] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+                m[nt] = mn;
+#pragma unroll
+                for (int c = 0; c < VCH; ++c) acc[nt][c] *= alpha;
+                if constexpr (DT == MF_F32) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) p32[nt][r] = p[r];
+                } else {
+                    p16[nt] = make_uint2(f32_to_bits<DT>(p[0]) | (f32_to_bits<DT>(p[1]) << 16),
+                                         f32_to_bits<DT>(p[2]) | (f32_to_bits<DT>(p[3]) << 16));
+                }
+            }
+        }
+        // O^T += V^T P^T, one MFMA per 16-row head_dim tile c: row i of tile c
+        // is head_dim element i*VCH + c.
+#pragma unroll
+        for (int c = 0; c < VCH; ++c) {
+            if constexpr (DT == MF_F32) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float va = __uint_as_float(vf[r][c]);
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        if (nt < nct)
+                            acc[nt][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, p32[nt][r], acc[nt][c], 0, 0, 0);
+                }
+            } else {
+                const int wd = c >> 1;
+                uint2 va;
+                if ((c & 1) == 0) {
+                    va.x = (vf[0][wd] & 0xffffu) | (vf[1][wd] << 16);
+                    va.y = (vf[2][wd] & 0xffffu) | (vf[3][wd] << 16);
+                } else {
+                    va.x = (vf[0][wd] >> 16) | (vf[1][wd] & 0xffff0000u);
+                    va.y = (vf[2][wd] >> 16) | (vf[3][wd] & 0xffff0000u);
+                }
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    if (nt < nct) acc[nt][c] = mfma_pv16<DT>(va, p16[nt], acc[nt][c]);
+            }
+        }
+    };
+
+    // ---- key loop, software-pipelined one tile ahead
+    uint4 kA[NL], kB[NL];
+    uint32_t vA[4][VWD], vB[4][VWD];
+    int kt = kt0;
+    if (kt < kt_end) load_tile(kt, kA, vA);
+    while (kt < kt_end) {
+        if (kt + 1 < kt_end) load_tile(kt + 1, kB, vB);
+        process(kt, kA, vA);
+        ++kt;
+        if (kt >= kt_end) break;
+        if (kt + 1 < kt_end) load_tile(kt + 1, kA, vA);
+        process(kt, kB, vB);
+        ++kt;
+    }
+
+    // ---- finish: the lane holds O^T[d = (4g + r)*VCH + c][column j], i.e. the
+    // contiguous head_dim range [4g*VCH, 4g*VCH + 4*VCH) of its column.
+    const int dbase = 4 * g * VCH;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        float lt = l[nt] + shfl_xor_f(l[nt], 16);
+        lt += shfl_xor_f(lt, 32);
+        if (nt >= nct || qpos[nt] < 0) continue;
+        if (pslot < 0) {
+            if (dbase < D) {
+                const float inv = lt > 0.f ? 1.f / lt : 0.f;
+                float vals[4 * VCH];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int c = 0; c < VCH; ++c) vals[r * VCH + c] = acc[nt][c][r] * inv;
+                char* op = a.out + ((int64_t)prow[nt] * a.o_sr + (int64_t)qhead[nt] * a.o_sh + dbase) * ES;
+                store_out_chunk<DT, VCH>(op, vals);
+            }
+        } else {
+            float* ps = a.partials + (int64_t)(pslot + nt) * (16 * (a.part_dstride + 2));
+            float vals[4 * VCH];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < VCH; ++c) vals[r * VCH + c] = acc[nt][c][r];
+            store_out_chunk<MF_F32, VCH>((char*)(ps + j * a.part_dstride + dbase), vals);
+            if (g == 0) {
+                ps[16 * a.part_dstride + j] = m[nt];
+                ps[16 * a.part_dstride + 16 + j] = lt;
+            }
+        }
+    }
+}
+
+// --------------------------------------------------------------- merge kernel
+// One wave per (sequence, kv head, 16-column tile) that was split over key
+// partitions: out = sum_p w_p acc_p / sum_p w_p l_p with w_p = 2^(m_p - max m).
+template <int DT, int DP>
+__global__ __launch_bounds__(256) void merge_kernel(AttnArgs a, const int32_t* merges, int num_merges) {
+    constexpr int VCH = DP / 16;
+    constexpr int ES = DT == MF_F32 ? 4 : 2;
+    constexpr float kNegInf = -__builtin_huge_valf();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int mi = blockIdx.x * kWaves + wave;
+    if (mi >= num_merges) return;
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15;
+    const int32_t* mg = merges + (int64_t)mi * MF_PLAN_MERGE_INTS;
+    const int s = mg[0], h = mg[1], ct = mg[2], np = mg[3], slot0 = mg[4], sstride = mg[5];
+    const int row0 = a.cu_seqlens[s];
+    const int ncols = (a.cu_seqlens[s + 1] - row0) * a.G;
+    const int cidx = ct * 16 + j;
+    if (cidx >= ncols) return;
+    const int r = cidx / a.G;
+    const int gq = cidx - r * a.G;
+    int pr = row0 + r;
+    if (a.row_map) pr = a.row_map[pr];
+    const int qhead = h * a.G + gq;
+    const int dbase = 4 * g * VCH;
+    if (dbase >= a.head_dim) return;
+    const int stride = 16 * (a.part_dstride + 2);
+
+    float mx = kNegInf;
+    for (int p = 0; p < np; ++p) {
+        const float* ps = a.partials + (int64_t)(slot0 + p * sstride) * stride;
+        mx = fmaxf(mx, ps[16 * a.part_dstride + j]);
+    }
+    float L = 0.f;
+    float o[4 * VCH];
+#pragma unroll
+    for (int e = 0; e < 4 * VCH; ++e) o[e] = 0.f;
+    for (int p = 0; p < np; ++p) {
+        const float* ps = a.partials + (int64_t)(slot0 + p * sstride) * stride;
+        const float mp = ps[16 * a.part_dstride + j];
+        const float w = (mp == kNegInf) ? 0.f : exp2f(mp - mx);
+        L += ps[16 * a.part_dstride + 16 + j] * w;
+        uint32_t raw[4 * VCH];
+        ld_words<16 * VCH>((const char*)(ps + j * a.part_dstride + dbase), raw);
+#pragma unroll
+        for (int e = 0; e < 4 * VCH; ++e) o[e] += w * __uint_as_float(raw[e]);
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4 * VCH; ++e) o[e] *= inv;
+    char* op = a.out + ((int64_t)pr * a.o_sr + (int64_t)qhead * a.o_sh + dbase) * ES;
+    store_out_chunk<DT, VCH>(op, o);
+}
+
+template <int DT, int DP>
+int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t n_wide,
+                     const int32_t* merges, int64_t n_merges, bool fast, hipStream_t stream) {
+    if (n_narrow > 0) {
+        a.items = items;
+        a.num_items = (int)n_narrow;
+        const dim3 grid((unsigned)((n_narrow + kWaves - 1) / kWaves));
+        if (fast) hipLaunchKernelGGL((attn_kernel<DT, DP, 1, true>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((attn_kernel<DT, DP, 1, false>), grid, dim3(256), 0, stream, a);
+        if (int st = check_launch()) return st;
+    }
+    constexpr int NTW = wide_tiles(DT, DP);
+    if constexpr (NTW > 1) {
+        if (n_wide > 0) {
+            a.items = items + n_narrow * MF_PLAN_ITEM_INTS;
+            a.num_items = (int)n_wide;
+            const dim3 grid((unsigned)((n_wide + kWaves - 1) / kWaves));
+            if (fast) hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, true>), grid, dim3(256), 0, stream, a);
+            else hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, false>), grid, dim3(256), 0, stream, a);
+            if (int st = check_launch()) return st;
+        }
+    } else {
+        if (n_wide > 0) return MF_ERR_ARG;  // the plan was made for another dtype
+    }
+    if (n_merges > 0) {
+        const dim3 grid((unsigned)((n_merges + kWaves - 1) / kWaves));
+        hipLaunchKernelGGL((merge_kernel<DT, DP>), grid, dim3(256), 0, stream, a, merges, (int)n_merges);
+        if (int st = check_launch()) return st;
+    }
+    return MF_OK;
+}
+
+// Padded head_dim the kernels are built for, or 0 if unsupported.
+int padded_head_dim(int dtype, int d) {
+    if (d <= 0 || (d & (d - 1)) != 0) return 0;  // powers of two only
+    if (dtype == MF_F32) {
+        if (d > 128) return 0;
+        return d < 16 ? 16 : d;
+    }
+    if (d > 256) return 0;
+    return d < 32 ? 32 : d;
+}
+
+inline int part_dstride_for(int head_dim) { return head_dim < 32 ? 32 : head_dim; }
+
+}  // namespace
+}  // namespace mf
+
+extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const int32_t* kv_lens,
+                                 int num_q_heads, int num_kv_heads, int head_dim, int dtype,
+                                 int partition_tiles, int32_t* items, int64_t items_capacity,
+                                 int32_t* merges, int64_t merges_capacity, int64_t* counts) {
+    if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || !counts)
+        return MF_ERR_ARG;
+    if (num_q_heads % num_kv_heads) return MF_ERR_ARG;
+    if (num_seqs > 0 && (!cu_seqlens || !kv_lens)) return MF_ERR_ARG;
+    const int DP = mf::padded_head_dim(dtype, head_dim);
+    if (!mf::dtype_ok(dtype) || !DP) return MF_ERR_UNSUPPORTED;
+    const int WT = mf::wide_tiles(dtype, DP);
+    const int G = num_q_heads / num_kv_heads;
+    const int Hkv = num_kv_heads;
+
+    auto col_tiles = [&](int s) -> int {
+        const int qlen = cu_seqlens[s + 1] - cu_seqlens[s];
+        if (qlen <= 0 || kv_lens[s] <= 0) return 0;
+        return (qlen * G + 15) / 16;
+    };
+
+    // Total (kv head, column group, key tile) units decide the partition size:
+    // enough items to keep every CU busy, few enough that partials stay small.
+    int64_t work = 0;
+    for (int s = 0; s < num_seqs; ++s) {
+        const int nct = col_tiles(s);
+        if (!nct) continue;
+        const int groups = (nct == 1 || WT == 1) ? nct : (nct + WT - 1) / WT;
+        work += (int64_t)Hkv * groups * ((kv_lens[s] + 15) / 16);
+    }
+    int P = partition_tiles;
+    if (P <= 0) {
+        const int64_t target_items = 8192;
+        int64_t want = (work + target_items - 1) / target_items;
+        P = 4;
+        while (P < want && P < 64) P *= 2;
+    }
+
+    // First walk: sizes only.
+    int64_t n_narrow = 0, n_wide = 0, n_merges = 0, n_slots = 0;
+    for (int s = 0; s < num_seqs; ++s) {
+        const int nct = col_tiles(s);
+        if (!nct) continue;
+        const bool narrow = nct == 1 || WT == 1;
+        const int tiles = (kv_lens[s] + 15) / 16;
+        const int nparts = (tiles + P - 1) / P;
+        const int width = narrow ? 1 : WT;
+        for (int cg0 = 0; cg0 < nct; cg0 += width) {
+            const int w = std::min(width, nct - cg0);
+            (narrow ? n_narrow : n_wide) += (int64_t)nparts * Hkv;
+            if (nparts > 1) {
+                n_slots += (int64_t)Hkv * nparts * w;
+                n_merges += (int64_t)Hkv * w;
+            }
+        }
+    }
+    const int64_t pstride = 16 * (int64_t)(mf::part_dstride_for(head_dim) + 2);
+    counts[0] = n_narrow;
+    counts[1] = n_wide;
+    counts[2] = n_merges;
+    counts[3] = n_slots * pstride;
+    if (n_narrow + n_wide > items_capacity || n_merges > merges_capacity) return MF_ERR_WORKSPACE;
+    if ((n_narrow + n_wide) > 0 && !items) return MF_ERR_ARG;
+    if (n_merges > 0 && !merges) return MF_ERR_ARG;
+
+    // Second walk: write items (narrow block first) and merges.
+    int64_t wi_narrow = 0, wi_wide = n_narrow, wm = 0, slots = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int s = 0; s < num_seqs; ++s) {
+            const int nct = col_tiles(s);
+            if (!nct) continue;
+            const bool narrow = nct == 1 || WT == 1;
+            if ((pass == 0) != narrow) continue;
+            const int tiles = (kv_lens[s] + 15) / 16;
+            const int nparts = (tiles + P - 1) / P;
+            const int width = narrow ? 1 : WT;
+            for (int cg0 = 0; cg0 < nct; cg0 += width) {
+                const int w = std::min(width, nct - cg0);
+                const int64_t group_base = slots;
+                if (nparts > 1) slots += (int64_t)Hkv * nparts * w;
+                for (int p = 0; p < nparts; ++p) {
+                    for (int h = 0; h < Hkv; ++h) {
+                        int64_t& wi = narrow ? wi_narrow : wi_wide;
+                        int32_t* o = items + wi * MF_PLAN_ITEM_INTS;
+                        o[0] = s;
+                        o[1] = h;
+                        o[2] = cg0;
+                        o[3] = w;
+                        o[4] = p * P;
+                        o[5] = std::min(tiles, (p + 1) * P);
+                        o[6] = nparts > 1 ? (int32_t)(group_base + ((int64_t)h * nparts + p) * w) : -1;
+                        o[7] = 0;
+                        ++wi;
+                    }
+                }
+                if (nparts > 1) {
+                    for (int h = 0; h < Hkv; ++h) {
+                        for (int o2 = 0; o2 < w; ++o2) {
+                            int32_t* o = merges + wm * MF_PLAN_MERGE_INTS;
+                            o[0] = s;
+                            o[1] = h;
+                            o[2] = cg0 + o2;
+                            o[3] = nparts;
+                            o[4] = (int32_t)(group_base + (int64_t)h * nparts * w + o2);
+                            o[5] = w;
+                            o[6] = 0;
+                            o[7] = 0;
+                            ++wm;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    return MF_OK;
+}
+
+extern "C" int mf_paged_attention(
+    const void* q, int64_t q_stride_row, int64_t q_stride_head, void* out, int64_t out_stride_row,
+    int64_t out_stride_head, int dtype, const void* k_pool, const void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head, int block_size,
+    const int32_t* block_tables, int64_t block_table_stride, const int32_t* cu_seqlens,
+    const int32_t* kv_lens, const int64_t* positions, const int32_t* row_map,
+    const int32_t* pool_lens, const void* new_k, const void* new_v, int64_t new_stride_row,
+    int64_t new_stride_head, int num_q_heads, int num_kv_heads, int head_dim, float scale,
+    const int32_t* plan_items, int64_t num_items_narrow, int64_t num_items_wide,
+    const int32_t* plan_merges, int64_t num_merges, float* partials, int64_t partials_floats,
+    mf_stream_t stream) {
+    using namespace mf;
+    if (!dtype_ok(dtype) || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
+        block_size <= 0 || num_items_narrow < 0 || num_items_wide < 0 || num_merges < 0)
+        return MF_ERR_ARG;
+    const int DP = padded_head_dim(dtype, head_dim);
+    if (!DP) return MF_ERR_UNSUPPORTED;
+    // A call may carry only items (partials left for a later merge-only call)
+    // or only merges; both are how a caller times the two kernels apart.
+    if (num_items_narrow + num_items_wide == 0 && num_merges == 0) return MF_OK;
+    if (!q || !out || !k_pool || !v_pool || !block_tables || !cu_seqlens || !kv_lens || !positions)
+        return MF_ERR_ARG;
+    if (num_items_narrow + num_items_wide > 0 && !plan_items) return MF_ERR_ARG;
+    if (pool_lens && (!new_k || !new_v)) return MF_ERR_ARG;
+    if (num_merges > 0 && (!plan_merges || !partials || partials_floats <= 0)) return MF_ERR_WORKSPACE;
+    // 16-byte row loads need 16-byte aligned rows.
+    const int es = dtype_size(dtype);
+    const int64_t epl = 16 / es;
+    const int64_t strides[] = {q_stride_row, q_stride_head, pool_stride_block, pool_stride_slot,
+                               pool_stride_head};
+    for (int64_t st : strides)
+        if (st % epl) return MF_ERR_ARG;
+    if (((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool) & 15) return MF_ERR_ARG;
+    if (pool_lens && ((new_stride_row % epl) || (new_stride_head % epl) ||
+                      (((uintptr_t)new_k | (uintptr_t)new_v) & 15)))
+        return MF_ERR_ARG;
+    const int out_align = std::min(16, 4 * (DP / 16) * es);
+    if ((out_stride_row * es) % out_align || (out_stride_head * es) % out_align ||
+        ((uintptr_t)out % out_align))
+        return MF_ERR_ARG;
+
+    AttnArgs a{};
+    a.q = (const char*)q;
+    a.q_sr = q_stride_row;
+    a.q_sh = q_stride_head;
+    a.out = (char*)out;
+    a.o_sr = out_stride_row;
+    a.o_sh = out_stride_head;
+    a.k_pool = (const char*)k_pool;
+    a.v_pool = (const char*)v_pool;
+    a.p_sb = pool_stride_block;
+    a.p_ss = pool_stride_slot;
+    a.p_sh = pool_stride_head;
+    a.block_size = block_size;
+    a.block_tables = block_tables;
+    a.bt_stride = block_table_stride;
+    a.cu_seqlens = cu_seqlens;
+    a.kv_lens = kv_lens;
+    a.positions = positions;
+    a.row_map = row_map;
+    a.pool_lens = pool_lens;
+    a.new_k = (const char*)new_k;
+    a.new_v = (const char*)new_v;
+    a.n_sr = new_stride_row;
+    a.n_sh = new_stride_head;
+    a.G = num_q_heads / num_kv_heads;
+    a.head_dim = head_dim;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.partials = partials;
+    a.part_dstride = part_dstride_for(head_dim);
+    const bool fast = block_size == 16 && pool_lens == nullptr;
+    hipStream_t st = (hipStream_t)stream;
+
+#define MF_ATTN_CASE(DT, DPV)                                                                  \
+    if (dtype == DT && DP == DPV)                                                              \
+        return launch_attention<DT, DPV>(a, plan_items, num_items_narrow, num_items_wide,      \
+                                         plan_merges, num_merges, fast, st);
+    MF_ATTN_CASE(MF_F32, 16)
+    MF_ATTN_CASE(MF_F32, 32)
+    MF_ATTN_CASE(MF_F32, 64)
+    MF_ATTN_CASE(MF_F32, 128)
+    MF_ATTN_CASE(MF_BF16, 32)
+    MF_ATTN_CASE(MF_BF16, 64)
+    MF_ATTN_CASE(MF_BF16, 128)
+    MF_ATTN_CASE(MF_BF16, 256)
+    MF_ATTN_CASE(MF_F16, 32)
+    MF_ATTN_CASE(MF_F16, 64)
+    MF_ATTN_CASE(MF_F16, 128)
+    MF_ATTN_CASE(MF_F16, 256)
+#undef MF_ATTN_CASE
+    return MF_ERR_UNSUPPORTED;
+}
