@@ -48,6 +48,10 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline duration")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--check", action="store_true", help="check a sample of rows against the oracle")
+    ap.add_argument("--fused", action="store_true",
+                    help="merge split-K partitions inside the attention kernel (last arrival) instead of a merge kernel")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device copy (scale factor for PMC byte counters)")
     return ap.parse_args()
 
 
@@ -137,6 +141,15 @@ def main():
     from memforge_amd import _native as nat
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        n = 256 << 20
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "copies": 3}))
+        return
     ctx, tables, kpool, vpool, q = make_workload(args.sigma, dev)
     out = torch.empty_like(q)
     bt = tables.to(dev)
@@ -147,21 +160,30 @@ def main():
                               args.partition_tiles)
     pool = nat.PoolView.from_bshd(kpool, vpool)
     partials = torch.empty(max(plan.partials_floats, 1), dtype=torch.float32, device=dev)
+    counters = torch.zeros(max(plan.n_merges, 1), dtype=torch.int32, device=dev)
     scale = 1.0 / math.sqrt(D)
     merges_only = nat.AttentionPlan(plan.items, plan.merges, 0, 0, plan.n_merges, plan.partials_floats,
                                     plan.items_host, plan.merges_host)
     items_only = nat.AttentionPlan(plan.items, plan.merges, plan.n_narrow, plan.n_wide, 0,
                                    plan.partials_floats, plan.items_host, plan.merges_host)
 
+    def run(p, fused):
+        nat.paged_attention(q, out, pool, bt, cu, kv_lens, positions, p, scale, HKV, partials=partials,
+                            counters=counters if fused else None, fused_merge=fused)
+
     def layer(events=None):
         if events is None:
-            nat.paged_attention(q, out, pool, bt, cu, kv_lens, positions, plan, scale, HKV, partials=partials)
+            run(plan, args.fused)
             return
         e0, e1, e2 = events
         e0.record()
-        nat.paged_attention(q, out, pool, bt, cu, kv_lens, positions, items_only, scale, HKV, partials=partials)
-        e1.record()
-        nat.paged_attention(q, out, pool, bt, cu, kv_lens, positions, merges_only, scale, HKV, partials=partials)
+        if not args.fused:
+            run(items_only, False)
+            e1.record()
+            run(merges_only, False)
+        else:
+            run(plan, True)
+            e1.record()
         e2.record()
 
     for _ in range(args.warmup):
@@ -241,7 +263,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": None,
-            "kernel": "attn_kernel<bf16,128,1,fast>",
+            "kernel": "attn_kernel<bf16,128,1,fast>" + (" (split-K merge fused)" if args.fused else ""),
             "kernel_avg_us": round(attn_avg_s * 1e6, 2),
             "merge_avg_us": round(float(np.mean(merge_ms)) * 1e3, 2),
             "bytes_per_launch": per_layer,

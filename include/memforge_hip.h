@@ -101,7 +101,7 @@ int mf_kv_gather(const void* k_pool, const void* v_pool, int pool_dtype,
  *   status[0] bit flags: MF_PACK_TABLE_OVERFLOW, MF_PACK_NEGATIVE_POSITION,
  *             MF_PACK_DUPLICATE_SLOT, MF_PACK_BAD_ENTRY
  *   status[1] first row needing a block past its table (or -1)
- *   status[2] first row whose slot another row also writes (or -1)
+ *   status[2] a row whose slot another row also writes (or -1)
  *   status[3] first malformed entry (or -1)
  * Duplicate detection runs when slot_bitmap is non-NULL: a device bitmap of
  * num_slots bits that must be all-zero on entry and is all-zero again on exit.
@@ -138,9 +138,13 @@ int mf_ragged_pack(const int32_t* entries, int num_entries,
  * accumulates in fp32; out is written in `dtype` (the q/K/V dtype).
  * Work is described by a plan from mf_attention_plan (device copy of its
  * items/merges); `partials` is fp32 scratch of at least the planned size.
- * Passing the plan's items with num_merges = 0, then a second call with no
- * items and only the merges, runs the same work as one call in two launches
- * (used to time the attention and merge kernels apart).
+ * merge_counters (device int32[num_merges], all-zero on entry and again on
+ * exit) lets the attention kernel merge split-K partitions itself: the last
+ * partition of a group to finish merges it. With merge_counters NULL a
+ * separate merge kernel runs after the attention kernel. Passing the plan's
+ * items with num_merges = 0, then a second call with no items and only the
+ * merges, runs the unfused work in two launches (to time them apart).
+ * Concurrent calls must not share partials or merge_counters.
  * Replaces paged_attention_varlen / _materialised (memforge_ml/kernels/
  * varlen_attention.py:78-235, 291-395), paged_attention_blockwise
  * (memforge_ml/kernels/block_attention.py:51-145), PagedAttention.forward
@@ -161,7 +165,7 @@ int mf_paged_attention(const void* q, int64_t q_stride_row, int64_t q_stride_hea
                        const int32_t* plan_items, int64_t num_items_narrow,
                        int64_t num_items_wide, const int32_t* plan_merges,
                        int64_t num_merges, float* partials, int64_t partials_floats,
-                       mf_stream_t stream);
+                       int32_t* merge_counters, mf_stream_t stream);
 
 /* Host-side planner for mf_paged_attention. Inputs are HOST arrays:
  * cu_seqlens[B+1] and kv_lens[B]. Splits every (sequence, kv head, column

@@ -47,7 +47,7 @@ _SIGNATURES = {
     "mf_paged_attention": (_c_int, [
         _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
         _c_int, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int,
-        _c_int, _c_f32, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp]),
+        _c_int, _c_f32, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _vp]),
     "mf_attention_plan": (_c_int, [_c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                    _vp, _c_i64, _vp, _c_i64, _vp]),
     "mf_spec_verify_workspace_size": (_c_i64, [_c_int, _c_int]),
@@ -245,17 +245,33 @@ def plan_attention(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_head
 
 
 class Workspace:
-    """Grow-only fp32 scratch for split-K partials, one per device."""
+    """Grow-only scratch for split-K partials (fp32) and merge arrival
+    counters (int32, kept all-zero between calls by the kernels), one per
+    (device, stream) so concurrent streams never share it."""
 
     def __init__(self) -> None:
-        self._buf: Optional[torch.Tensor] = None
+        self._partials = {}
+        self._counters = {}
 
-    def get(self, floats: int, device) -> Optional[torch.Tensor]:
+    def partials(self, floats: int, device) -> Optional[torch.Tensor]:
         if floats <= 0:
             return None
-        if self._buf is None or self._buf.numel() < floats or self._buf.device != torch.device(device):
-            self._buf = torch.empty(max(floats, 1 << 16), dtype=torch.float32, device=device)
-        return self._buf
+        key = (str(device), _stream())
+        buf = self._partials.get(key)
+        if buf is None or buf.numel() < floats:
+            buf = torch.empty(max(floats, 1 << 16), dtype=torch.float32, device=device)
+            self._partials[key] = buf
+        return buf
+
+    def counters(self, n: int, device) -> Optional[torch.Tensor]:
+        if n <= 0:
+            return None
+        key = (str(device), _stream())
+        buf = self._counters.get(key)
+        if buf is None or buf.numel() < n:
+            buf = torch.zeros(max(n, 1 << 12), dtype=torch.int32, device=device)
+            self._counters[key] = buf
+        return buf
 
 
 _WORKSPACE = Workspace()
@@ -268,8 +284,15 @@ def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView
                     pool_lens: Optional[torch.Tensor] = None,
                     new_k_rows: Optional[torch.Tensor] = None,
                     new_v_rows: Optional[torch.Tensor] = None,
-                    partials: Optional[torch.Tensor] = None) -> None:
-    """Varlen paged attention into ``out_rows`` ((rows, Hq, D) views, device)."""
+                    partials: Optional[torch.Tensor] = None,
+                    counters: Optional[torch.Tensor] = None, fused_merge: bool = False) -> None:
+    """Varlen paged attention into ``out_rows`` ((rows, Hq, D) views, device).
+
+    Split-K partitions are merged by a separate merge kernel; with
+    ``fused_merge`` the attention kernel merges them itself (the last partition
+    of a group to finish, through arrival counters from the workspace unless
+    given) -- correct, but slower on MI355X because every arriving partition
+    must release its partials with an agent-scope fence."""
     _rows_ok(q_rows, "q_rows")
     _rows_ok(out_rows, "out_rows")
     require_device(q_rows, out_rows, pool.k, block_tables, cu_seqlens, kv_lens, positions)
@@ -281,7 +304,11 @@ def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView
             raise TypeError(f"{name} must be a contiguous {dt} tensor")
     Hq, D = q_rows.shape[1], q_rows.shape[2]
     if partials is None:
-        partials = _WORKSPACE.get(plan.partials_floats, q_rows.device)
+        partials = _WORKSPACE.partials(plan.partials_floats, q_rows.device)
+    if fused_merge and counters is None:
+        counters = _WORKSPACE.counters(plan.n_merges, q_rows.device)
+    if not fused_merge:
+        counters = None
     nk = new_k_rows if new_k_rows is not None else None
     nv = new_v_rows if new_v_rows is not None else None
     if pool_lens is not None:
@@ -301,7 +328,7 @@ def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView
         nk.stride(0) if nk is not None else 0, nk.stride(1) if nk is not None else 0,
         Hq, num_kv_heads, D, float(scale),
         _ptr(plan.items), plan.n_narrow, plan.n_wide, _ptr(plan.merges), plan.n_merges,
-        _ptr(partials), partials.numel() if partials is not None else 0, _stream(),
+        _ptr(partials), partials.numel() if partials is not None else 0, _ptr(counters), _stream(),
     ), "mf_paged_attention")
 
 

@@ -22,6 +22,7 @@
 // kernel combines them with the log-sum-exp rule.
 #include <algorithm>
 #include <cmath>
+#include <vector>
 
 #include "mf_common.h"
 
@@ -35,6 +36,7 @@ typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
 
 constexpr int kWaves = 4;  // waves per workgroup; each wave runs its own item
+constexpr int kMaxItemTiles = 64;  // key tiles per work item (one block-table entry per lane)
 
 // 16-column tiles one wave carries for multi-tile (prefill / wide verify)
 // items: as many as fit in registers without spilling.
@@ -68,6 +70,8 @@ struct AttnArgs {
     int num_items;
     float* partials;
     int part_dstride;  // floats per column of a partial slot's output block
+    const int32_t* merges;  // plan merge records (fused split-K merge)
+    int32_t* counters;      // per-group arrival counters; null = separate merge kernel
 };
 
 // ------------------------------------------------------------- MFMA wrappers
@@ -152,6 +156,86 @@ __device__ __forceinline__ void store_out_chunk(char* p, const float* vals) {
             w[e] = f32_to_bits<DT>(vals[2 * e]) | (f32_to_bits<DT>(vals[2 * e + 1]) << 16);
         st_words<NE * 2>(p, w);
     }
+}
+
+// ------------------------------------------------------------- split-K merge
+// Partials of one 16-column tile (merge record `mg`) live in slots
+// slot0 + p*sstride, p < np; each slot holds [16 columns][part_dstride] fp32
+// unnormalised outputs followed by 16 running maxima and 16 sums. The merged
+// output is sum_p w_p acc_p / sum_p w_p l_p with w_p = 2^(m_p - max_p m_p).
+//
+// merge_range accumulates partitions p0, p0+pinc, ... relative to their own
+// maximum `mx` (lane (g, j): column j, head_dim range [4g*VCH, 4g*VCH+4*VCH)),
+// issuing the loads of two partitions before using them so the loop is not a
+// memory round trip per partition.
+template <int DP>
+__device__ __forceinline__ void merge_range(const AttnArgs& a, const int32_t* mg, int p0, int pinc, int j,
+                                            int dbase, float& mx, float& L, float (&o)[DP / 4]) {
+    constexpr int VCH = DP / 16;
+    constexpr float kNegInf = -__builtin_huge_valf();
+    const int np = mg[3], slot0 = mg[4], sstride = mg[5];
+    const int64_t stride = 16 * (int64_t)(a.part_dstride + 2);
+    const float* base = a.partials + (int64_t)slot0 * stride;
+    const int64_t pstep = (int64_t)sstride * stride;
+    const int moff = 16 * a.part_dstride + j;
+    mx = kNegInf;
+    for (int p = p0; p < np; p += pinc) mx = fmaxf(mx, base[p * pstep + moff]);
+    L = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4 * VCH; ++e) o[e] = 0.f;
+    auto absorb = [&](const uint32_t* raw, float mp, float lp) {
+        const float w = (mp == kNegInf) ? 0.f : exp2f(mp - mx);
+        L += lp * w;
+#pragma unroll
+        for (int e = 0; e < 4 * VCH; ++e) o[e] += w * __uint_as_float(raw[e]);
+    };
+    int p = p0;
+    for (; p + pinc < np; p += 2 * pinc) {
+        uint32_t r0[4 * VCH], r1[4 * VCH];
+        const float* q0 = base + p * pstep;
+        const float* q1 = q0 + pinc * pstep;
+        ld_words<16 * VCH>((const char*)(q0 + j * a.part_dstride + dbase), r0);
+        ld_words<16 * VCH>((const char*)(q1 + j * a.part_dstride + dbase), r1);
+        const float m0 = q0[moff], l0 = q0[moff + 16];
+        const float m1 = q1[moff], l1 = q1[moff + 16];
+        absorb(r0, m0, l0);
+        absorb(r1, m1, l1);
+    }
+    if (p < np) {
+        uint32_t r0[4 * VCH];
+        const float* q0 = base + p * pstep;
+        ld_words<16 * VCH>((const char*)(q0 + j * a.part_dstride + dbase), r0);
+        absorb(r0, q0[moff], q0[moff + 16]);
+    }
+}
+
+// Output row/head of column tile ct's column j, or false for a padding column.
+__device__ __forceinline__ bool merge_column(const AttnArgs& a, int s, int h, int ct, int j, int& prow, int& qhead) {
+    const int row0 = a.cu_seqlens[s];
+    const int ncols = (a.cu_seqlens[s + 1] - row0) * a.G;
+    const int cidx = ct * 16 + j;
+    if (cidx >= ncols) return false;
+    const int r = cidx / a.G;
+    prow = row0 + r;
+    if (a.row_map) prow = a.row_map[prow];
+    qhead = h * a.G + (cidx - r * a.G);
+    return true;
+}
+
+// Single-wave merge of one record (used by the fused in-kernel merge).
+template <int DT, int DP>
+__device__ __forceinline__ void merge_tile(const AttnArgs& a, const int32_t* mg, int g, int j) {
+    constexpr int VCH = DP / 16;
+    constexpr int ES = DT == MF_F32 ? 4 : 2;
+    int prow, qhead;
+    const int dbase = 4 * g * VCH;
+    if (!merge_column(a, mg[0], mg[1], mg[2], j, prow, qhead) || dbase >= a.head_dim) return;
+    float mx, L, o[4 * VCH];
+    merge_range<DP>(a, mg, 0, 1, j, dbase, mx, L, o);
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4 * VCH; ++e) o[e] *= inv;
+    store_out_chunk<DT, VCH>(a.out + ((int64_t)prow * a.o_sr + (int64_t)qhead * a.o_sh + dbase) * ES, o);
 }
 
 // -------------------------------------------------------------- main kernel
@@ -250,26 +334,34 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 
     // K: lane (g, j) loads key j's head_dim chunks (c*4 + g).
     // V: lane (g, j) loads keys 4g..4g+3, head_dim elements [j*VCH, j*VCH+VCH).
+    // FAST path (16-token blocks, no in-flight keys, head_dim == DP): every
+    // load is unconditional, so the compiler can keep the next tile's loads in
+    // flight while the current tile is processed; the item's block-table
+    // entries (at most kMaxItemTiles = 64) are fetched once, one per lane, and
+    // read back with readlane.
+    int tbl = 0;
+    const int tbl_base = kt0;
+    // byte offsets of this lane's K chunk (key j, chunk g) and V chunk (keys
+    // 4g.., head_dim j*VCH..) inside one block of one kv head
+    const uint32_t k_lane_off = (uint32_t)(((int64_t)j * a.p_ss + g * EPL) * ES);
+    const uint32_t v_row_bytes = (uint32_t)(a.p_ss * ES);
+    const uint32_t v_lane_off = (uint32_t)(((int64_t)(4 * g) * a.p_ss + j * VCH) * ES);
+    if constexpr (FAST) {
+        const int idx = kt0 + lane;
+        tbl = idx < kt_end ? a.block_tables[(int64_t)s * a.bt_stride + idx] : 0;
+    }
     auto load_tile = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
         if constexpr (FAST) {
-            const int phys = a.block_tables[(int64_t)s * a.bt_stride + kt];
-            const int64_t base = (int64_t)phys * a.p_sb + (int64_t)h * a.p_sh;
-            const char* kp = a.k_pool + (base + (int64_t)j * a.p_ss) * ES;
+            // block base is wave-uniform (scalar registers); the lane's byte
+            // offsets inside a block never change, so they are computed once
+            const int phys = __builtin_amdgcn_readlane(tbl, kt - tbl_base);
+            const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
+            const char* kb = a.k_pool + boff;
+            const char* vb = a.v_pool + boff;
 #pragma unroll
-            for (int c = 0; c < NL; ++c) {
-                const int d0 = (c * 4 + g) * EPL;
-                kf[c] = d0 < D ? *(const uint4*)(kp + (int64_t)d0 * ES) : make_uint4(0, 0, 0, 0);
-            }
-            const char* vp = a.v_pool + (base + (int64_t)j * VCH) * ES;
+            for (int c = 0; c < NL; ++c) kf[c] = *(const uint4*)(kb + k_lane_off + c * 4 * 16);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (j * VCH < D) {
-                    ld_words<VB>(vp + (int64_t)(4 * g + r) * a.p_ss * ES, vf[r]);
-                } else {
-#pragma unroll
-                    for (int w = 0; w < VWD; ++w) vf[r][w] = 0;
-                }
-            }
+            for (int r = 0; r < 4; ++r) ld_words<VB>(vb + v_lane_off + r * v_row_bytes, vf[r]);
         } else {
             const char* kp = key_row(a.k_pool, a.new_k, kt * 16 + j);
 #pragma unroll
@@ -372,19 +464,43 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
     };
 
-    // ---- key loop, software-pipelined one tile ahead
+    // ---- key loop, software-pipelined. Single-tile fast items (decode) keep
+    // two tiles in flight ahead of the one being processed (three register
+    // buffers; that kernel is at two waves per SIMD either way), the rest one. The
+    // prefetch is unconditional -- the last iterations re-read the final tile,
+    // an L2 hit -- because a conditional load makes the compiler drain every
+    // outstanding load at the join and serialises the pipeline.
     uint4 kA[NL], kB[NL];
     uint32_t vA[4][VWD], vB[4][VWD];
-    int kt = kt0;
-    if (kt < kt_end) load_tile(kt, kA, vA);
-    while (kt < kt_end) {
-        if (kt + 1 < kt_end) load_tile(kt + 1, kB, vB);
-        process(kt, kA, vA);
-        ++kt;
-        if (kt >= kt_end) break;
-        if (kt + 1 < kt_end) load_tile(kt + 1, kA, vA);
-        process(kt, kB, vB);
-        ++kt;
+    if (kt0 < kt_end) {
+        const int last = kt_end - 1;
+        int kt = kt0;
+        load_tile(kt, kA, vA);
+        if constexpr (FAST && NT == 1) {
+            uint4 kC[NL];
+            uint32_t vC[4][VWD];
+            load_tile(min(kt + 1, last), kB, vB);
+            for (;;) {
+                load_tile(min(kt + 2, last), kC, vC);
+                process(kt, kA, vA);
+                if (++kt > last) break;
+                load_tile(min(kt + 2, last), kA, vA);
+                process(kt, kB, vB);
+                if (++kt > last) break;
+                load_tile(min(kt + 2, last), kB, vB);
+                process(kt, kC, vC);
+                if (++kt > last) break;
+            }
+        } else {
+            for (;;) {
+                load_tile(min(kt + 1, last), kB, vB);
+                process(kt, kA, vA);
+                if (++kt > last) break;
+                load_tile(min(kt + 1, last), kA, vA);
+                process(kt, kB, vB);
+                if (++kt > last) break;
+            }
+        }
     }
 
     // ---- finish: the lane holds O^T[d = (4g + r)*VCH + c][column j], i.e. the
@@ -420,65 +536,84 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             }
         }
     }
+
+    // ---- fused split-K merge: the last partition of a group to arrive merges
+    // the group. Release the partials (agent-scope fence: the L2s of the XCDs
+    // are not coherent with each other), count the arrival, and on the last
+    // arrival acquire everyone else's partials and reset the counter for the
+    // next call. Every wave runs to the end; nothing waits on another wave.
+    if (pslot >= 0 && a.counters != nullptr) {
+        const int m0 = it[7];
+        __threadfence();
+        int prev = 0;
+        if (lane == 0) prev = atomicAdd(a.counters + m0, 1);
+        prev = __shfl(prev, 0, 64);
+        const int32_t* mg0 = a.merges + (int64_t)m0 * MF_PLAN_MERGE_INTS;
+        if (prev == mg0[3] - 1) {
+            __threadfence();
+            if (lane == 0) a.counters[m0] = 0;
+            for (int o = 0; o < nct; ++o) merge_tile<DT, DP>(a, mg0 + o * MF_PLAN_MERGE_INTS, g, j);
+        }
+    }
 }
 
 // --------------------------------------------------------------- merge kernel
-// One wave per (sequence, kv head, 16-column tile) that was split over key
-// partitions: out = sum_p w_p acc_p / sum_p w_p l_p with w_p = 2^(m_p - max m).
+// One workgroup per merge record: wave w merges partitions w, w+4, ... and the
+// four partial results are combined through LDS by wave 0.
 template <int DT, int DP>
 __global__ __launch_bounds__(256) void merge_kernel(AttnArgs a, const int32_t* merges, int num_merges) {
     constexpr int VCH = DP / 16;
     constexpr int ES = DT == MF_F32 ? 4 : 2;
     constexpr float kNegInf = -__builtin_huge_valf();
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int mi = blockIdx.x * kWaves + wave;
+    __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+    __shared__ float s_o[kWaves][16][DP];
+    const int mi = blockIdx.x;
     if (mi >= num_merges) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15;
     const int32_t* mg = merges + (int64_t)mi * MF_PLAN_MERGE_INTS;
-    const int s = mg[0], h = mg[1], ct = mg[2], np = mg[3], slot0 = mg[4], sstride = mg[5];
-    const int row0 = a.cu_seqlens[s];
-    const int ncols = (a.cu_seqlens[s + 1] - row0) * a.G;
-    const int cidx = ct * 16 + j;
-    if (cidx >= ncols) return;
-    const int r = cidx / a.G;
-    const int gq = cidx - r * a.G;
-    int pr = row0 + r;
-    if (a.row_map) pr = a.row_map[pr];
-    const int qhead = h * a.G + gq;
+    int prow = 0, qhead = 0;
     const int dbase = 4 * g * VCH;
-    if (dbase >= a.head_dim) return;
-    const int stride = 16 * (a.part_dstride + 2);
-
-    float mx = kNegInf;
-    for (int p = 0; p < np; ++p) {
-        const float* ps = a.partials + (int64_t)(slot0 + p * sstride) * stride;
-        mx = fmaxf(mx, ps[16 * a.part_dstride + j]);
-    }
-    float L = 0.f;
-    float o[4 * VCH];
+    const bool active = merge_column(a, mg[0], mg[1], mg[2], j, prow, qhead) && dbase < a.head_dim;
+    float mx = kNegInf, L = 0.f, o[4 * VCH];
 #pragma unroll
     for (int e = 0; e < 4 * VCH; ++e) o[e] = 0.f;
-    for (int p = 0; p < np; ++p) {
-        const float* ps = a.partials + (int64_t)(slot0 + p * sstride) * stride;
-        const float mp = ps[16 * a.part_dstride + j];
-        const float w = (mp == kNegInf) ? 0.f : exp2f(mp - mx);
-        L += ps[16 * a.part_dstride + 16 + j] * w;
-        uint32_t raw[4 * VCH];
-        ld_words<16 * VCH>((const char*)(ps + j * a.part_dstride + dbase), raw);
-#pragma unroll
-        for (int e = 0; e < 4 * VCH; ++e) o[e] += w * __uint_as_float(raw[e]);
+    if (active) merge_range<DP>(a, mg, wave, kWaves, j, dbase, mx, L, o);
+    if (g == 0) {
+        s_m[wave][j] = mx;
+        s_l[wave][j] = L;
     }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
-    for (int e = 0; e < 4 * VCH; ++e) o[e] *= inv;
-    char* op = a.out + ((int64_t)pr * a.o_sr + (int64_t)qhead * a.o_sh + dbase) * ES;
-    store_out_chunk<DT, VCH>(op, o);
+    for (int e = 0; e < 4 * VCH; ++e) s_o[wave][j][dbase + e] = o[e];
+    __syncthreads();
+    if (wave != 0 || !active) return;
+    float gm = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) gm = fmaxf(gm, s_m[w][j]);
+    float tot = 0.f, res[4 * VCH];
+#pragma unroll
+    for (int e = 0; e < 4 * VCH; ++e) res[e] = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const float mw = s_m[w][j];
+        const float sc = (mw == kNegInf) ? 0.f : exp2f(mw - gm);
+        tot += s_l[w][j] * sc;
+#pragma unroll
+        for (int e = 0; e < 4 * VCH; ++e) res[e] += s_o[w][j][dbase + e] * sc;
+    }
+    const float inv = tot > 0.f ? 1.f / tot : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4 * VCH; ++e) res[e] *= inv;
+    store_out_chunk<DT, VCH>(a.out + ((int64_t)prow * a.o_sr + (int64_t)qhead * a.o_sh + dbase) * ES, res);
 }
 
 template <int DT, int DP>
 int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t n_wide,
                      const int32_t* merges, int64_t n_merges, bool fast, hipStream_t stream) {
+    // With arrival counters the attention kernel merges its own partitions;
+    // a merges-only call (no items) still runs the separate merge kernel.
+    const bool fused = a.counters != nullptr && (n_narrow + n_wide) > 0;
     if (n_narrow > 0) {
         a.items = items;
         a.num_items = (int)n_narrow;
@@ -500,8 +635,8 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
     } else {
         if (n_wide > 0) return MF_ERR_ARG;  // the plan was made for another dtype
     }
-    if (n_merges > 0) {
-        const dim3 grid((unsigned)((n_merges + kWaves - 1) / kWaves));
+    if (n_merges > 0 && !fused) {
+        const dim3 grid((unsigned)n_merges);
         hipLaunchKernelGGL((merge_kernel<DT, DP>), grid, dim3(256), 0, stream, a, merges, (int)n_merges);
         if (int st = check_launch()) return st;
     }
@@ -553,12 +688,12 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
         const int groups = (nct == 1 || WT == 1) ? nct : (nct + WT - 1) / WT;
         work += (int64_t)Hkv * groups * ((kv_lens[s] + 15) / 16);
     }
-    int P = partition_tiles;
+    int P = std::min(partition_tiles, mf::kMaxItemTiles);
     if (P <= 0) {
         const int64_t target_items = 8192;
         int64_t want = (work + target_items - 1) / target_items;
         P = 4;
-        while (P < want && P < 64) P *= 2;
+        while (P < want && P < mf::kMaxItemTiles) P *= 2;
     }
 
     // First walk: sizes only.
@@ -602,6 +737,7 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
             for (int cg0 = 0; cg0 < nct; cg0 += width) {
                 const int w = std::min(width, nct - cg0);
                 const int64_t group_base = slots;
+                const int64_t merge_base = wm;
                 if (nparts > 1) slots += (int64_t)Hkv * nparts * w;
                 for (int p = 0; p < nparts; ++p) {
                     for (int h = 0; h < Hkv; ++h) {
@@ -614,7 +750,7 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
                         o[4] = p * P;
                         o[5] = std::min(tiles, (p + 1) * P);
                         o[6] = nparts > 1 ? (int32_t)(group_base + ((int64_t)h * nparts + p) * w) : -1;
-                        o[7] = 0;
+                        o[7] = nparts > 1 ? (int32_t)(merge_base + (int64_t)h * w) : -1;
                         ++wi;
                     }
                 }
@@ -637,6 +773,27 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
             }
         }
     }
+    // Longest items first within each class: the hardware hands out
+    // workgroups in order as slots free up, so the last round of the grid is
+    // made of the short remainder partitions instead of a few long ones.
+    // Stable, so equal-length items keep their heads-adjacent order.
+    auto by_length = [&](int64_t first, int64_t count) {
+        if (count < 2) return;
+        std::vector<int64_t> idx(count);
+        for (int64_t i = 0; i < count; ++i) idx[i] = first + i;
+        std::stable_sort(idx.begin(), idx.end(), [&](int64_t x, int64_t y) {
+            const int32_t* a = items + x * MF_PLAN_ITEM_INTS;
+            const int32_t* b = items + y * MF_PLAN_ITEM_INTS;
+            return (a[5] - a[4]) > (b[5] - b[4]);
+        });
+        std::vector<int32_t> tmp((size_t)count * MF_PLAN_ITEM_INTS);
+        for (int64_t i = 0; i < count; ++i)
+            std::copy(items + idx[i] * MF_PLAN_ITEM_INTS, items + (idx[i] + 1) * MF_PLAN_ITEM_INTS,
+                      tmp.begin() + i * MF_PLAN_ITEM_INTS);
+        std::copy(tmp.begin(), tmp.end(), items + first * MF_PLAN_ITEM_INTS);
+    };
+    by_length(0, n_narrow);
+    by_length(n_narrow, n_wide);
     return MF_OK;
 }
 
@@ -650,7 +807,7 @@ extern "C" int mf_paged_attention(
     int64_t new_stride_head, int num_q_heads, int num_kv_heads, int head_dim, float scale,
     const int32_t* plan_items, int64_t num_items_narrow, int64_t num_items_wide,
     const int32_t* plan_merges, int64_t num_merges, float* partials, int64_t partials_floats,
-    mf_stream_t stream) {
+    int32_t* merge_counters, mf_stream_t stream) {
     using namespace mf;
     if (!dtype_ok(dtype) || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
         block_size <= 0 || num_items_narrow < 0 || num_items_wide < 0 || num_merges < 0)
@@ -710,7 +867,9 @@ extern "C" int mf_paged_attention(
     a.scale_log2 = scale * 1.4426950408889634f;
     a.partials = partials;
     a.part_dstride = part_dstride_for(head_dim);
-    const bool fast = block_size == 16 && pool_lens == nullptr;
+    a.merges = plan_merges;
+    a.counters = num_merges > 0 ? merge_counters : nullptr;
+    const bool fast = block_size == 16 && pool_lens == nullptr && head_dim == DP;
     hipStream_t st = (hipStream_t)stream;
 
 #define MF_ATTN_CASE(DT, DPV)                                                                  \

@@ -1,0 +1,75 @@
+"""Host-side launcher of the varlen paged-attention kernel from per-sequence
+descriptions (Python lists or tensors of block ids, per-row sequence ids and
+positions). Shared by every attention entry point of the package; the engine
+uses its own pre-packed path instead of this one."""
+
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from memforge_amd import _native as nat
+
+
+def as_table_list(table) -> List[int]:
+    if isinstance(table, torch.Tensor):
+        return [int(x) for x in table.reshape(-1).tolist()]
+    return [int(x) for x in table]
+
+
+def padded_tables(tables: Sequence[Sequence[int]], device) -> torch.Tensor:
+    width = max(1, max((len(t) for t in tables), default=1))
+    out = np.zeros((max(1, len(tables)), width), dtype=np.int32)
+    for i, t in enumerate(tables):
+        if len(t):
+            out[i, : len(t)] = np.asarray(t, dtype=np.int64).astype(np.int32)
+    return torch.from_numpy(out).to(device)
+
+
+def run_varlen(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: nat.PoolView,
+               tables: Sequence[Sequence[int]], seq_ids: Sequence[int], positions: Sequence[int],
+               scale: Optional[float], num_kv_heads: int, kv_lens: Optional[Sequence[int]] = None,
+               pool_lens: Optional[Sequence[int]] = None, new_k_rows: Optional[torch.Tensor] = None,
+               new_v_rows: Optional[torch.Tensor] = None) -> None:
+    """Attention for packed rows in any order.
+
+    q_rows / out_rows: (T, Hq, D) device views. Row r belongs to table
+    ``seq_ids[r]`` and sees keys 0..positions[r]. ``kv_lens`` (per table)
+    defaults to max position + 1 of that table's rows. With ``pool_lens`` the
+    keys at or above pool_lens[s] are the in-flight rows of sequence s's own
+    query rows, in position order.
+    """
+    dev = q_rows.device
+    T, hq, d = q_rows.shape
+    groups = {}
+    order: List[int] = []
+    for r, s in enumerate(seq_ids):
+        if s not in groups:
+            groups[s] = []
+            order.append(s)
+        groups[s].append(r)
+    row_map: List[int] = []
+    cu = [0]
+    kvl: List[int] = []
+    for s in order:
+        rows = sorted(groups[s], key=lambda r: positions[r])
+        row_map.extend(rows)
+        cu.append(len(row_map))
+        kvl.append(kv_lens[s] if kv_lens is not None else max(positions[r] for r in rows) + 1)
+    identity = row_map == list(range(T))
+    bt = padded_tables([tables[s] for s in order], dev)
+    plan = nat.plan_attention(cu, kvl, hq, num_kv_heads, d, q_rows.dtype, dev)
+    meta = torch.tensor(cu + kvl, dtype=torch.int32).to(dev)
+    pl = None
+    if pool_lens is not None:
+        pl = torch.tensor([pool_lens[s] for s in order], dtype=torch.int32).to(dev)
+    nat.paged_attention(
+        q_rows, out_rows, pool, bt, meta[: len(cu)], meta[len(cu):],
+        torch.tensor(list(positions), dtype=torch.int64).to(dev), plan,
+        scale if scale is not None else 1.0 / math.sqrt(d), num_kv_heads,
+        row_map=None if identity else torch.tensor(row_map, dtype=torch.int32).to(dev),
+        pool_lens=pl, new_k_rows=new_k_rows, new_v_rows=new_v_rows,
+    )

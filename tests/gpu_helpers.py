@@ -40,7 +40,8 @@ def gpu_varlen(q: torch.Tensor, kpool: torch.Tensor, vpool: torch.Tensor,
                tables: Sequence[Sequence[int]], seq_ids: Sequence[int], positions: Sequence[int],
                scale: Optional[float] = None, partition_tiles: int = 0,
                pool_lens: Optional[Sequence[int]] = None, new_k: Optional[torch.Tensor] = None,
-               new_v: Optional[torch.Tensor] = None, layout: str = "bshd") -> torch.Tensor:
+               new_v: Optional[torch.Tensor] = None, layout: str = "bshd",
+               fused: bool = False) -> torch.Tensor:
     """Varlen paged attention through the C ABI.
 
     q: (Hq, T, D) on the device; pools one layer (N, bs, Hkv, D) ("bshd") or
@@ -79,7 +80,7 @@ def gpu_varlen(q: torch.Tensor, kpool: torch.Tensor, vpool: torch.Tensor,
         torch.tensor(list(positions), dtype=torch.int64, device=dev),
         plan, scale if scale is not None else 1.0 / float(np.sqrt(d)), hkv,
         row_map=torch.tensor(row_map, dtype=torch.int32, device=dev),
-        pool_lens=pl, new_k_rows=new_k, new_v_rows=new_v,
+        pool_lens=pl, new_k_rows=new_k, new_v_rows=new_v, fused_merge=fused,
     )
     return out.permute(1, 0, 2)
 

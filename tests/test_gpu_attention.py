@@ -209,3 +209,30 @@ def test_operator_layout_bhsd(device):
                      layout="bhsd")
     got = got.permute(1, 0, 2).reshape(1, qlen, h * d)
     assert np.abs(to_np64(got) - want).max() <= 1e-5
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_split_k_merge_fused_and_separate_agree(device, fused):
+    """The in-kernel (last arrival) merge and the separate merge kernel give the
+    oracle's result, call after call: the arrival counters return to zero."""
+    gen = torch.Generator().manual_seed(21)
+    bs, hq, hkv, d = 16, 40, 8, 128
+    ctx = [1, 16, 17, 700, 3000]
+    n = sum((c + bs - 1) // bs for c in ctx)
+    tables = random_tables(gen, n, ctx, bs)
+    kp, vp = _pool(gen, n, bs, hkv, d, torch.bfloat16, device)
+    q = torch.randn((hq, len(ctx), d), generator=gen).to(torch.bfloat16).to(device)
+    positions = [c - 1 for c in ctx]
+    want = oatt.varlen_attention(to_np64(q), to_np64(kp), to_np64(vp), tables, list(range(5)), positions, bs)
+    first = None
+    for _ in range(3):
+        got = gpu_varlen(q, kp, vp, tables, list(range(5)), positions, partition_tiles=2, fused=fused)
+        _check(to_np64(got), want, torch.bfloat16)
+        if first is None:
+            first = got.clone()
+        else:
+            assert torch.equal(got, first)
+    from memforge_amd import _native as nat
+
+    for buf in nat._WORKSPACE._counters.values():
+        assert int(buf.abs().sum()) == 0

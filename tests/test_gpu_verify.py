@@ -1,0 +1,95 @@
+"""Rejection-sampling verify kernel: accepted-token sequences bit-exact against
+the oracle's restatement of RejectionSampler.verify_tokens given the same
+randomness (uniforms for the accept tests, Exp(1) noise for the final draw)."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from memforge_amd import _native as nat
+from oracle import rejection as orj
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_both(device, draft_logits, target_logits, draft_tokens, u, noise, temperature):
+    """draft_logits (B, K, V); target_logits (B, K+1, Vt >= V)."""
+    B, K, V = draft_logits.shape
+    draft_probs = torch.stack([
+        torch.from_numpy(np.stack([orj.probs_from_logits(draft_logits[b, i].numpy(), temperature)
+                                   for i in range(K)])) for b in range(B)])
+    res = nat.spec_verify(draft_tokens.to(device), draft_probs.to(device), target_logits.to(device),
+                          temperature, u.to(device), noise.to(device))
+    tokens = res.tokens.cpu().numpy()
+    flags = res.is_draft.cpu().numpy()
+    count = res.count.cpu().numpy()
+    nacc = res.num_accepted.cpu().numpy()
+    for b in range(B):
+        want_tok, want_flags, want_acc = orj.resolve_round(
+            draft_tokens[b].tolist(), [draft_probs[b, i].numpy() for i in range(K)],
+            [target_logits[b, i].numpy() for i in range(K + 1)], temperature,
+            u[b].tolist(), noise[b].numpy())
+        n = int(count[b])
+        assert tokens[b, :n].tolist() == want_tok, f"row {b}"
+        assert [bool(x) for x in flags[b, :n]] == want_flags, f"row {b}"
+        assert int(nacc[b]) == want_acc, f"row {b}"
+    return count, nacc
+
+
+def _inputs(seed, B, K, V, Vt=None, agree=0.0):
+    """N(0,2) logits (std sqrt(2)); target = agree * draft + noise, so larger
+    `agree` gives a higher acceptance rate."""
+    gen = torch.Generator().manual_seed(seed)
+    Vt = Vt or V
+    draft = torch.randn((B, K, V), generator=gen) * math.sqrt(2.0)
+    target = torch.randn((B, K + 1, Vt), generator=gen) * math.sqrt(2.0)
+    target[:, :K, :V] = agree * draft + (1 - agree) * target[:, :K, :V]
+    probs = torch.softmax(draft, dim=-1)
+    tokens = torch.multinomial(probs.reshape(B * K, V), 1, generator=gen).reshape(B, K).to(torch.int32)
+    u = torch.rand((B, K), generator=gen)
+    noise = torch.empty((B, V)).exponential_(1.0, generator=gen)
+    return draft, target, tokens, u, noise
+
+
+@pytest.mark.parametrize("agree", [0.0, 0.9, 1.0])
+def test_c3_shape_bit_exact(device, agree):
+    """Config 3's rejection step: 16 rows, k=4, vocab 49152, fp32 logits."""
+    draft, target, tokens, u, noise = _inputs(0, 16, 4, 49152, agree=agree)
+    count, nacc = _run_both(device, draft, target, tokens, u, noise, 1.0)
+    if agree == 1.0:
+        assert (nacc == 4).all() and (count == 5).all()
+
+
+@pytest.mark.parametrize("temperature", [0.7, 1.3])
+def test_temperatures_and_wider_target_vocab(device, temperature):
+    """Target vocabulary wider than the draft's is clipped before the softmax
+    (test_vocab_padding.py:6-35)."""
+    draft, target, tokens, u, noise = _inputs(1, 8, 3, 3000, Vt=3128, agree=0.8)
+    _run_both(device, draft, target, tokens, u, noise, temperature)
+
+
+def test_greedy_known_answers(device):
+    """temperature 0: a candidate equal to the target argmax is always accepted;
+    the first that differs is replaced by the target argmax and ends the row
+    (test_rejection_sampler.py:5-50, test_batched_speculative.py:320-376)."""
+    B, K, V = 3, 4, 50
+    gen = torch.Generator().manual_seed(2)
+    target = torch.randn((B, K + 1, V), generator=gen)
+    greedy = target.argmax(-1)
+    draft = torch.randn((B, K, V), generator=gen)
+    tokens = greedy[:, :K].clone().to(torch.int32)
+    tokens[1, 2] = (greedy[1, 2] + 1) % V   # row 1 diverges at position 2
+    tokens[2, 0] = (greedy[2, 0] + 7) % V   # row 2 diverges at once
+    # one-hot drafts on the proposed tokens (the greedy draft distribution)
+    for b in range(B):
+        for i in range(K):
+            draft[b, i] = -1e4
+            draft[b, i, int(tokens[b, i])] = 0.0
+    u = torch.rand((B, K), generator=gen)
+    noise = torch.empty((B, V)).exponential_(1.0, generator=gen)
+    count, nacc = _run_both(device, draft, target, tokens, u, noise, 0.0)
+    assert nacc.tolist() == [4, 2, 0] and count.tolist() == [5, 3, 1]
