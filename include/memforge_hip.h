@@ -196,7 +196,8 @@ int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const int32_t* kv
  * ties), which is torch.multinomial(w, 1) given the same Exp(1) noise.
  * Target probabilities are softmax(target_logits[b][i][:V] / temperature) in
  * fp32, or a one-hot argmax when temperature <= 0; target logits wider than the
- * draft vocabulary V are clipped to V first.
+ * draft vocabulary V are clipped to V first. With target_is_probs != 0 the
+ * target rows already are probabilities (fp32) and are used as given.
  * Outputs: out_tokens[b][0..out_count[b]) (at most K+1), out_is_draft likewise,
  * out_num_accepted[b] draft tokens accepted.
  * workspace: at least mf_spec_verify_workspace_size(B, K) bytes.
@@ -210,7 +211,7 @@ int mf_spec_verify(int num_rows, int num_draft, int vocab,
                    const float* draft_probs, int64_t dp_stride_row, int64_t dp_stride_pos,
                    const void* target_logits, int target_dtype,
                    int64_t tl_stride_row, int64_t tl_stride_pos,
-                   float temperature, const float* u_accept,
+                   float temperature, int target_is_probs, const float* u_accept,
                    const float* exp_noise, int64_t noise_stride_row,
                    int32_t* out_tokens, uint8_t* out_is_draft, int32_t* out_count,
                    int32_t* out_num_accepted, void* workspace, int64_t workspace_bytes,

@@ -52,8 +52,8 @@ _SIGNATURES = {
                                    _vp, _c_i64, _vp, _c_i64, _vp]),
     "mf_spec_verify_workspace_size": (_c_i64, [_c_int, _c_int]),
     "mf_spec_verify": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _c_i64, _c_i64, _vp, _c_int,
-                                _c_i64, _c_i64, _c_f32, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp,
-                                _vp, _c_i64, _vp]),
+                                _c_i64, _c_i64, _c_f32, _c_int, _vp, _vp, _c_i64, _vp, _vp, _vp,
+                                _vp, _vp, _c_i64, _vp]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -383,9 +383,11 @@ class VerifyResult:
 
 
 def spec_verify(draft_tokens: torch.Tensor, draft_probs: torch.Tensor, target_logits: torch.Tensor,
-                temperature: float, u_accept: torch.Tensor, exp_noise: torch.Tensor) -> VerifyResult:
+                temperature: float, u_accept: torch.Tensor, exp_noise: torch.Tensor,
+                target_is_probs: bool = False) -> VerifyResult:
     """Batched rejection sampling. Shapes: draft_tokens (B, K) int32,
-    draft_probs (B, K, V) fp32, target_logits (B, K+1, >=V), u_accept (B, K) fp32,
+    draft_probs (B, K, V) fp32, target_logits (B, K+1, >=V) -- or target
+    probabilities (fp32) with ``target_is_probs`` --, u_accept (B, K) fp32,
     exp_noise (B, V) fp32."""
     require_device(draft_tokens, draft_probs, target_logits, u_accept, exp_noise)
     B, K = draft_tokens.shape
@@ -410,7 +412,7 @@ def spec_verify(draft_tokens: torch.Tensor, draft_probs: torch.Tensor, target_lo
         B, K, V, _ptr(draft_tokens), _ptr(draft_probs),
         draft_probs.stride(0) if K > 0 else 0, draft_probs.stride(1) if K > 0 else 0,
         _ptr(target_logits), dtype_code(target_logits.dtype), target_logits.stride(0),
-        target_logits.stride(1), float(temperature), _ptr(u_accept), _ptr(exp_noise),
+        target_logits.stride(1), float(temperature), int(bool(target_is_probs)), _ptr(u_accept), _ptr(exp_noise),
         exp_noise.stride(0), _ptr(res.tokens), _ptr(res.is_draft), _ptr(res.count),
         _ptr(res.num_accepted), _ptr(ws), ws_bytes, _stream(),
     ), "mf_spec_verify")

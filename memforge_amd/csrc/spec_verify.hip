@@ -30,6 +30,7 @@ struct VerifyArgs {
     int ldt;
     int64_t tl_sr, tl_sp;
     float temperature;
+    int target_is_probs;  // target rows are probabilities, not logits
     const float* u_accept;
     const float* noise;
     int64_t noise_sr;
@@ -118,6 +119,7 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(VerifyArgs a) {
 
 // Target probability of token v at position i of row b.
 __device__ __forceinline__ float target_prob(const VerifyArgs& a, int b, int i, int v) {
+    if (a.target_is_probs) return load_logit(a, b, i, v);
     const int row = b * (a.K + 1) + i;
     if (a.temperature <= 0.f) return v == a.row_argmax[row] ? 1.f : 0.f;
     const float x = load_logit(a, b, i, v) / a.temperature;
@@ -200,7 +202,8 @@ extern "C" int64_t mf_spec_verify_workspace_size(int num_rows, int num_draft) {
 extern "C" int mf_spec_verify(int num_rows, int num_draft, int vocab, const int32_t* draft_tokens,
                               const float* draft_probs, int64_t dp_stride_row, int64_t dp_stride_pos,
                               const void* target_logits, int target_dtype, int64_t tl_stride_row,
-                              int64_t tl_stride_pos, float temperature, const float* u_accept,
+                              int64_t tl_stride_pos, float temperature, int target_is_probs,
+                              const float* u_accept,
                               const float* exp_noise, int64_t noise_stride_row, int32_t* out_tokens,
                               uint8_t* out_is_draft, int32_t* out_count, int32_t* out_num_accepted,
                               void* workspace, int64_t workspace_bytes, mf_stream_t stream) {
@@ -217,12 +220,14 @@ extern "C" int mf_spec_verify(int num_rows, int num_draft, int vocab, const int3
     // candidates the bonus row is the only draw and q is never read.
     VerifyArgs a{num_rows, num_draft, vocab, draft_tokens, draft_probs, dp_stride_row, dp_stride_pos,
                  (const char*)target_logits, target_dtype, tl_stride_row, tl_stride_pos, temperature,
-                 u_accept, exp_noise, noise_stride_row, out_tokens, out_is_draft, out_count,
+                 target_is_probs, u_accept, exp_noise, noise_stride_row, out_tokens, out_is_draft, out_count,
                  out_num_accepted, (float*)workspace, (float*)workspace + nrow,
                  (int32_t*)((float*)workspace + 2 * nrow)};
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(row_stats_kernel, dim3((unsigned)nrow), dim3(kThreads), 0, st, a);
-    if (int e = check_launch()) return e;
+    if (!target_is_probs) {
+        hipLaunchKernelGGL(row_stats_kernel, dim3((unsigned)nrow), dim3(kThreads), 0, st, a);
+        if (int e = check_launch()) return e;
+    }
     hipLaunchKernelGGL(decide_kernel, dim3((unsigned)num_rows), dim3(kThreads), 0, st, a);
     return check_launch();
 }

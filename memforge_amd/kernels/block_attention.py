@@ -56,6 +56,6 @@ def reference_attention(query: torch.Tensor, keys: torch.Tensor, values: torch.T
     if group > 1:
         k = k.repeat_interleave(group, dim=1)
         v = v.repeat_interleave(group, dim=1)
-    scores = torch.einsum("bhqd,bhtd->bhqt", query.to(torch.float32), k) * scale
+    scores = torch.matmul(query.to(torch.float32), k.transpose(2, 3).contiguous()) * scale
     weights = torch.softmax(scores, dim=-1)
-    return torch.einsum("bhqt,bhtd->bhqd", weights, v).to(query.dtype)
+    return torch.matmul(weights, v.contiguous()).to(query.dtype)

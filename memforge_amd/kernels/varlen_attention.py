@@ -124,6 +124,7 @@ def reference_varlen_attention(query: torch.Tensor, key_pool: torch.Tensor, valu
             keys = keys.repeat_interleave(group, dim=1)
             values = values.repeat_interleave(group, dim=1)
         q = query[0, :, row, :].float()
-        weights = torch.softmax(torch.einsum("hd,thd->ht", q, keys) * scale, dim=-1)
-        out[:, row, :] = torch.einsum("ht,thd->hd", weights, values)
+        scores = torch.matmul(keys.permute(1, 0, 2).contiguous(), q.unsqueeze(-1)).squeeze(-1) * scale
+        weights = torch.softmax(scores, dim=-1)  # (heads, visible)
+        out[:, row, :] = torch.matmul(weights.unsqueeze(1), values.permute(1, 0, 2).contiguous()).squeeze(1)
     return out.unsqueeze(0).to(query.dtype)

@@ -1,0 +1,781 @@
+"""ContinuousBatchingEngine on the MI355X.
+
+Same public surface as the reference engine (memforge_ml/runtime/
+continuous_engine.py:131-1613): submit / abort / step / run_until_idle /
+generate / result_for / drain_events / telemetry, with the C++ scheduler and
+block allocator (``memforge_c``) deciding every step which sequences run and
+which physical blocks they own.
+
+What differs is the execution of a step. The reference runs prefill chunks
+and decodes as separate passes (a padded, gathered batch for decode; an
+optional fused varlen pass). Here EVERY step is one packed pass through the
+model, because the varlen HIP kernel serves prefill chunks and decodes alike:
+
+1. the scheduler's step output becomes one descriptor per contributing
+   sequence (prefill entries first, then decodes, in scheduler order, as in the
+   reference's fused step), staged in pinned memory and copied to the GPU in
+   one transfer together with the block tables and the step's token ids;
+2. the ragged-pack kernel builds token ids, positions, slot_mapping,
+   cu_seqlens and padded block tables on the device;
+3. the model runs once over the packed row; each layer's cache update is the
+   KV-write kernel through slot_mapping and its attention the varlen kernel
+   reading the pool in place -- nothing is gathered or padded;
+4. only each sequence's last row goes through the LM head, and greedy
+   sampling is one device argmax and one device-to-host copy per step.
+
+Speculative decoding (draft model + lookahead) verifies all candidate runs in
+one varlen pass with the candidates attended in flight, resolves them with the
+rejection sampler, and writes only the confirmed K/V.
+"""
+
+from __future__ import annotations
+
+import logging
+import threading
+import time
+from collections import deque
+from dataclasses import dataclass, field
+from typing import Any, Deque, Dict, List, Optional
+
+import numpy as np
+import torch
+
+from memforge_amd import _native as nat
+from memforge_amd.kernels import attention_backend
+from memforge_amd.runtime.batched_speculative import (
+    DraftState,
+    propose_draft_tokens,
+    resolve_round,
+    scatter_accepted_kv,
+    verify_candidates_batched,
+)
+from memforge_amd.runtime.kv_pool import ModelKVSpec, PagedKVPool
+from memforge_amd.runtime.prefix_sharing import block_owners, copy_block, sharing_telemetry
+from memforge_amd.runtime.sampling import SamplingParams, sample_logits
+from memforge_amd.runtime.varlen_cache import VarlenPackedCache
+
+LOGGER = logging.getLogger(__name__)
+
+try:
+    from memforge_amd import memforge_c
+
+    HAS_CPP_ENGINE = True
+except ImportError:  # pragma: no cover - only on an unbuilt checkout
+    memforge_c = None
+    HAS_CPP_ENGINE = False
+
+
+@dataclass
+class TokenEvent:
+    """A single emitted token."""
+
+    seq_id: int
+    index: int
+    token_id: int
+    text: str
+    source: str = "target"  # "target" | "draft" | "resample"
+
+
+class SequenceCursor:
+    """Where a running sequence's resident KV ends and which blocks hold it
+    (the engine-side state the reference keeps in each sequence's PagedCache)."""
+
+    __slots__ = ("block_table", "position", "_table_tensor")
+
+    def __init__(self, block_table: List[int], position: int = 0):
+        self.block_table = list(block_table)
+        self.position = position
+        self._table_tensor = None
+
+    def rebind(self, block_table: List[int]) -> None:
+        if list(block_table) != self.block_table:
+            self.block_table = list(block_table)
+            self._table_tensor = None
+
+    def block_table_tensor(self, device) -> torch.Tensor:
+        if self._table_tensor is None:
+            self._table_tensor = torch.tensor(self.block_table, dtype=torch.long, device=device)
+        return self._table_tensor
+
+
+@dataclass
+class SequenceRuntime:
+    """Python-side state for one in-flight sequence (the C++ side owns memory)."""
+
+    seq_id: int
+    prompt_ids: List[int]
+    params: SamplingParams
+    tokens: List[int]
+    cache: Optional[SequenceCursor] = None
+    generated: List[int] = field(default_factory=list)
+    sources: List[str] = field(default_factory=list)
+    events: Deque[TokenEvent] = field(default_factory=deque)
+    generator: Optional[torch.Generator] = None
+    submitted_at: float = field(default_factory=time.perf_counter)
+    first_token_at: Optional[float] = None
+    finished_at: Optional[float] = None
+    finish_reason: Optional[str] = None
+    num_prefills: int = 0
+    num_preemptions: int = 0
+    decoded_chars: int = 0
+    draft: Optional[DraftState] = None
+    num_draft_proposed: int = 0
+    num_draft_accepted: int = 0
+
+    @property
+    def done(self) -> bool:
+        return self.finish_reason is not None
+
+    @property
+    def prompt_len(self) -> int:
+        return len(self.prompt_ids)
+
+
+@dataclass
+class StepReport:
+    """Telemetry for one iteration-level scheduler step."""
+
+    step_index: int
+    num_running: int
+    num_waiting: int
+    num_prefill: int
+    num_decode: int
+    tokens_emitted: int
+    finished: List[int]
+    preempted: List[int]
+    aborted: List[int]
+    free_blocks: int
+    total_blocks: int
+    memory_utilization: float
+    step_latency_ms: float
+    events: List[TokenEvent]
+
+
+class _Staging:
+    """Grow-only pinned host buffer and its device twin for the per-step
+    descriptors, so a step's metadata crosses PCIe in one copy."""
+
+    def __init__(self, device):
+        self.device = device
+        self.host = torch.empty(0, dtype=torch.int32).pin_memory()
+        self.dev = torch.empty(0, dtype=torch.int32, device=device)
+        self.copied = None  # event recorded after the last copy out of ``host``
+
+    def upload(self, arr: np.ndarray) -> torch.Tensor:
+        n = arr.size
+        if self.copied is not None:
+            # the previous copy must have left the pinned buffer before it is rewritten
+            self.copied.synchronize()
+        if self.host.numel() < n:
+            cap = max(n, 2 * self.host.numel(), 1 << 16)
+            self.host = torch.empty(cap, dtype=torch.int32).pin_memory()
+            self.dev = torch.empty(cap, dtype=torch.int32, device=self.device)
+        self.host[:n].numpy()[:] = arr
+        self.dev[:n].copy_(self.host[:n], non_blocking=True)
+        self.copied = torch.cuda.Event()
+        self.copied.record()
+        return self.dev[:n]
+
+
+class ContinuousBatchingEngine:
+    def __init__(self, model, tokenizer, *, block_size: int = 16, num_blocks: Optional[int] = None,
+                 kv_budget_mb: float = 512.0, max_num_seqs: int = 16, max_model_len: int = 2048,
+                 dtype: Optional[torch.dtype] = None, device: Optional[str] = None,
+                 batched_decode: bool = True, enable_prefix_sharing: bool = True,
+                 decode_view_cache: bool = False, view_cache_budget_mb: float = 512.0,
+                 block_attention: bool = False, max_prefill_tokens_per_step: int = 0,
+                 draft_model=None, lookahead_k: int = 0, fused_prefill: bool = False,
+                 paged_attn_kernel: str = "gather", draft_cuda_graph=False, paged_cuda_graph=False):
+        if not HAS_CPP_ENGINE:
+            raise RuntimeError("The native memforge_c extension is required; build it with "
+                               "`python -m memforge_amd._build`")
+        if decode_view_cache:
+            raise NotImplementedError("the contiguous decode mirror is not part of memforge_amd")
+        self.model = model
+        self.tokenizer = tokenizer
+        self.device = device or str(next(model.parameters()).device)
+        if torch.device(self.device).type != "cuda":
+            raise ValueError(f"memforge_amd runs the engine on the GPU; got device {self.device!r}")
+        self.dtype = dtype or next(model.parameters()).dtype
+        self.block_size = block_size
+        self.max_num_seqs = max_num_seqs
+        self.max_model_len = max_model_len
+        # Accepted for API compatibility: every step is one packed varlen pass,
+        # which is what the reference's batched_decode / block_attention /
+        # fused_prefill / paged kernel options choose between.
+        self.batched_decode = batched_decode
+        self.fused_prefill = True
+        self.block_attention = True
+        self.decode_view_cache = False
+
+        self.spec = ModelKVSpec.from_config(model.config, self.dtype, self.device)
+        if num_blocks is None:
+            num_blocks = PagedKVPool.blocks_for_budget(self.spec, block_size, kv_budget_mb)
+        self.pool = PagedKVPool(self.spec, num_blocks=num_blocks, block_size=block_size)
+
+        self.allocator = memforge_c.BlockAllocator(num_blocks, block_size)
+        self.prefix_cache = memforge_c.PrefixCache(self.allocator, block_size) if enable_prefix_sharing else None
+        self.max_prefill_tokens_per_step = max(0, int(max_prefill_tokens_per_step))
+        self.draft_model = draft_model
+        self.lookahead_k = max(0, int(lookahead_k)) if draft_model is not None else 0
+        lookahead_slots = self.lookahead_k + 1 if self.lookahead_k > 0 else 0
+        self.scheduler = memforge_c.Scheduler(self.allocator, max_num_seqs, self.prefix_cache,
+                                              self.max_prefill_tokens_per_step, lookahead_slots)
+        if not attention_backend.register():
+            raise RuntimeError("the transformers attention registry is required")
+        self._staging = _Staging(self.device)
+
+        self.eos_token_ids = self._resolve_eos_ids()
+        self.runtimes: Dict[int, SequenceRuntime] = {}
+        self._next_seq_id = 1
+        self._step_index = 0
+        self.total_tokens_generated = 0
+        self.total_prefill_tokens = 0
+        self.total_steps = 0
+        self.total_forward_passes = 0
+        self.total_preemptions = 0
+        self.total_cached_prefix_tokens = 0
+        self.total_cow_copies = 0
+        self.total_prefill_chunks = 0
+        self.total_fused_steps = 0
+        self.total_fused_tokens = 0
+        self.total_draft_tokens_proposed = 0
+        self.total_draft_tokens_accepted = 0
+        self.total_speculative_rounds = 0
+        self.total_speculative_sequence_rounds = 0
+        self.total_blockwise_layers = 0
+        self.total_blockwise_fallbacks = 0
+        self.engine_started_at = time.perf_counter()
+        self._abort_lock = threading.Lock()
+        self._pending_aborts: set = set()
+        self.throughput_window_s = 5.0
+        self._recent_tokens: Deque[float] = deque()
+
+    # ------------------------------------------------------------------ setup
+
+    def _resolve_eos_ids(self) -> set:
+        ids = set()
+        cfg_eos = getattr(self.model.config, "eos_token_id", None)
+        for candidate in (cfg_eos, getattr(self.tokenizer, "eos_token_id", None)):
+            if isinstance(candidate, int):
+                ids.add(candidate)
+            elif isinstance(candidate, (list, tuple)):
+                ids.update(int(c) for c in candidate)
+        return ids
+
+    def describe(self) -> Dict[str, Any]:
+        return {
+            "engine": "C++ native (memforge_c) + HIP data path (libmemforge_hip)",
+            "model": getattr(self.model.config, "name_or_path", "unknown"),
+            "device": self.device,
+            "dtype": str(self.dtype),
+            "max_num_seqs": self.max_num_seqs,
+            "max_model_len": self.max_model_len,
+            "batched_decode": True,
+            "prefix_sharing": self.prefix_cache is not None,
+            "decode_view_cache": False,
+            "block_attention": True,
+            "max_prefill_tokens_per_step": self.max_prefill_tokens_per_step,
+            "chunked_prefill": self.max_prefill_tokens_per_step > 0,
+            "eos_token_ids": sorted(self.eos_token_ids),
+            "kv_pool": self.pool.describe(),
+        }
+
+    # ------------------------------------------------------------- submission
+
+    def submit(self, prompt, params: Optional[SamplingParams] = None) -> int:
+        """Enqueue a request; nothing runs until ``step()`` (continuous_engine.py:381-414)."""
+        params = params or SamplingParams()
+        if isinstance(prompt, str):
+            prompt_ids = self.tokenizer(prompt, return_tensors=None)["input_ids"]
+        else:
+            prompt_ids = list(prompt)
+        if not prompt_ids:
+            raise ValueError("cannot submit an empty prompt")
+        headroom = self.max_model_len - len(prompt_ids)
+        if headroom <= 0:
+            raise ValueError(f"prompt of {len(prompt_ids)} tokens leaves no room under "
+                             f"max_model_len={self.max_model_len}")
+        params = params.clamped(headroom)
+        seq_id = self._next_seq_id
+        self._next_seq_id += 1
+        generator = None
+        if params.seed is not None:
+            generator = torch.Generator(device="cpu").manual_seed(params.seed)
+        self.runtimes[seq_id] = SequenceRuntime(seq_id=seq_id, prompt_ids=list(prompt_ids), params=params,
+                                                tokens=list(prompt_ids), generator=generator)
+        self.scheduler.add_sequence(seq_id, list(prompt_ids), params.max_new_tokens)
+        return seq_id
+
+    def abort(self, seq_id: int) -> bool:
+        """Request abandonment from any thread; applied at the top of the next step."""
+        rt = self.runtimes.get(seq_id)
+        if rt is None or rt.done:
+            return False
+        with self._abort_lock:
+            self._pending_aborts.add(seq_id)
+        return True
+
+    def _process_pending_aborts(self) -> None:
+        with self._abort_lock:
+            if not self._pending_aborts:
+                return
+            pending, self._pending_aborts = self._pending_aborts, set()
+        for seq_id in pending:
+            rt = self.runtimes.get(seq_id)
+            if rt is None or rt.done:
+                continue
+            self.scheduler.abort_sequence(seq_id)
+            self._finish(rt, "aborted")
+
+    # ------------------------------------------------------------------ steps
+
+    def has_work(self) -> bool:
+        with self._abort_lock:
+            if self._pending_aborts:
+                return True
+        return self.scheduler.has_unfinished_sequences() or any(not rt.done for rt in self.runtimes.values())
+
+    @property
+    def speculation_enabled(self) -> bool:
+        return self.draft_model is not None and self.lookahead_k > 0
+
+    def step(self) -> StepReport:
+        """Run exactly one iteration-level scheduling + execution step."""
+        t0 = time.perf_counter()
+        self._process_pending_aborts()
+        result = self.scheduler.step()
+        self._step_index += 1
+        self.total_steps += 1
+
+        for seq_id in result.aborted_sequence_ids:
+            rt = self.runtimes.get(seq_id)
+            if rt is not None and not rt.done:
+                self._finish(rt, "aborted_unschedulable")
+        for seq_id in result.preempted_sequence_ids:
+            rt = self.runtimes.get(seq_id)
+            if rt is not None and rt.cache is not None:
+                rt.cache = None
+                rt.num_preemptions += 1
+                self.total_preemptions += 1
+
+        prefill_infos = [i for i in result.running_sequences if i.is_prefill]
+        decode_infos = [i for i in result.running_sequences if not i.is_prefill]
+        events: List[TokenEvent] = []
+
+        plan: List[dict] = []
+        for info in prefill_infos:
+            entry = self._prepare_prefill(info)
+            if entry is not None:
+                plan.append(entry)
+        n_prefill = len(plan)
+        spec_rts: List[SequenceRuntime] = []
+        for info in decode_infos:
+            rt = self.runtimes.get(info.seq_id)
+            if rt is None or rt.done or rt.cache is None:
+                continue
+            self._begin_write_step(rt, info)
+            if self.speculation_enabled and self._speculation_headroom(rt):
+                spec_rts.append(rt)
+            else:
+                plan.append({"rt": rt, "kind": "decode", "tokens": [rt.tokens[-1]],
+                             "start": rt.cache.position, "table": rt.cache.block_table})
+        if plan:
+            events.extend(self._run_packed(plan))
+            if n_prefill and len(plan) > n_prefill:
+                self.total_fused_steps += 1
+        if spec_rts:
+            events.extend(self._run_speculative(spec_rts))
+
+        for seq_id in result.finished_sequence_ids:
+            rt = self.runtimes.get(seq_id)
+            if rt is not None and not rt.done:
+                self._finish(rt, "length")
+
+        return StepReport(
+            step_index=self._step_index,
+            num_running=len(result.running_sequences),
+            num_waiting=result.num_waiting,
+            num_prefill=n_prefill,
+            num_decode=len(plan) - n_prefill + len(spec_rts),
+            tokens_emitted=len(events),
+            finished=list(result.finished_sequence_ids),
+            preempted=list(result.preempted_sequence_ids),
+            aborted=list(result.aborted_sequence_ids),
+            free_blocks=result.num_free_blocks,
+            total_blocks=result.total_blocks,
+            memory_utilization=result.memory_utilization_ratio,
+            step_latency_ms=(time.perf_counter() - t0) * 1000.0,
+            events=events,
+        )
+
+    def _prepare_prefill(self, info) -> Optional[dict]:
+        """This step's prefill chunk of one sequence, with the reference's chunk
+        arithmetic (continuous_engine.py:603-640, 782-832)."""
+        rt = self.runtimes.get(info.seq_id)
+        if rt is None or rt.done:
+            return None
+        table = list(info.block_table)
+        if rt.cache is None:
+            rt.cache = SequenceCursor(table)
+        else:
+            rt.cache.rebind(table)
+        cached = int(getattr(info, "num_cached_tokens", 0) or 0)
+        total = len(rt.tokens)
+        chunk_end = int(getattr(info, "prefill_chunk_end", 0) or 0)
+        if chunk_end <= 0 or chunk_end > total:
+            chunk_end = total
+        if cached >= total:
+            cached, chunk_end = 0, total
+        if chunk_end <= cached:
+            return None  # budget exhausted this step; resumes next step
+        rt.num_prefills += 1
+        rt.cache.position = cached
+        return {"rt": rt, "kind": "prefill", "tokens": rt.tokens[cached:chunk_end], "start": cached,
+                "table": table, "cached": cached, "chunk_end": chunk_end, "is_final": chunk_end >= total}
+
+    def _begin_write_step(self, rt: SequenceRuntime, info) -> None:
+        """Rebind a decoding sequence's table, copying a shared block on write
+        (continuous_engine.py:974-1006)."""
+        rt.cache.rebind(list(info.block_table))
+        if self.prefix_cache is None:
+            return
+        seq = self.scheduler.get_sequence(rt.seq_id)
+        if seq is None:
+            return
+        cow = self.allocator.prepare_write(seq, rt.cache.position // self.block_size)
+        if cow is None:
+            return
+        old_block, new_block = cow
+        copy_block(self.pool, old_block, new_block)
+        rt.cache.rebind(list(seq.get_block_table()))
+        self.total_cow_copies += 1
+
+    # ------------------------------------------------------------ packed pass
+
+    def _run_packed(self, plan: List[dict]) -> List[TokenEvent]:
+        """One forward over every entry of ``plan`` (prefill chunks, then decodes)."""
+        bs = self.block_size
+        B = len(plan)
+        q_lens = [len(e["tokens"]) for e in plan]
+        starts = [e["start"] for e in plan]
+        kv_lens = [s + q for s, q in zip(starts, q_lens)]
+        tables = [e["table"] for e in plan]
+        for e, kv, t in zip(plan, kv_lens, tables):
+            if kv > len(t) * bs:
+                raise IndexError(f"sequence {e['rt'].seq_id} needs {kv} slots but its block table "
+                                 f"has {len(t)} blocks of {bs}")
+        max_blocks = max(len(t) for t in tables)
+        T = int(sum(q_lens))
+        cu = np.zeros(B + 1, dtype=np.int64)
+        np.cumsum(q_lens, out=cu[1:])
+
+        # descriptors | tables | tokens in one int32 upload
+        ent = np.empty((B, nat.ENTRY_INTS), dtype=np.int32)
+        t_off = np.zeros(B, dtype=np.int64)
+        t_off[1:] = np.cumsum([len(t) for t in tables])[:-1]
+        ent[:, 0] = q_lens
+        ent[:, 1] = starts
+        ent[:, 2] = kv_lens
+        ent[:, 3] = t_off
+        ent[:, 4] = [len(t) for t in tables]
+        ent[:, 5] = cu[:-1]
+        flat_tables = np.fromiter((b for t in tables for b in t), dtype=np.int32)
+        flat_tokens = np.fromiter((tok for e in plan for tok in e["tokens"]), dtype=np.int32)
+        buf = np.concatenate([ent.reshape(-1), flat_tables, flat_tokens])
+        dev = self._staging.upload(buf)
+        ne, nt = ent.size, flat_tables.size
+        packed = nat.ragged_pack(dev[:ne].view(B, nat.ENTRY_INTS), dev[ne:ne + nt], dev[ne + nt:],
+                                 T, bs, max_blocks)
+        attn_plan = nat.plan_attention(cu.tolist(), kv_lens, self.model.config.num_attention_heads,
+                                       self.spec.num_kv_heads, self.spec.head_dim, self.dtype, self.device)
+        meta = {"block_tables": packed.block_tables, "cu_seqlens": packed.cu_seqlens,
+                "kv_lens": packed.kv_lens, "positions": packed.positions, "row_map": None,
+                "plan": attn_plan}
+        binding = attention_backend._VarlenBinding.from_packed(self.pool, meta, T)
+        cache = VarlenPackedCache.from_slot_mapping(self.pool, self.spec.num_layers, packed.slot_mapping)
+
+        # only rows that produce a token go through the LM head
+        emit = [i for i, e in enumerate(plan) if e["kind"] == "decode" or e["is_final"]]
+        keep = torch.tensor([int(cu[i + 1]) - 1 for i in emit], dtype=torch.long).to(self.device)
+        with attention_backend.backend_enabled_on(self.model) as routed:
+            if not routed:
+                raise RuntimeError("the packed pass needs the attention registry")
+            with attention_backend.bind_varlen(binding):
+                with torch.no_grad():
+                    out = self.model(input_ids=packed.token_ids.view(1, T),
+                                     position_ids=packed.positions.view(1, T),
+                                     past_key_values=cache, use_cache=True, logits_to_keep=keep)
+        if binding.used != self.spec.num_layers:
+            raise RuntimeError(f"packed pass: {binding.used} of {self.spec.num_layers} layers used the kernel")
+        self.total_forward_passes += 1
+        self.total_blockwise_layers += binding.used
+        self.total_fused_tokens += T
+
+        logits = out.logits[0]  # (len(emit), vocab)
+        greedy = [j for j, i in enumerate(emit) if plan[i]["rt"].params.temperature <= 0.0]
+        tokens: Dict[int, int] = {}
+        if greedy:
+            idx = torch.tensor(greedy, dtype=torch.long).to(self.device)
+            for j, tok in zip(greedy, logits.index_select(0, idx).argmax(dim=-1).tolist()):
+                tokens[j] = int(tok)
+        for j, i in enumerate(emit):
+            if j not in tokens:
+                rt = plan[i]["rt"]
+                row = logits[j].float()
+                if rt.generator is not None:  # a seeded request draws from its own CPU generator
+                    row = row.cpu()
+                tokens[j] = sample_logits(row, rt.params, rt.generator)
+
+        events: List[TokenEvent] = []
+        j = 0
+        for i, entry in enumerate(plan):
+            rt = entry["rt"]
+            if entry["kind"] == "prefill":
+                rt.cache.position = entry["chunk_end"]
+                self.total_prefill_tokens += len(entry["tokens"])
+                self.total_cached_prefix_tokens += entry["cached"]
+                self.total_prefill_chunks += 1
+                if not entry["is_final"]:
+                    continue
+                if self.prefix_cache is not None:
+                    self.prefix_cache.register_full_blocks(rt.tokens, entry["table"])
+            else:
+                rt.cache.position += 1
+            ev = self._accept_token(rt, tokens[j], source="target")
+            j += 1
+            if ev is not None:
+                events.append(ev)
+        return events
+
+    # ----------------------------------------------------- speculative decode
+
+    def _speculation_headroom(self, rt: SequenceRuntime) -> bool:
+        span = self.lookahead_k + 1
+        if rt.cache.position + span > self.max_model_len:
+            return False
+        return len(rt.generated) + span <= rt.params.max_new_tokens
+
+    def _run_speculative(self, rts: List[SequenceRuntime]) -> List[TokenEvent]:
+        """Draft proposals, one batched verify pass, rejection, confirmed-prefix
+        write (continuous_engine.py:1212-1341)."""
+        k = self.lookahead_k
+        proposals, draft_probs, token_counts = [], [], []
+        for rt in rts:
+            if rt.draft is None:
+                rt.draft = DraftState()
+            token_counts.append(len(rt.tokens))
+            cand, probs = propose_draft_tokens(self.draft_model, rt.draft, rt.tokens, k,
+                                               rt.params.temperature, self.device)
+            proposals.append(cand)
+            draft_probs.append(probs)
+        ctx = [rt.cache.position for rt in rts]
+        tables = [rt.cache.block_table_tensor(self.device) for rt in rts]
+        queries = [[rt.tokens[-1]] + cand for rt, cand in zip(rts, proposals)]
+        logits, new_kv, _ = verify_candidates_batched(self.model, self.pool, None, tables, ctx, queries, self.device)
+        self.total_forward_passes += 1
+        self.total_speculative_rounds += 1
+        self.total_speculative_sequence_rounds += len(rts)
+        events: List[TokenEvent] = []
+        for row, rt in enumerate(rts):
+            round_ = resolve_round(rt.seq_id, proposals[row], draft_probs[row],
+                                   [x.float() for x in logits[row]], rt.params.temperature)
+            confirmed = 0
+            for position, token_id in enumerate(round_.accepted):
+                source = "draft" if round_.is_draft[position] else "target"
+                ev = self._accept_token(rt, token_id, source=source)
+                confirmed += 1
+                if ev is not None:
+                    events.append(ev)
+                if rt.done:
+                    break
+            rt.num_draft_proposed += len(round_.candidates)
+            rt.num_draft_accepted += round_.num_accepted_draft
+            self.total_draft_tokens_proposed += len(round_.candidates)
+            self.total_draft_tokens_accepted += round_.num_accepted_draft
+            if rt.done:
+                continue
+            scatter_accepted_kv(self.pool, tables[row], ctx[row], new_kv, row, confirmed)
+            rt.cache.position += confirmed
+            rt.draft.rollback_to(token_counts[row] + round_.num_accepted_draft)
+        return events
+
+    # ------------------------------------------------------------ bookkeeping
+
+    def _accept_token(self, rt: SequenceRuntime, token_id: int, source: str) -> Optional[TokenEvent]:
+        now = time.perf_counter()
+        if rt.first_token_at is None:
+            rt.first_token_at = now
+        rt.tokens.append(token_id)
+        rt.generated.append(token_id)
+        rt.sources.append(source)
+        self.total_tokens_generated += 1
+        self._recent_tokens.append(now)
+        is_eos = rt.params.stop_on_eos and token_id in self.eos_token_ids
+        hit_limit = len(rt.generated) >= rt.params.max_new_tokens
+        self.scheduler.update_sequence(rt.seq_id, token_id, bool(is_eos))
+        event = TokenEvent(seq_id=rt.seq_id, index=len(rt.generated) - 1, token_id=token_id,
+                           text=self._decode_delta(rt), source=source)
+        rt.events.append(event)
+        if is_eos:
+            self._finish(rt, "stop")
+        elif hit_limit:
+            self._finish(rt, "length")
+        return event
+
+    def _decode_delta(self, rt: SequenceRuntime) -> str:
+        full = self.tokenizer.decode(rt.generated, skip_special_tokens=True)
+        delta = full[rt.decoded_chars:]
+        rt.decoded_chars = len(full)
+        return delta
+
+    def _finish(self, rt: SequenceRuntime, reason: str) -> None:
+        if rt.done:
+            return
+        rt.finish_reason = reason
+        rt.finished_at = time.perf_counter()
+        rt.draft = None
+        rt.cache = None  # the scheduler frees the physical blocks on its next step
+
+    # ----------------------------------------------------------------- output
+
+    def result_for(self, seq_id: int) -> Dict[str, Any]:
+        rt = self.runtimes[seq_id]
+        elapsed = (rt.finished_at or time.perf_counter()) - rt.submitted_at
+        ttft = (rt.first_token_at - rt.submitted_at) if rt.first_token_at else None
+        return {
+            "seq_id": seq_id,
+            "prompt_tokens": rt.prompt_len,
+            "generated_tokens": len(rt.generated),
+            "text": self.tokenizer.decode(rt.generated, skip_special_tokens=True),
+            "token_ids": list(rt.generated),
+            "token_sources": list(rt.sources),
+            "finish_reason": rt.finish_reason,
+            "time_to_first_token_ms": round(ttft * 1000, 2) if ttft else None,
+            "total_time_s": round(elapsed, 4),
+            "tokens_per_second": round(len(rt.generated) / elapsed, 2) if elapsed > 0 else 0.0,
+            "num_prefills": rt.num_prefills,
+            "num_preemptions": rt.num_preemptions,
+        }
+
+    def drain_events(self, seq_id: int) -> List[TokenEvent]:
+        rt = self.runtimes[seq_id]
+        out = list(rt.events)
+        rt.events.clear()
+        return out
+
+    def recent_tokens_per_second(self) -> float:
+        cutoff = time.perf_counter() - self.throughput_window_s
+        while self._recent_tokens and self._recent_tokens[0] < cutoff:
+            self._recent_tokens.popleft()
+        if len(self._recent_tokens) < 2:
+            return 0.0
+        span = self._recent_tokens[-1] - self._recent_tokens[0]
+        return round(len(self._recent_tokens) / span, 2) if span > 0 else 0.0
+
+    def _device_telemetry(self) -> Dict[str, Any]:
+        """Where the pool lives and what the device holds (continuous_engine.py:1432-1483)."""
+        pool = self.pool.describe()
+        mb = 1024 * 1024
+        free_bytes, total_bytes = torch.cuda.mem_get_info()
+        return {
+            "device": pool["device"],
+            "dtype": pool["dtype"],
+            "num_blocks": pool["num_blocks"],
+            "block_size": pool["block_size"],
+            "capacity_tokens": pool["capacity_tokens"],
+            "pool_mb": pool["total_mb"],
+            "cuda_available": True,
+            "device_name": torch.cuda.get_device_name(0),
+            "allocated_mb": round(torch.cuda.memory_allocated() / mb, 2),
+            "peak_memory_mb": round(torch.cuda.max_memory_allocated() / mb, 2),
+            "reserved_mb": round(torch.cuda.memory_reserved() / mb, 2),
+            "vram_total_mb": round(total_bytes / mb, 2),
+            "vram_free_mb": round(free_bytes / mb, 2),
+        }
+
+    def telemetry(self) -> Dict[str, Any]:
+        uptime = time.perf_counter() - self.engine_started_at
+        free = self.allocator.get_num_free_blocks()
+        total = self.allocator.get_total_blocks()
+        sharing = sharing_telemetry(self.allocator, self.pool, self.prefix_cache, owners=self.block_owners())
+        return {
+            **sharing,
+            **self._device_telemetry(),
+            "uptime_s": round(uptime, 2),
+            "steps": self.total_steps,
+            "forward_passes": self.total_forward_passes,
+            "tokens_generated": self.total_tokens_generated,
+            "prefill_tokens": self.total_prefill_tokens,
+            "tokens_per_second": self.recent_tokens_per_second(),
+            "lifetime_tokens_per_second": round(self.total_tokens_generated / uptime, 2) if uptime > 0 else 0.0,
+            "tokens_per_forward_pass": (round(self.total_tokens_generated / self.total_forward_passes, 3)
+                                        if self.total_forward_passes else 0.0),
+            "active_sequences": sum(1 for rt in self.runtimes.values() if not rt.done),
+            "waiting_sequences": self.scheduler.get_num_waiting(),
+            "running_sequences": self.scheduler.get_num_running(),
+            "preemptions": self.total_preemptions,
+            "cached_prefix_tokens": self.total_cached_prefix_tokens,
+            "cow_copies": self.total_cow_copies,
+            "prefill_chunks": self.total_prefill_chunks,
+            "fused_prefill_enabled": True,
+            "fused_steps": self.total_fused_steps,
+            "fused_tokens": self.total_fused_tokens,
+            "chunked_prefill_enabled": self.max_prefill_tokens_per_step > 0,
+            "max_prefill_tokens_per_step": self.max_prefill_tokens_per_step,
+            "speculation_enabled": self.speculation_enabled,
+            "lookahead_k": self.lookahead_k,
+            "speculative_rounds": self.total_speculative_rounds,
+            "speculative_sequences_per_round": (round(self.total_speculative_sequence_rounds
+                                                      / self.total_speculative_rounds, 3)
+                                                if self.total_speculative_rounds else 0.0),
+            "draft_tokens_proposed": self.total_draft_tokens_proposed,
+            "draft_tokens_accepted": self.total_draft_tokens_accepted,
+            "draft_acceptance_rate": (round(self.total_draft_tokens_accepted / self.total_draft_tokens_proposed, 4)
+                                      if self.total_draft_tokens_proposed else 0.0),
+            "decode_view_cache_enabled": False,
+            "block_attention_enabled": True,
+            "blockwise_layer_calls": self.total_blockwise_layers,
+            "blockwise_fallbacks": self.total_blockwise_fallbacks,
+            "view_cache_mb_in_use": 0.0,
+            "view_cache_budget_mb": 0.0,
+            "view_cache_grants": 0,
+            "view_cache_denials": 0,
+            "total_blocks": total,
+            "free_blocks": free,
+            "allocated_blocks": total - free,
+            "memory_utilization": round(self.allocator.get_utilization_ratio(), 4),
+            "block_size": self.block_size,
+            "kv_pool_mb": self.pool.describe()["total_mb"],
+        }
+
+    def _live_block_tables(self) -> List[Any]:
+        return [(seq_id, rt.cache.block_table) for seq_id, rt in self.runtimes.items()
+                if not rt.done and rt.cache is not None]
+
+    def block_occupancy(self) -> List[int]:
+        occupancy = [0] * self.allocator.get_total_blocks()
+        for seq_id, table in self._live_block_tables():
+            for block_id in table:
+                if 0 <= block_id < len(occupancy):
+                    occupancy[block_id] = seq_id
+        return occupancy
+
+    def block_owners(self) -> Dict[str, List[int]]:
+        return block_owners(self._live_block_tables(), self.allocator.get_total_blocks())
+
+    # ------------------------------------------------------- blocking helpers
+
+    def run_until_idle(self, max_steps: int = 100_000) -> List[StepReport]:
+        reports = []
+        steps = 0
+        while self.has_work() and steps < max_steps:
+            reports.append(self.step())
+            steps += 1
+        return reports
+
+    def generate(self, prompts, params: Optional[SamplingParams] = None) -> List[Dict[str, Any]]:
+        prompt_list = [prompts] if isinstance(prompts, str) else list(prompts)
+        ids = [self.submit(p, params) for p in prompt_list]
+        self.run_until_idle()
+        return [self.result_for(i) for i in ids]

@@ -1,0 +1,54 @@
+"""Pool-side half of prefix sharing: the copy-on-write block copy and the
+sharing figures (same functions as the reference, memforge_ml/runtime/
+prefix_sharing.py:27-140). Which blocks are shared is decided by the C++
+``PrefixCache`` and ``BlockAllocator``; this file only moves K/V and reports.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Dict, Iterable, List, Optional, Tuple
+
+from memforge_amd.runtime.kv_pool import PagedKVPool
+
+
+def copy_block(pool: PagedKVPool, src: int, dst: int) -> None:
+    """Copy block ``src`` to ``dst`` in every layer, K and V (one device copy
+    each over the (layers, blocks, slots, heads, dim) pool); a no-op on itself."""
+    if src == dst:
+        return
+    pool.key_pool[:, dst].copy_(pool.key_pool[:, src])
+    pool.value_pool[:, dst].copy_(pool.value_pool[:, src])
+
+
+def block_owners(runtimes: Iterable[Tuple[int, List[int]]], total_blocks: int) -> Dict[str, List[int]]:
+    """Every in-range physical block mapped to all sequences whose table holds
+    it, owners sorted; keys are strings (JSON)."""
+    owners: Dict[str, List[int]] = {}
+    for seq_id, table in runtimes:
+        for block_id in table:
+            if 0 <= block_id < total_blocks:
+                owners.setdefault(str(block_id), []).append(seq_id)
+    for ids in owners.values():
+        ids.sort()
+    return owners
+
+
+def sharing_telemetry(allocator: Any, pool: PagedKVPool, prefix_cache: Optional[Any],
+                      owners: Optional[Dict[str, List[int]]] = None) -> Dict[str, Any]:
+    """Sharing figures with a stable shape (zeros when sharing is off).
+    ``memory_saved_mb`` = blocks saved (sum of references minus distinct
+    allocated blocks) x the pool's bytes per block."""
+    saved = allocator.get_num_blocks_saved()
+    payload: Dict[str, Any] = {
+        "shared_blocks": allocator.get_num_shared_blocks(),
+        "blocks_saved": saved,
+        "memory_saved_mb": round(saved * pool.bytes_per_block / (1024 * 1024), 3),
+        "cached_prefix_blocks": prefix_cache.num_cached_blocks() if prefix_cache else 0,
+        "prefix_hit_rate": round(prefix_cache.hit_rate(), 4) if prefix_cache else 0.0,
+        "prefix_cache_hits": prefix_cache.num_hits() if prefix_cache else 0,
+        "prefix_cache_misses": prefix_cache.num_misses() if prefix_cache else 0,
+        "prefix_sharing_enabled": prefix_cache is not None,
+    }
+    if owners is not None:
+        payload["block_owners"] = owners
+    return payload

@@ -89,3 +89,38 @@ def resolve_round(candidates: Sequence[int], draft_probs: Sequence[np.ndarray],
         target_logits = [np.asarray(t)[..., :width] for t in target_logits]
     target_probs = [probs_from_logits(t, temperature) for t in target_logits]
     return verify_tokens(candidates, draft_probs, target_probs, u, noise)
+
+
+def verify_tokens_global_rng(draft_tokens, draft_probs, target_probs):
+    """``RejectionSampler.verify_tokens`` (rejection_sampler.py:28-83) drawing
+    from torch's global generators exactly as the reference does:
+    ``torch.rand(1)`` per examined candidate and ``torch.multinomial`` on the
+    probabilities' device for the draw that ends the round. Takes and returns
+    what the reference does; used to check that a drop-in consumes the same
+    random numbers in the same order."""
+    import torch
+
+    def draw(probs):
+        probs = torch.clamp(probs, min=0.0)
+        total = probs.sum()
+        probs = torch.ones_like(probs) / probs.shape[0] if total == 0 else probs / total
+        return int(torch.multinomial(probs, num_samples=1).item())
+
+    accepted, is_draft = [], []
+    for i, tok in enumerate(draft_tokens):
+        q = float(draft_probs[i][tok].item())
+        p = float(target_probs[i][tok].item())
+        acceptance = min(1.0, p / (q + 1e-9))
+        if float(torch.rand(1).item()) <= acceptance:
+            accepted.append(int(tok))
+            is_draft.append(True)
+            continue
+        diff = torch.clamp(target_probs[i] - draft_probs[i], min=0.0)
+        total = diff.sum()
+        accepted.append(draw(diff / total) if total > 0 else draw(target_probs[i]))
+        is_draft.append(False)
+        return accepted, is_draft, i
+    if len(target_probs) > len(draft_tokens):
+        accepted.append(draw(target_probs[len(draft_tokens)]))
+        is_draft.append(False)
+    return accepted, is_draft, len(draft_tokens)

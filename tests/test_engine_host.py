@@ -1,0 +1,367 @@
+"""CPU tests of the native host engine (``memforge_amd.memforge_c``): block
+allocator, prefix cache and continuous-batching scheduler.
+
+Two kinds of check:
+* the behaviours the reference's own tests assert (tests/cpp/
+  test_block_allocator.cpp, test_prefix_cache.cpp, test_scheduler.cpp and
+  tests/python/test_scheduler_bridge.py), run against this engine and -- where
+  ``oracle/_ref`` holds the reference engine built from its own sources --
+  against the reference too, so the assertions are known to hold there;
+* differential runs: seeded random workloads (arrivals, chunked prefill,
+  prefix sharing, copy-on-write, lookahead, aborts, memory pressure) drive
+  both engines through identical call sequences, and every step result --
+  block tables, flags, chunk bounds, finished/preempted/aborted ids, pool
+  counters -- must be identical.
+"""
+
+import random
+
+import pytest
+
+from memforge_amd import memforge_c as mine
+from oracle import build_ref
+
+REF = build_ref.load()
+IMPLS = [pytest.param(mine, id="memforge_amd")]
+if REF is not None:
+    IMPLS.append(pytest.param(REF, id="reference"))
+
+
+@pytest.fixture(params=IMPLS)
+def mc(request):
+    return request.param
+
+
+def ramp(n, offset=0):
+    return [i + offset for i in range(n)]
+
+
+def admit(cache, allocator, tokens, bs=16):
+    shared = cache.acquire_shared_prefix(tokens)
+    needed = (len(tokens) + bs - 1) // bs - len(shared)
+    table = list(shared) + (list(allocator.allocate_blocks(needed)) if needed else [])
+    cache.register_full_blocks(tokens, table)
+    return table
+
+
+# ------------------------------------------------------------------ allocator
+
+
+def test_basic_allocation_is_fifo_from_block_zero(mc):
+    a = mc.BlockAllocator(10, 16)
+    assert (a.get_total_blocks(), a.get_num_free_blocks(), a.get_num_allocated_blocks()) == (10, 10, 0)
+    assert a.allocate() == 0
+    blocks = a.allocate_blocks(3)
+    assert len(blocks) == 3 and a.get_num_free_blocks() == 6
+    a.free(0)
+    a.free_blocks(blocks)
+    assert a.get_num_free_blocks() == 10
+
+
+def test_sequence_capacity_and_lookahead(mc):
+    a = mc.BlockAllocator(10, 16)
+    seq = mc.Sequence(1, [1, 2, 3, 4, 5], 32, 16)
+    assert seq.get_num_required_blocks() == 1 and a.ensure_capacity(seq)
+    for i in range(12):
+        seq.append_token(100 + i)
+    assert seq.get_total_len() == 17 and seq.get_num_required_blocks() == 2
+    assert a.ensure_capacity(seq) and len(seq.get_block_table()) == 2
+    assert len(a.free_sequence(seq)) == 2 and a.get_num_free_blocks() == 10
+
+    a = mc.BlockAllocator(10, 4)
+    seq = mc.Sequence(1, [1, 2, 3], 32, 4)
+    assert seq.get_num_required_blocks_with_lookahead(5) == 2
+    assert seq.get_num_required_blocks_with_lookahead(1) == 1
+    assert a.ensure_capacity_with_lookahead(seq, 5) and len(seq.get_block_table()) == 2
+    assert a.ensure_capacity_with_lookahead(seq, 5) and len(seq.get_block_table()) == 2
+
+
+def test_lookahead_reservation_is_all_or_nothing(mc):
+    a = mc.BlockAllocator(3, 4)
+    seq = mc.Sequence(1, [1, 2, 3, 4], 64, 4)
+    assert a.ensure_capacity(seq) and a.get_num_free_blocks() == 2
+    assert not a.ensure_capacity_with_lookahead(seq, 40)
+    assert len(seq.get_block_table()) == 1 and a.get_num_free_blocks() == 2
+    assert a.ensure_capacity_with_lookahead(seq, 4) and len(seq.get_block_table()) == 2
+
+
+def test_out_of_range_ids_are_refused(mc):
+    a = mc.BlockAllocator(4, 4)
+    for bad in (4, 999999, -1):
+        assert a.get_ref_count(bad) == 0
+        assert not a.add_ref(bad)
+        a.free(bad)
+    assert a.get_num_free_blocks() == 4
+    good = a.allocate()
+    assert a.add_ref(good) and a.get_ref_count(good) == 2
+    a.free(good)
+    a.free(good)
+    assert a.get_num_free_blocks() == 4 and not a.add_ref(good)
+    seq = mc.Sequence(1, [1, 2, 3], 8, 4)
+    assert a.ensure_capacity(seq) and a.prepare_write(seq, 99) is None
+
+
+def test_allocator_refuses_to_oversubscribe(mc):
+    a = mc.BlockAllocator(4, 16)
+    assert a.can_allocate(4) and not a.can_allocate(5)
+    with pytest.raises(Exception):
+        a.allocate_blocks(5)
+    assert a.get_num_free_blocks() == 4
+    first, second = a.allocate_blocks(2), a.allocate_blocks(2)
+    assert not set(first) & set(second)
+
+
+def test_copy_on_write(mc):
+    a = mc.BlockAllocator(16, 16)
+    seq = mc.Sequence(1, ramp(40), 32, 16)
+    assert a.ensure_capacity(seq)
+    assert a.prepare_write(seq, 2) is None
+    shared = seq.get_block_table()[0]
+    assert a.add_ref(shared)
+    old, new = a.prepare_write(seq, 0)
+    assert old == shared and new != shared and seq.get_block_table()[0] == new
+    assert a.get_ref_count(new) == 1 and a.get_ref_count(shared) == 1
+
+
+# --------------------------------------------------------------- prefix cache
+
+
+def test_hash_is_chained_and_never_zero(mc):
+    a, b = ramp(16), ramp(16, 100)
+    assert mc.hash_block(0, a) == mc.hash_block(0, a) != mc.hash_block(0, b)
+    assert mc.hash_block(0, a) != mc.hash_block(12345, a)
+    assert mc.hash_block(0, a) != 0 and mc.hash_block(0, b) != 0
+
+
+def test_hash_values_equal_the_reference():
+    if REF is None:
+        pytest.skip("reference engine not built")
+    rng = random.Random(5)
+    parent = 0
+    for n in (0, 1, 7, 16, 33):
+        toks = [rng.randrange(0, 1 << 31) for _ in range(n)]
+        assert mine.hash_block(parent, toks) == REF.hash_block(parent, toks)
+        parent = mine.hash_block(parent, toks)
+
+
+def test_identical_prompts_share_full_blocks(mc):
+    a = mc.BlockAllocator(64, 16)
+    c = mc.PrefixCache(a, 16)
+    first = admit(c, a, ramp(40))
+    assert len(first) == 3 and a.get_num_allocated_blocks() == 3 and c.num_cached_blocks() == 2
+    second = admit(c, a, ramp(40))
+    assert second[:2] == first[:2] and second[2] != first[2]
+    assert a.get_num_allocated_blocks() == 4 and a.get_num_shared_blocks() == 2 and a.get_num_blocks_saved() == 2
+
+
+def test_sharing_stops_at_first_divergence_and_boundaries(mc):
+    a = mc.BlockAllocator(64, 16)
+    c = mc.PrefixCache(a, 16)
+    base = ramp(4 * 16 + 5)
+    admit(c, a, base)
+    variant = list(base)
+    variant[2 * 16 + 3] = 9999
+    shared = c.acquire_shared_prefix(variant)
+    assert len(shared) == 2
+    c.release_acquired(shared)
+    a2 = mc.BlockAllocator(64, 16)
+    c2 = mc.PrefixCache(a2, 16)
+    admit(c2, a2, ramp(15))
+    assert c2.num_cached_blocks() == 0 and list(c2.acquire_shared_prefix(ramp(15))) == []
+    admit(c2, a2, ramp(48, 500))
+    assert c2.num_cached_blocks() == 2
+    shared = c2.acquire_shared_prefix(ramp(48, 500))
+    assert len(shared) == 2
+    c2.release_acquired(shared)
+
+
+def test_refcount_lifecycle_eviction_and_stale_entries(mc):
+    a = mc.BlockAllocator(64, 16)
+    c = mc.PrefixCache(a, 16)
+    x = admit(c, a, ramp(40))
+    y = admit(c, a, ramp(40))
+    freed = a.release(x)
+    c.evict(freed)
+    assert len(freed) == 1 and a.get_ref_count(x[0]) == 1 and c.num_cached_blocks() == 2
+    freed = a.release(y)
+    c.evict(freed)
+    assert len(freed) == 3 and a.get_num_free_blocks() == 64 and c.num_cached_blocks() == 0
+
+    a = mc.BlockAllocator(8, 16)
+    c = mc.PrefixCache(a, 16)
+    table = admit(c, a, ramp(40))
+    freed = a.release(table)
+    a.allocate_blocks(3)
+    c.evict(freed)
+    assert c.num_cached_blocks() == 0 and list(c.acquire_shared_prefix(ramp(40))) == []
+
+
+def test_release_acquired_and_hit_accounting(mc):
+    a = mc.BlockAllocator(64, 16)
+    c = mc.PrefixCache(a, 16)
+    table = admit(c, a, ramp(40))
+    base = a.get_num_allocated_blocks()
+    assert c.num_hits() == 0
+    for _ in range(5):
+        shared = c.acquire_shared_prefix(ramp(40))
+        assert len(shared) == 2
+        c.release_acquired(shared)
+        assert a.get_num_allocated_blocks() == base and a.get_ref_count(table[0]) == 1
+    assert c.num_hits() == 10 and 0.0 < c.hit_rate() <= 1.0
+
+
+# ------------------------------------------------------------------ scheduler
+
+
+def test_continuous_scheduling(mc):
+    a = mc.BlockAllocator(20, 16)
+    s = mc.Scheduler(a, 4)
+    s.add_sequence(101, [1, 2, 3], 5)
+    s.add_sequence(102, [4, 5, 6, 7], 5)
+    assert (s.get_num_waiting(), s.get_num_running()) == (2, 0)
+    r = s.step()
+    assert len(r.running_sequences) == 2 and r.running_sequences[0].is_prefill
+    for i in range(5):
+        s.update_sequence(101, 1000 + i, i == 4)
+    r = s.step()
+    assert list(r.finished_sequence_ids) == [101]
+
+
+def test_block_table_grows_one_block_at_a_time(mc):
+    a = mc.BlockAllocator(64, 4)
+    s = mc.Scheduler(a, 4)
+    s.add_sequence(1, [1, 2, 3, 4], 32)
+    assert len(s.step().running_sequences[0].block_table) == 1
+    sizes = []
+    for _ in range(9):
+        s.update_sequence(1, 7, False)
+        sizes.append(len(s.step().running_sequences[0].block_table))
+    assert sizes == [2, 2, 2, 2, 3, 3, 3, 3, 4]
+
+
+def test_preemption_requeues_for_recompute(mc):
+    a = mc.BlockAllocator(6, 16)
+    s = mc.Scheduler(a, 8)
+    for seq_id in (1, 2, 3):
+        s.add_sequence(seq_id, list(range(32)), 200)
+    r = s.step()
+    assert len(r.running_sequences) == 3
+    victim = None
+    for _ in range(40):
+        for info in r.running_sequences:
+            s.update_sequence(info.seq_id, 7, False)
+        r = s.step()
+        if r.preempted_sequence_ids:
+            victim = r.preempted_sequence_ids[0]
+            break
+    assert victim is not None and r.num_waiting >= 1
+    seq = s.get_sequence(victim)
+    assert seq.get_output_len() > 0 and not seq.has_completed_prefill() and len(seq.get_block_table()) == 0
+    assert a.get_num_free_blocks() + a.get_num_allocated_blocks() == a.get_total_blocks()
+
+
+def test_impossible_request_is_aborted_and_caps_hold(mc):
+    a = mc.BlockAllocator(4, 16)
+    s = mc.Scheduler(a, 8)
+    s.add_sequence(99, list(range(500)), 10)
+    s.add_sequence(100, list(range(16)), 10)
+    r = s.step()
+    assert 99 in r.aborted_sequence_ids and [i.seq_id for i in r.running_sequences] == [100]
+    a = mc.BlockAllocator(64, 16)
+    s = mc.Scheduler(a, 2)
+    for seq_id in range(1, 6):
+        s.add_sequence(seq_id, [1, 2, 3], 16)
+    r = s.step()
+    assert len(r.running_sequences) == 2 and r.num_waiting == 3
+    assert s.abort_sequence(1) and not s.abort_sequence(12345)
+
+
+def test_step_reports_pool_utilisation_and_chunk_bounds(mc):
+    a = mc.BlockAllocator(10, 16)
+    s = mc.Scheduler(a, 4)
+    s.add_sequence(1, list(range(32)), 16)
+    r = s.step()
+    assert r.total_blocks == 10 and r.num_free_blocks == 8
+    assert r.memory_utilization_ratio == pytest.approx(0.2)
+    a = mc.BlockAllocator(64, 16)
+    s = mc.Scheduler(a, 4, None, 20)
+    s.add_sequence(1, list(range(50)), 4)
+    ends = []
+    for _ in range(3):
+        info = s.step().running_sequences[0]
+        ends.append((info.num_cached_tokens, info.prefill_chunk_end))
+    assert ends == [(0, 20), (20, 40), (40, 50)]
+
+
+# ---------------------------------------------------------------- differential
+
+
+def _snapshot(r):
+    return (
+        [(i.seq_id, list(i.block_table), i.prompt_length, i.output_length, i.total_length, int(i.status),
+          bool(i.is_prefill), i.num_cached_tokens, i.prefill_chunk_end) for i in r.running_sequences],
+        list(r.finished_sequence_ids), list(r.preempted_sequence_ids), list(r.aborted_sequence_ids),
+        r.num_waiting, r.num_free_blocks, r.total_blocks, round(r.memory_utilization_ratio, 9),
+    )
+
+
+def _drive(mod, seed, num_blocks, bs, max_seqs, sharing, chunk, lookahead, steps=160):
+    """A scripted engine loop; every choice comes from ``seed`` and the
+    engine's own answers, so two engines that agree take identical paths."""
+    rng = random.Random(seed)
+    a = mod.BlockAllocator(num_blocks, bs)
+    pc = mod.PrefixCache(a, bs) if sharing else None
+    s = mod.Scheduler(a, max_seqs, pc, chunk, lookahead)
+    prefixes = [[rng.randrange(2, 500) for _ in range(rng.randrange(1, 3 * bs))] for _ in range(3)]
+    trace, next_id, live = [], 1, set()
+    for _ in range(steps):
+        if rng.random() < 0.5:
+            prompt = list(rng.choice(prefixes)) + [rng.randrange(2, 500) for _ in range(rng.randrange(1, 2 * bs))]
+            if rng.random() < 0.03:  # larger than the whole pool: aborted as unschedulable
+                prompt = prompt * (num_blocks * bs // len(prompt) + 2)
+            s.add_sequence(next_id, prompt, rng.randrange(1, 64))
+            live.add(next_id)
+            next_id += 1
+        if live and rng.random() < 0.05:
+            victim = rng.choice(sorted(live))
+            trace.append(("abort", victim, s.abort_sequence(victim)))
+        r = s.step()
+        trace.append(_snapshot(r))
+        for sid in list(r.finished_sequence_ids) + list(r.aborted_sequence_ids):
+            live.discard(sid)
+        for info in r.running_sequences:
+            if info.is_prefill:
+                end = info.prefill_chunk_end or info.total_length
+                if end < info.total_length:
+                    continue
+                if pc is not None:
+                    seq = s.get_sequence(info.seq_id)
+                    pc.register_full_blocks(list(seq.get_all_tokens()), list(info.block_table))
+            else:
+                seq = s.get_sequence(info.seq_id)
+                if pc is not None and seq is not None:
+                    cow = a.prepare_write(seq, (info.total_length - 1) // bs)
+                    trace.append(("cow", info.seq_id, None if cow is None else tuple(cow)))
+            n = rng.randrange(1, lookahead + 1) if lookahead and not info.is_prefill else 1
+            for _ in range(n):
+                s.update_sequence(info.seq_id, rng.randrange(2, 500), rng.random() < 0.02)
+        trace.append((a.get_num_free_blocks(), a.get_num_shared_blocks(), a.get_num_blocks_saved(),
+                      pc.num_cached_blocks() if pc else -1, pc.num_hits() if pc else -1))
+    return trace
+
+
+@pytest.mark.skipif(REF is None, reason="reference engine not built (oracle/build_ref.py)")
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("cfg", [
+    dict(num_blocks=40, bs=4, max_seqs=6, sharing=False, chunk=0, lookahead=0),
+    dict(num_blocks=64, bs=16, max_seqs=8, sharing=True, chunk=0, lookahead=0),
+    dict(num_blocks=48, bs=8, max_seqs=8, sharing=True, chunk=24, lookahead=0),
+    dict(num_blocks=30, bs=4, max_seqs=5, sharing=False, chunk=10, lookahead=3),
+    dict(num_blocks=24, bs=16, max_seqs=16, sharing=True, chunk=32, lookahead=4),
+], ids=["plain", "sharing", "chunked+sharing", "chunked+lookahead", "pressure+all"])
+def test_engine_matches_the_reference_step_for_step(seed, cfg):
+    got = _drive(mine, 1000 + seed, **cfg)
+    want = _drive(REF, 1000 + seed, **cfg)
+    for i, (g, w) in enumerate(zip(got, want)):
+        assert g == w, f"first difference at trace entry {i}"
+    assert len(got) == len(want)

@@ -1,0 +1,266 @@
+"""GPU tests of ContinuousBatchingEngine: every step is one packed varlen pass
+through the HIP kernels, and its greedy output must be exactly what plain
+transformers decoding produces for each request on its own (the reference's
+tests/python/test_continuous_engine.py, test_chunked_prefill.py,
+test_prefix_sharing.py, test_fused_prefill.py and test_speculative_batching.py
+cover the same behaviour)."""
+
+import pytest
+import torch
+
+from tests.tiny_models import StubTokenizer, hf_greedy, tiny_llama
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def model(device):
+    return tiny_llama(num_layers=2, seed=0)
+
+
+@pytest.fixture(scope="module")
+def draft(device):
+    return tiny_llama(num_layers=1, seed=1)
+
+
+@pytest.fixture(scope="module")
+def tok():
+    return StubTokenizer()
+
+
+def greedy(n=8, **kw):
+    from memforge_amd.runtime.sampling import SamplingParams
+
+    return SamplingParams(max_new_tokens=n, temperature=0.0, top_p=1.0, **kw)
+
+
+def make_engine(model, tok, **kw):
+    from memforge_amd.runtime.continuous_engine import ContinuousBatchingEngine
+
+    opts = dict(block_size=4, num_blocks=64, max_num_seqs=4, max_model_len=128)
+    opts.update(kw)
+    return ContinuousBatchingEngine(model, tok, **opts)
+
+
+PROMPTS = ["alpha prompt", "a much longer beta prompt here", "gamma", "the fourth one, mid length"]
+
+
+def expected(model, tok, prompts, n, stop_on_eos=True):
+    return [hf_greedy(model, tok(p)["input_ids"], n, stop_on_eos=stop_on_eos) for p in prompts]
+
+
+def test_batched_greedy_equals_plain_transformers(model, tok):
+    engine = make_engine(model, tok)
+    results = engine.generate(PROMPTS, greedy(10))
+    for r, exp in zip(results, expected(model, tok, PROMPTS, 10)):
+        assert r["token_ids"] == exp
+    assert engine.total_forward_passes < sum(r["generated_tokens"] for r in results)
+    assert engine.telemetry()["tokens_per_forward_pass"] > 1.0
+
+
+@pytest.mark.parametrize("block_size", [4, 16])
+def test_block_sizes_agree(model, tok, block_size):
+    engine = make_engine(model, tok, block_size=block_size, num_blocks=256 // block_size)
+    results = engine.generate(PROMPTS[:3], greedy(6))
+    for r, exp in zip(results, expected(model, tok, PROMPTS[:3], 6)):
+        assert r["token_ids"] == exp
+
+
+def test_generates_the_requested_count_and_reclaims_every_block(model, tok):
+    engine = make_engine(model, tok)
+    total = engine.allocator.get_total_blocks()
+    r = engine.generate("hello world", greedy(8, stop_on_eos=False))[0]
+    assert r["generated_tokens"] == 8 and r["finish_reason"] == "length"
+    assert r["time_to_first_token_ms"] is not None
+    engine.step()
+    assert engine.allocator.get_num_free_blocks() == total
+
+
+def test_requests_can_join_while_others_are_running(model, tok):
+    from memforge_amd.runtime.sampling import SamplingParams
+
+    engine = make_engine(model, tok)
+    first = engine.submit("early request", SamplingParams(max_new_tokens=12, temperature=0.0, stop_on_eos=False))
+    for _ in range(3):
+        engine.step()
+    late = engine.submit("late request", SamplingParams(max_new_tokens=4, temperature=0.0, stop_on_eos=False))
+    engine.step()
+    engine.step()
+    assert len(engine.runtimes[late].generated) >= 1 and not engine.runtimes[first].done
+    engine.run_until_idle()
+    assert engine.runtimes[first].generated == hf_greedy(model, tok("early request")["input_ids"], 12,
+                                                         stop_on_eos=False)
+    assert engine.runtimes[late].generated == hf_greedy(model, tok("late request")["input_ids"], 4,
+                                                        stop_on_eos=False)
+    assert engine.total_fused_steps > 0, "a prefill joined a step that also decoded"
+
+
+def test_preempted_output_matches_an_unpressured_run(model, tok):
+    prompts = ["prompt number one", "prompt number two", "prompt number three"]
+    params = greedy(10, stop_on_eos=False)
+    pressured = make_engine(model, tok, num_blocks=12, max_num_seqs=3)
+    roomy = make_engine(model, tok, num_blocks=128, max_num_seqs=3)
+    a = pressured.generate(prompts, params)
+    b = roomy.generate(prompts, params)
+    pressured.step()
+    assert pressured.total_preemptions > 0 and roomy.total_preemptions == 0
+    for x, y in zip(a, b):
+        assert x["token_ids"] == y["token_ids"] and x["generated_tokens"] == 10
+    assert pressured.allocator.get_num_free_blocks() == pressured.allocator.get_total_blocks()
+
+
+def test_submit_validation(model, tok):
+    engine = make_engine(model, tok, max_model_len=32)
+    with pytest.raises(ValueError):
+        engine.submit("x" * 40, greedy(4))
+    with pytest.raises(ValueError):
+        engine.submit([], greedy(4))
+    seq = engine.submit("x" * 20, greedy(100))
+    assert engine.runtimes[seq].params.max_new_tokens == 12
+
+
+def test_abort_stops_a_sequence_and_frees_its_memory(model, tok):
+    engine = make_engine(model, tok)
+    seq = engine.submit("abort me please", greedy(50, stop_on_eos=False))
+    engine.step()
+    engine.step()
+    assert engine.abort(seq)
+    engine.run_until_idle()
+    engine.step()
+    assert engine.runtimes[seq].finish_reason == "aborted"
+    assert engine.allocator.get_num_free_blocks() == engine.allocator.get_total_blocks()
+    assert not engine.abort(seq)
+
+
+def test_eos_stops_generation_early(model, tok):
+    engine = make_engine(model, tok)
+    engine.eos_token_ids = set(range(256))  # every token is EOS
+    r = engine.generate("stop at once", greedy(8))[0]
+    assert r["generated_tokens"] == 1 and r["finish_reason"] == "stop"
+
+
+def test_seeded_sampling_is_reproducible(model, tok):
+    from memforge_amd.runtime.sampling import SamplingParams
+
+    p = SamplingParams(max_new_tokens=10, temperature=0.9, top_p=0.95, seed=123, stop_on_eos=False)
+    a = make_engine(model, tok).generate("sample this", p)[0]["token_ids"]
+    b = make_engine(model, tok).generate("sample this", p)[0]["token_ids"]
+    assert a == b and len(a) == 10
+
+
+def test_chunked_prefill_does_not_change_the_output(model, tok):
+    long_prompt = "a long prompt that needs several chunks to prefill " * 2
+    prompts = [long_prompt, "short one"]
+    plain = make_engine(model, tok, num_blocks=128, max_model_len=256)
+    chunked = make_engine(model, tok, num_blocks=128, max_model_len=256, max_prefill_tokens_per_step=16)
+    a = plain.generate(prompts, greedy(8))
+    b = chunked.generate(prompts, greedy(8))
+    for x, y, exp in zip(a, b, expected(model, tok, prompts, 8)):
+        assert x["token_ids"] == y["token_ids"] == exp
+    assert chunked.total_prefill_chunks > plain.total_prefill_chunks
+    t = chunked.telemetry()
+    assert t["chunked_prefill_enabled"] and t["max_prefill_tokens_per_step"] == 16
+
+
+def test_prefix_sharing_is_byte_identical_and_saves_blocks(model, tok):
+    shared = "a shared system prompt that spans several blocks: "
+    prompts = [shared + "first question", shared + "second question", shared + "third"]
+    on = make_engine(model, tok, num_blocks=128, max_model_len=256, enable_prefix_sharing=True)
+    off = make_engine(model, tok, num_blocks=128, max_model_len=256, enable_prefix_sharing=False)
+    first = on.generate(prompts[:1], greedy(6))  # registers the prefix
+    rest = on.generate(prompts[1:], greedy(6))
+    ref = off.generate(prompts, greedy(6))
+    assert [r["token_ids"] for r in first + rest] == [r["token_ids"] for r in ref]
+    assert on.total_cached_prefix_tokens > 0 and off.total_cached_prefix_tokens == 0
+    t = on.telemetry()
+    assert t["prefix_sharing_enabled"] and t["prefix_cache_hits"] > 0
+    assert off.telemetry()["memory_saved_mb"] == 0.0
+    on.step()
+    assert on.allocator.get_num_allocated_blocks() == 0
+    assert on.allocator.get_num_free_blocks() == on.allocator.get_total_blocks()
+    assert on.prefix_cache.num_cached_blocks() == 0 and on.allocator.get_num_shared_blocks() == 0
+
+
+def test_concurrent_identical_prefixes_share_blocks(model, tok):
+    prefix = [2 + ((i * 7) % 200) for i in range(40)]
+    engine = make_engine(model, tok, block_size=16, num_blocks=64, max_model_len=256)
+    first = engine.submit(prefix + [50], greedy(30, stop_on_eos=False))
+    engine.step()  # prefill registers the two full blocks
+    second = engine.submit(prefix + [51], greedy(4, stop_on_eos=False))
+    engine.step()
+    engine.step()
+    assert engine.allocator.get_num_shared_blocks() >= 2
+    owners = engine.telemetry()["block_owners"]
+    assert any(sorted(v) == sorted([first, second]) for v in owners.values())
+    engine.run_until_idle()
+    want = hf_greedy(model, prefix + [51], 4, stop_on_eos=False)
+    assert engine.runtimes[second].generated == want
+
+
+def test_block_occupancy_and_owners(model, tok):
+    engine = make_engine(model, tok)
+    a = engine.submit("owner one", greedy(20, stop_on_eos=False))
+    b = engine.submit("owner two", greedy(20, stop_on_eos=False))
+    engine.step()
+    engine.step()
+    occ = engine.block_occupancy()
+    assert {a, b} <= set(occ)
+    owners = engine.block_owners()
+    for block_id, seqs in owners.items():
+        assert occ[int(block_id)] in seqs
+
+
+def test_telemetry_and_describe(model, tok):
+    engine = make_engine(model, tok)
+    engine.generate(["one", "two"], greedy(4))
+    t = engine.telemetry()
+    for key in ("tokens_generated", "forward_passes", "free_blocks", "total_blocks", "block_size", "kv_pool_mb",
+                "fused_steps", "speculation_enabled", "memory_utilization"):
+        assert key in t
+    assert t["total_blocks"] == 64 and t["block_size"] == 4
+    d = engine.describe()
+    assert d["kv_pool"]["num_blocks"] == 64 and d["block_attention"]
+    with pytest.raises(NotImplementedError):
+        make_engine(model, tok, decode_view_cache=True)
+
+
+def test_model_routing_is_restored_after_each_step(model, tok):
+    from memforge_amd.kernels import attention_backend
+
+    before = model.config._attn_implementation
+    make_engine(model, tok).generate("routing", greedy(3))
+    assert model.config._attn_implementation == before
+    assert not attention_backend.is_enabled_on(model)
+
+
+def test_bf16_engine_runs_and_first_tokens_agree(tok, device):
+    m = tiny_llama(num_layers=2, seed=0, dtype=torch.bfloat16, hidden=256, heads=4, kv_heads=2)
+    engine = make_engine(m, tok, block_size=16, num_blocks=32)
+    results = engine.generate(PROMPTS, greedy(4))
+    exp = expected(m, tok, PROMPTS, 4)
+    same_first = sum(r["token_ids"][0] == e[0] for r, e in zip(results, exp))
+    assert same_first >= len(PROMPTS) - 1, "bf16 first tokens should agree with transformers"
+
+
+# ------------------------------------------------------------------ speculation
+
+
+def test_self_draft_accepts_everything_and_stays_greedy(model, tok):
+    engine = make_engine(model, tok, draft_model=model, lookahead_k=3, num_blocks=128)
+    results = engine.generate(PROMPTS[:3], greedy(12, stop_on_eos=False))
+    for r, exp in zip(results, expected(model, tok, PROMPTS[:3], 12, stop_on_eos=False)):
+        assert r["token_ids"] == exp
+    t = engine.telemetry()
+    assert t["speculation_enabled"] and t["draft_acceptance_rate"] == 1.0
+    assert t["speculative_rounds"] > 0
+
+
+def test_speculative_output_is_identical_to_plain_greedy(model, draft, tok):
+    plain = make_engine(model, tok, num_blocks=128).generate(PROMPTS, greedy(12, stop_on_eos=False))
+    spec = make_engine(model, tok, num_blocks=128, draft_model=draft, lookahead_k=2)
+    results = spec.generate(PROMPTS, greedy(12, stop_on_eos=False))
+    for a, b in zip(results, plain):
+        assert a["token_ids"] == b["token_ids"]
+    spec.step()
+    assert spec.allocator.get_num_free_blocks() == spec.allocator.get_total_blocks()
+    assert spec.total_speculative_sequence_rounds >= spec.total_speculative_rounds

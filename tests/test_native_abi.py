@@ -1,0 +1,134 @@
+"""CPU tests of the C ABI library: it loads, exports every entry point the
+header declares, and its host-only routines (status strings, the attention
+work planner, workspace sizing) behave as documented. Nothing here launches a
+kernel."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from memforge_amd import _native as nat
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "memforge_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mf_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(nat.LIB_PATH))
+    names = declared_functions()
+    assert len(names) >= 9, names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    # every declared function also has a ctypes signature in the binding
+    assert set(names) <= set(nat._SIGNATURES), set(names) - set(nat._SIGNATURES)
+
+
+def test_version_and_status_strings():
+    L = nat.lib()
+    assert L.mf_version().decode().startswith("memforge_hip")
+    for code in (0, -1, -2, -3, -4):
+        s = L.mf_status_string(code).decode()
+        assert s and s != L.mf_status_string(12345).decode()
+
+
+def _plan(cu, kv, hq=8, hkv=2, d=128, dtype=torch.bfloat16, pt=0):
+    return nat.plan_attention(cu, kv, hq, hkv, d, dtype, "cpu", partition_tiles=pt)
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float32, 64), (torch.float16, 256),
+                                     (torch.float32, 128)])
+@pytest.mark.parametrize("pt", [0, 1, 3, 64])
+def test_plan_covers_every_tile_exactly_once_and_merges_line_up(dtype, d, pt):
+    rng = np.random.default_rng(pt + d)
+    q_lens = [1, 1, 7, 40, 0, 3, 130, 1]
+    kv = [int(x) for x in rng.integers(1, 3000, len(q_lens))]
+    kv[4] = 0
+    kv[2] = 7
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).tolist()
+    hq, hkv = 8, 2
+    G = hq // hkv
+    p = _plan(cu, kv, hq, hkv, d, dtype, pt)
+    items = p.items_host
+    merges = p.merges_host
+    assert items.shape[0] == p.n_narrow + p.n_wide
+    cover = {}
+    slots = {}
+    for it in items:
+        s, h, c0, nct, kt0, kt1, slot, merge = (int(x) for x in it)
+        assert kt1 > kt0 and kt1 - kt0 <= 64
+        for c in range(c0, c0 + nct):
+            for kt in range(kt0, kt1):
+                key = (s, h, c, kt)
+                assert key not in cover, f"tile {key} planned twice"
+                cover[key] = True
+            if slot >= 0:
+                sl = slot + (c - c0)
+                assert sl not in slots
+                slots[sl] = (s, h, c)
+    for s, (q, n) in enumerate(zip(q_lens, kv)):
+        if q == 0 or n == 0:
+            continue
+        nct = (q * G + 15) // 16
+        for h in range(hkv):
+            for c in range(nct):
+                for kt in range((n + 15) // 16):
+                    assert (s, h, c, kt) in cover
+    assert len(cover) == sum(hkv * ((q * G + 15) // 16) * ((n + 15) // 16)
+                             for q, n in zip(q_lens, kv) if q and n)
+    # each merge record reads exactly the partial slots of its (s, h, column)
+    seen = set()
+    for m in merges:
+        s, h, c, nparts, slot0, stride = (int(x) for x in m[:6])
+        want = sorted(sl for sl, owner in slots.items() if owner == (s, h, c))
+        got = sorted(slot0 + j * stride for j in range(nparts))
+        assert got == want and nparts > 1
+        seen.add((s, h, c))
+    assert len(seen) == merges.shape[0]
+    assert p.partials_floats >= len(slots) * 16 * (max(d, 32) + 2)
+
+
+def test_plan_capacity_and_argument_errors():
+    L = nat.lib()
+    cu = np.array([0, 1, 2], dtype=np.int32)
+    kv = np.array([100, 5000], dtype=np.int32)
+    counts = np.zeros(4, dtype=np.int64)
+    st = L.mf_attention_plan(2, cu.ctypes.data, kv.ctypes.data, 8, 2, 128, 2, 4, None, 0, None, 0,
+                             counts.ctypes.data)
+    assert st == -3 and counts[0] > 0  # sizes reported even when the buffers are too small
+    assert L.mf_attention_plan(2, cu.ctypes.data, kv.ctypes.data, 8, 3, 128, 2, 4, None, 0, None, 0,
+                               counts.ctypes.data) == -1  # heads not a multiple
+    assert L.mf_attention_plan(2, cu.ctypes.data, kv.ctypes.data, 8, 2, 512, 2, 4, None, 0, None, 0,
+                               counts.ctypes.data) == -2  # head_dim beyond the kernels
+    with pytest.raises(ValueError):
+        nat.plan_attention([0, 1], [5, 6], 8, 2, 128, torch.bfloat16, "cpu")
+
+
+def test_plan_orders_longest_items_first():
+    p = _plan([0, 1, 2, 3], [40, 4000, 900], pt=64)
+    narrow = p.items_host[: p.n_narrow]
+    lengths = narrow[:, 5] - narrow[:, 4]
+    assert list(lengths) == sorted(lengths, reverse=True)
+
+
+def test_verify_workspace_size_grows_with_the_batch():
+    L = nat.lib()
+    a = L.mf_spec_verify_workspace_size(4, 3)
+    b = L.mf_spec_verify_workspace_size(64, 3)
+    assert 0 <= a <= b
+
+
+def test_product_path_has_no_cpu_fallback(monkeypatch):
+    """The HIP entry points refuse CPU tensors instead of computing elsewhere."""
+    k = torch.zeros((4, 16, 2, 64))
+    with pytest.raises(Exception):
+        nat.kv_write(torch.zeros((3, 2, 64)), torch.zeros((3, 2, 64)), torch.zeros(3, dtype=torch.int64),
+                     nat.PoolView.from_bshd(k, k.clone()))
