@@ -36,6 +36,12 @@ HBM_PEAK_GBPS = 8000.0
 
 B, HQ, HKV, D, BS, LAYERS = 256, 40, 8, 128, 16, 48
 
+# HBM traffic of one attention launch on the default workload, from two
+# rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch). Each is
+# scaled by what the same counter reads for a plain copy of exactly 1 GiB on
+# the MI355X: FETCH_SIZE reports half the bytes (x2.0), WRITE_SIZE all (x1.0).
+PMC_DEFAULT = {"fetch_kib": 1610776.2, "write_kib": 18176.4, "fetch_scale": 2.0, "write_scale": 1.0}
+
 
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -52,6 +58,10 @@ def parse_args():
                     help="merge split-K partitions inside the attention kernel (last arrival) instead of a merge kernel")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (scale factor for PMC byte counters)")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end continuous-batching run")
+    ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end continuous-batching run")
+    ap.add_argument("--e2e-requests", type=int, default=64)
+    ap.add_argument("--e2e-tokens", type=int, default=128)
     return ap.parse_args()
 
 
@@ -129,6 +139,124 @@ def cpu_baseline(ctx, tables, kpool, vpool, q, seconds: float):
     }
 
 
+# --------------------------------------------------------------------- C4 E2E
+
+E2E_MODEL = dict(vocab_size=49152, hidden_size=960, intermediate_size=2560, num_hidden_layers=32,
+                 num_attention_heads=15, num_key_value_heads=5, head_dim=64)
+E2E_RATE = 20.0  # requests per second
+E2E_KV_MB = 4096
+
+
+class _NullTokenizer:
+    """Token ids in, short text out: the engine detokenizes every emitted token,
+    and a real tokenizer (none is available offline) would only add host time."""
+
+    eos_token_id = None
+    pad_token_id = 0
+
+    def __call__(self, text, return_tensors=None):
+        return {"input_ids": [2 + (ord(c) % 1000) for c in text]}
+
+    def decode(self, ids, skip_special_tokens=True):
+        return "x" * len(ids)
+
+
+def e2e_workload(n: int, seed: int = 0):
+    """Arrival times (Exp(rate 20) gaps), prompts with lengths U[32, 1024] and
+    ids U[0, 49152), drawn in that order from one seeded CPU generator."""
+    gen = torch.Generator().manual_seed(seed)
+    gaps = torch.empty(n, dtype=torch.float64).exponential_(E2E_RATE, generator=gen)
+    arrivals = torch.cumsum(gaps, 0).tolist()
+    lens = torch.randint(32, 1025, (n,), generator=gen)
+    prompts = [torch.randint(0, E2E_MODEL["vocab_size"], (int(m),), generator=gen).tolist() for m in lens]
+    return arrivals, prompts
+
+
+def _drive(engine, prompts, arrivals, params):
+    """Run requests to completion. With ``arrivals`` the clock is virtual: it
+    advances by each step's measured wall time and jumps to the next arrival
+    when the engine is idle; request i is submitted before the first step
+    that starts at or after arrivals[i]. Without, all are submitted at 0."""
+    n = len(prompts)
+    i, clock, steps, ids = 0, 0.0, 0, []
+    if arrivals is None:
+        ids = [engine.submit(p, params) for p in prompts]
+        i = n
+    t0 = time.perf_counter()
+    while i < n or engine.has_work():
+        if arrivals is not None:
+            if i < n and not engine.has_work():
+                clock = max(clock, arrivals[i])
+            while i < n and arrivals[i] <= clock:
+                ids.append(engine.submit(prompts[i], params))
+                i += 1
+        s0 = time.perf_counter()
+        engine.step()
+        clock += time.perf_counter() - s0
+        steps += 1
+    wall = time.perf_counter() - t0
+    tokens = sum(len(engine.runtimes[x].generated) for x in ids)
+    return ids, tokens, steps, wall, clock
+
+
+def run_e2e(args, dev):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from memforge_amd.runtime import ContinuousBatchingEngine, SamplingParams
+
+    cfg = LlamaConfig(**E2E_MODEL, max_position_embeddings=2048, tie_word_embeddings=True,
+                      bos_token_id=1, eos_token_id=2, pad_token_id=0)
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = LlamaForCausalLM(cfg)
+    model = model.to(torch.bfloat16).eval()
+    n_params = sum(p.numel() for p in model.parameters())
+    engine = ContinuousBatchingEngine(model, _NullTokenizer(), block_size=BS, kv_budget_mb=E2E_KV_MB,
+                                      max_num_seqs=64, max_model_len=2048, dtype=torch.bfloat16)
+    params = SamplingParams(max_new_tokens=args.e2e_tokens, temperature=0.0, top_p=1.0, stop_on_eos=False)
+    arrivals, prompts = e2e_workload(args.e2e_requests)
+
+    _drive(engine, prompts[:4], None, SamplingParams(max_new_tokens=4, temperature=0.0, stop_on_eos=False))
+    torch.cuda.synchronize()
+
+    ids, tok_p, steps_p, wall_p, clock_p = _drive(engine, prompts, arrivals, params)
+    kv0, rows0, passes0 = (engine.total_attended_kv_tokens, engine.total_packed_rows,
+                           engine.total_forward_passes)
+    ids_s, tok_s, steps_s, wall_s, _ = _drive(engine, prompts, None, params)
+    kv_tokens = engine.total_attended_kv_tokens - kv0
+    rows = engine.total_packed_rows - rows0
+    passes = engine.total_forward_passes - passes0
+    spec = engine.spec
+    kv_bytes_per_token = spec.bytes_per_token  # K and V, every layer
+    # bytes a step cannot avoid: every weight once per pass, every visible K/V
+    # row once, every new K/V row written once
+    bytes_s = passes * 2 * n_params + kv_tokens * kv_bytes_per_token + rows * kv_bytes_per_token
+    ideal_s = bytes_s / (HBM_PEAK_GBPS * 1e9)
+    return {
+        "workload": (f"C4: {args.e2e_requests} requests, Poisson {E2E_RATE:g} req/s (virtual time), prompts "
+                     f"U[32,1024], {args.e2e_tokens} greedy tokens, SmolLM2-360M-shaped Llama bf16 random "
+                     f"init, KV {E2E_KV_MB} MB in 16-token blocks, max_num_seqs 64"),
+        "poisson_tok_s": round(tok_p / max(clock_p - arrivals[0], 1e-9), 1),
+        "poisson_steps": steps_p,
+        "poisson_virtual_s": round(clock_p - arrivals[0], 3),
+        "saturated_tok_s": round(tok_s / wall_s, 1),
+        "saturated_steps": steps_s,
+        "saturated_wall_s": round(wall_s, 3),
+        "saturated_ms_per_step": round(wall_s / steps_s * 1e3, 3),
+        "output_tokens": tok_s,
+        "params": n_params,
+        "kv_pool_blocks": engine.pool.num_blocks,
+        "roofline": {
+            "bound": "hbm",
+            "bytes": bytes_s,
+            "ideal_s": round(ideal_s, 4),
+            "frac": round(ideal_s / wall_s, 4),
+            "note": "algorithmic bytes of the saturated run (weights once per pass + visible K/V + K/V "
+                    "writes) at 8 TB/s over its wall time",
+        },
+    }
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -149,6 +277,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "copies": 3}))
+        return
+    if args.e2e_only:
+        print(json.dumps({"e2e": run_e2e(args, dev)}))
         return
     ctx, tables, kpool, vpool, q = make_workload(args.sigma, dev)
     out = torch.empty_like(q)
@@ -226,6 +357,10 @@ def main():
 
     per_layer = attn_bytes(ctx)
     total = per_layer * args.layers * args.steps
+    traffic = None
+    if args.sigma == 1.0 and args.partition_tiles == 0 and not args.fused:
+        traffic = int(PMC_DEFAULT["fetch_kib"] * 1024 * PMC_DEFAULT["fetch_scale"]
+                      + PMC_DEFAULT["write_kib"] * 1024 * PMC_DEFAULT["write_scale"])
     value = total / wall / 1e9
     attn_avg_s = float(np.mean(attn_ms)) / 1e3
     achieved = per_layer / attn_avg_s / 1e9
@@ -262,7 +397,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "kernel": "attn_kernel<bf16,128,1,fast>" + (" (split-K merge fused)" if args.fused else ""),
             "kernel_avg_us": round(attn_avg_s * 1e6, 2),
             "merge_avg_us": round(float(np.mean(merge_ms)) * 1e3, 2),
@@ -271,6 +406,10 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(ctx, tables, kpool, vpool, q, args.cpu_seconds)
+    if not args.no_e2e:
+        del kpool, vpool, partials
+        torch.cuda.empty_cache()
+        result["e2e"] = run_e2e(args, dev)
     print(json.dumps(result))
 
 

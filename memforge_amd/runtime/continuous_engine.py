@@ -245,6 +245,8 @@ class ContinuousBatchingEngine:
         self.total_speculative_sequence_rounds = 0
         self.total_blockwise_layers = 0
         self.total_blockwise_fallbacks = 0
+        self.total_attended_kv_tokens = 0  # sum over passes of every sequence's kv length
+        self.total_packed_rows = 0  # query rows through the model (prefill + decode + verify)
         self.engine_started_at = time.perf_counter()
         self._abort_lock = threading.Lock()
         self._pending_aborts: set = set()
@@ -511,6 +513,8 @@ class ContinuousBatchingEngine:
         self.total_forward_passes += 1
         self.total_blockwise_layers += binding.used
         self.total_fused_tokens += T
+        self.total_attended_kv_tokens += int(sum(kv_lens))
+        self.total_packed_rows += T
 
         logits = out.logits[0]  # (len(emit), vocab)
         greedy = [j for j, i in enumerate(emit) if plan[i]["rt"].params.temperature <= 0.0]
@@ -574,6 +578,8 @@ class ContinuousBatchingEngine:
         queries = [[rt.tokens[-1]] + cand for rt, cand in zip(rts, proposals)]
         logits, new_kv, _ = verify_candidates_batched(self.model, self.pool, None, tables, ctx, queries, self.device)
         self.total_forward_passes += 1
+        self.total_attended_kv_tokens += sum(c + k + 1 for c in ctx)
+        self.total_packed_rows += (k + 1) * len(rts)
         self.total_speculative_rounds += 1
         self.total_speculative_sequence_rounds += len(rts)
         events: List[TokenEvent] = []
@@ -737,6 +743,8 @@ class ContinuousBatchingEngine:
             "block_attention_enabled": True,
             "blockwise_layer_calls": self.total_blockwise_layers,
             "blockwise_fallbacks": self.total_blockwise_fallbacks,
+            "attended_kv_tokens": self.total_attended_kv_tokens,
+            "packed_rows": self.total_packed_rows,
             "view_cache_mb_in_use": 0.0,
             "view_cache_budget_mb": 0.0,
             "view_cache_grants": 0,
