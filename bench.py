@@ -62,6 +62,7 @@ def parse_args():
     ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end continuous-batching run")
     ap.add_argument("--e2e-requests", type=int, default=64)
     ap.add_argument("--e2e-tokens", type=int, default=128)
+    ap.add_argument("--no-mixed", action="store_true", help="skip the C2 mixed-step and C3 verify measurements")
     return ap.parse_args()
 
 
@@ -136,6 +137,238 @@ def cpu_baseline(ctx, tables, kpool, vpool, q, seconds: float):
         "sample": (f"{len(sample)} of {B} sequences ({int(cs.sum())} context tokens), 1 layer, "
                    f"{passes} passes in {dt:.1f}s; reference gather+materialised attention ported "
                    f"to torch-CPU float32, bytes counted as the bf16 workload's"),
+    }
+
+
+# ------------------------------------------------------------- C2 / C3 steps
+
+SM_HQ, SM_HKV, SM_D, SM_LAYERS = 15, 5, 64, 32  # SmolLM2-360M attention shape
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def _tables_for(kv_lens, gen):
+    nblk = [(int(n) + BS - 1) // BS for n in kv_lens]
+    perm = torch.randperm(sum(nblk), generator=gen).tolist()
+    tables, k = [], 0
+    for nb in nblk:
+        tables.append(perm[k:k + nb])
+        k += nb
+    return tables, sum(nblk)
+
+
+def _event_us(pairs):
+    return float(np.mean([a.elapsed_time(b) for a, b in pairs])) * 1e3
+
+
+def run_c2(dev, layers=SM_LAYERS, reps=3):
+    """Mixed ragged step: 4 prefill chunks of 512 on priors U[0,2048] + 28
+    decodes with contexts U[64,4096]; per layer the KV scatter of all 2076
+    new tokens, then one varlen attention launch pair (decode items, prefill
+    items) and the split-K merge. A real per-layer pool (32 layers) so no
+    layer's reads come from a cache another layer filled."""
+    from memforge_amd import _native as nat
+
+    gen = torch.Generator().manual_seed(0)
+    prior = torch.randint(0, 2049, (4,), generator=gen).tolist()
+    dctx = torch.randint(64, 4097, (28,), generator=gen).tolist()
+    q_lens = [512] * 4 + [1] * 28
+    kv = [p + 512 for p in prior] + dctx
+    starts = prior + [c - 1 for c in dctx]
+    tables, nblocks = _tables_for(kv, gen)
+    T = sum(q_lens)
+    gdev = torch.Generator(device=dev).manual_seed(0)
+    kp = torch.randn((layers, nblocks, BS, SM_HKV, SM_D), generator=gdev, device=dev, dtype=torch.bfloat16)
+    vp = torch.randn_like(kp)
+    q = torch.randn((T, SM_HQ, SM_D), generator=gdev, device=dev, dtype=torch.bfloat16)
+    knew = torch.randn((layers, T, SM_HKV, SM_D), generator=gdev, device=dev, dtype=torch.bfloat16)
+    vnew = torch.randn_like(knew)
+    out = torch.empty_like(q)
+    cu = [0]
+    for n in q_lens:
+        cu.append(cu[-1] + n)
+    positions = [s + i for s, n in zip(starts, q_lens) for i in range(n)]
+    slots = [tables[e][p // BS] * BS + p % BS for e, (s0, n) in enumerate(zip(starts, q_lens))
+             for p in range(s0, s0 + n)]
+    slot_t = torch.tensor(slots, dtype=torch.int64, device=dev)
+    bt = torch.zeros((len(kv), max(len(t) for t in tables)), dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    bt = bt.to(dev)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
+    kv_t = torch.tensor(kv, dtype=torch.int32, device=dev)
+    pos_t = torch.tensor(positions, dtype=torch.int64, device=dev)
+    plan = nat.plan_attention(cu, kv, SM_HQ, SM_HKV, SM_D, torch.bfloat16, dev)
+    partials = torch.empty(max(plan.partials_floats, 1), dtype=torch.float32, device=dev)
+    narrow = nat.AttentionPlan(plan.items, plan.merges, plan.n_narrow, 0, 0, plan.partials_floats,
+                               plan.items_host, plan.merges_host)
+    wide = nat.AttentionPlan(plan.items[plan.n_narrow:], plan.merges, 0, plan.n_wide, 0, plan.partials_floats,
+                             plan.items_host, plan.merges_host)
+    merges = nat.AttentionPlan(plan.items, plan.merges, 0, 0, plan.n_merges, plan.partials_floats,
+                               plan.items_host, plan.merges_host)
+    scale = 1.0 / math.sqrt(SM_D)
+    views = [nat.PoolView.from_bshd(kp[i], vp[i]) for i in range(layers)]
+
+    def layer(i, ev=None):
+        if ev:
+            ev[0].record()
+        nat.kv_write(knew[i], vnew[i], slot_t, views[i])
+        if ev:
+            ev[1].record()
+        for part, e in ((narrow, 2), (wide, 3), (merges, 4)):
+            if part.n_narrow + part.n_wide + part.n_merges:
+                nat.paged_attention(q, out, views[i], bt, cu_t, kv_t, pos_t, part, scale, SM_HKV, partials=partials)
+            if ev:
+                ev[e].record()
+
+    for i in range(layers):
+        layer(i)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(layers * reps)]
+    for r in range(reps):
+        for i in range(layers):
+            layer(i, evs[r * layers + i])
+    torch.cuda.synchronize()
+    write_us = _event_us([(e[0], e[1]) for e in evs])
+    dec_us = _event_us([(e[1], e[2]) for e in evs])
+    pre_us = _event_us([(e[2], e[3]) for e in evs])
+    mrg_us = _event_us([(e[3], e[4]) for e in evs])
+    kvb = SM_HKV * SM_D * 2 * 2  # K+V bytes per token per layer
+    write_bytes = T * kvb * 2 + T * 8  # read new rows, write pool rows, read slots
+    dec_bytes = sum(dctx) * kvb + 28 * SM_HQ * SM_D * 2 * 2
+    pre_bytes = sum(p + 512 for p in prior) * kvb + 4 * 512 * SM_HQ * SM_D * 2 * 2
+    pre_flops = sum(4 * SM_HQ * SM_D * (p + i + 1) for p in prior for i in range(512))
+    return {
+        "workload": "C2: 4 prefill chunks x 512 (prior U[0,2048]) + 28 decodes (ctx U[64,4096]), 15q/5kv, "
+                    "D 64, bf16, block 16, KV scatter of 2076 tokens, 32 layers x 3 reps",
+        "kv_write_us": round(write_us, 2),
+        "kv_write_gbps": round(write_bytes / write_us / 1e3, 1),
+        "kv_write_frac": round(write_bytes / write_us / 1e3 / HBM_PEAK_GBPS, 4),
+        "decode_attn_us": round(dec_us, 2),
+        "decode_attn_gbps": round(dec_bytes / dec_us / 1e3, 1),
+        "prefill_attn_us": round(pre_us, 2),
+        "prefill_attn_tflops": round(pre_flops / pre_us / 1e6, 1),
+        "prefill_mfma_frac": round(pre_flops / pre_us / 1e6 / BF16_PEAK_TFLOPS, 4),
+        "prefill_attn_gbps": round(pre_bytes / pre_us / 1e3, 1),
+        "merge_us": round(mrg_us, 2),
+        "plan": {"narrow": plan.n_narrow, "wide": plan.n_wide, "merges": plan.n_merges},
+        "step_attn_us": round(dec_us + pre_us + mrg_us, 2),
+    }
+
+
+def run_kv_write_large(dev, tokens=33792, reps=20):
+    """KV write of a C4-sized prefill step (33,792 tokens of the SmolLM2
+    shape, bf16) into a shuffled pool: the streaming case of the same kernel."""
+    from memforge_amd import _native as nat
+
+    gen = torch.Generator().manual_seed(1)
+    nblocks = (tokens + BS - 1) // BS + 64
+    perm = torch.randperm(nblocks * BS, generator=gen)[:tokens].to(dev)
+    kp = torch.zeros((nblocks, BS, SM_HKV, SM_D), device=dev, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    k = torch.randn((tokens, SM_HKV, SM_D), device=dev, dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    view = nat.PoolView.from_bshd(kp, vp)
+    nat.kv_write(k, v, perm, view)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in evs:
+        a.record()
+        nat.kv_write(k, v, perm, view)
+        b.record()
+    torch.cuda.synchronize()
+    us = _event_us(evs)
+    nbytes = tokens * SM_HKV * SM_D * 2 * 2 * 2 + tokens * 8
+    return {"tokens": tokens, "us": round(us, 2), "gbps": round(nbytes / us / 1e3, 1),
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4)}
+
+
+def run_c3(dev, layers=SM_LAYERS, reps=3):
+    """Speculative verify step: 16 sequences, ctx U[128,2048], lookahead 4,
+    so 5 query rows per sequence attend to the pool plus their own in-flight
+    candidates; then rejection sampling over (16,5,49152) target and
+    (16,4,49152) draft logits, N(0, variance 2), with seeded uniforms/noise."""
+    from memforge_amd import _native as nat
+
+    gen = torch.Generator().manual_seed(0)
+    B, K, V = 16, 4, 49152
+    ctx = torch.randint(128, 2049, (B,), generator=gen).tolist()
+    tables, nblocks = _tables_for([c + K + 1 for c in ctx], gen)
+    tl = torch.randn((B, K + 1, V), generator=gen) * math.sqrt(2.0)
+    dl = torch.randn((B, K, V), generator=gen) * math.sqrt(2.0)
+    dprobs = torch.softmax(dl, dim=-1)
+    dtok = torch.stack([torch.multinomial(dprobs[b], 1, generator=gen).view(-1) for b in range(B)])
+    u = torch.rand((B, K), generator=gen)
+    noise = torch.empty((B, V)).exponential_(1.0, generator=gen)
+    gdev = torch.Generator(device=dev).manual_seed(0)
+    kp = torch.randn((layers, nblocks, BS, SM_HKV, SM_D), generator=gdev, device=dev, dtype=torch.bfloat16)
+    vp = torch.randn_like(kp)
+    T = B * (K + 1)
+    q = torch.randn((T, SM_HQ, SM_D), generator=gdev, device=dev, dtype=torch.bfloat16)
+    nk = torch.randn((layers, T, SM_HKV, SM_D), generator=gdev, device=dev, dtype=torch.bfloat16)
+    nv = torch.randn_like(nk)
+    out = torch.empty_like(q)
+    cu = [b * (K + 1) for b in range(B + 1)]
+    kvl = [c + K + 1 for c in ctx]
+    positions = [c + j for c in ctx for j in range(K + 1)]
+    bt = torch.zeros((B, max(len(t) for t in tables)), dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    bt = bt.to(dev)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=dev)
+    kv_t = torch.tensor(kvl, dtype=torch.int32, device=dev)
+    pl_t = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    pos_t = torch.tensor(positions, dtype=torch.int64, device=dev)
+    plan = nat.plan_attention(cu, kvl, SM_HQ, SM_HKV, SM_D, torch.bfloat16, dev)
+    partials = torch.empty(max(plan.partials_floats, 1), dtype=torch.float32, device=dev)
+    scale = 1.0 / math.sqrt(SM_D)
+    views = [nat.PoolView.from_bshd(kp[i], vp[i]) for i in range(layers)]
+
+    def layer(i):
+        nat.paged_attention(q, out, views[i], bt, cu_t, kv_t, pos_t, plan, scale, SM_HKV, pool_lens=pl_t,
+                            new_k_rows=nk[i], new_v_rows=nv[i], partials=partials)
+
+    for i in range(layers):
+        layer(i)
+    torch.cuda.synchronize()
+    evs = []
+    for _ in range(reps):
+        for i in range(layers):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            layer(i)
+            b.record()
+            evs.append((a, b))
+    torch.cuda.synchronize()
+    attn_us = _event_us(evs)
+    kvb = SM_HKV * SM_D * 2 * 2
+    attn_bytes = sum(c + K + 1 for c in ctx) * kvb + T * SM_HQ * SM_D * 2 * 2
+    attn_flops = sum(4 * SM_HQ * SM_D * (c + j + 1) for c in ctx for j in range(K + 1))
+
+    tl_d, dp_d, dt_d = tl.to(dev), dprobs.to(dev), dtok.to(torch.int32).to(dev)
+    u_d, n_d = u.to(dev), noise.to(dev)
+    res = nat.spec_verify(dt_d, dp_d, tl_d, 1.0, u_d, n_d)
+    torch.cuda.synchronize()
+    vevs = []
+    for _ in range(10):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        nat.spec_verify(dt_d, dp_d, tl_d, 1.0, u_d, n_d)
+        b.record()
+        vevs.append((a, b))
+    torch.cuda.synchronize()
+    ver_us = _event_us(vevs)
+    ver_bytes = (B * (K + 1) * V + B * K * V) * 4
+    return {
+        "workload": "C3: 16 sequences, ctx U[128,2048], lookahead 4 (5 query rows each, candidates attended "
+                    "in flight), 15q/5kv, D 64, bf16, 32 layers x 3 reps; rejection over (16,5,49152) target "
+                    "and (16,4,49152) draft fp32 logits N(0, var 2), temperature 1",
+        "verify_attn_us": round(attn_us, 2),
+        "verify_attn_gbps": round(attn_bytes / attn_us / 1e3, 1),
+        "verify_attn_frac": round(attn_bytes / attn_us / 1e3 / HBM_PEAK_GBPS, 4),
+        "verify_attn_tflops": round(attn_flops / attn_us / 1e6, 2),
+        "rejection_us": round(ver_us, 2),
+        "rejection_gbps": round(ver_bytes / ver_us / 1e3, 1),
+        "accepted_per_row": res.num_accepted.cpu().tolist(),
     }
 
 
@@ -406,8 +639,15 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(ctx, tables, kpool, vpool, q, args.cpu_seconds)
-    if not args.no_e2e:
+    if not args.no_mixed:
         del kpool, vpool, partials
+        torch.cuda.empty_cache()
+        result["c2"] = run_c2(dev)
+        result["c2"]["kv_write_c4_prefill"] = run_kv_write_large(dev)
+        result["c3"] = run_c3(dev)
+        torch.cuda.empty_cache()
+    if not args.no_e2e:
+        kpool = vpool = partials = None
         torch.cuda.empty_cache()
         result["e2e"] = run_e2e(args, dev)
     print(json.dumps(result))
