@@ -399,9 +399,10 @@ def spec_verify(draft_tokens: torch.Tensor, draft_probs: torch.Tensor, target_lo
     draft_tokens = draft_tokens.to(torch.int32).contiguous()
     u_accept = u_accept.to(torch.float32).contiguous()
     dev = target_logits.device
+    # only the first count[b] entries of each row are written
     res = VerifyResult(
-        tokens=torch.zeros((B, K + 1), dtype=torch.int32, device=dev),
-        is_draft=torch.zeros((B, K + 1), dtype=torch.uint8, device=dev),
+        tokens=torch.empty((B, K + 1), dtype=torch.int32, device=dev),
+        is_draft=torch.empty((B, K + 1), dtype=torch.uint8, device=dev),
         count=torch.empty(B, dtype=torch.int32, device=dev),
         num_accepted=torch.empty(B, dtype=torch.int32, device=dev),
     )

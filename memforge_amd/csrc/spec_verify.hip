@@ -1,25 +1,37 @@
 // Speculative rejection sampling with caller-supplied randomness.
 //
-// Launch 1 (one workgroup per target row (b, i), i <= K): softmax statistics
-// of logits[b][i][:V] / T -- running max and sum of exp in a single pass --
-// plus the first index of the maximum logit (the greedy distribution).
-// Launch 2 (one workgroup per draft row b): the sequential accept loop over
-// the K candidates (one lane, double precision, exactly the reference's
-// arithmetic), then the resample over the vocabulary: the residual
-// max(p - q, 0), its normalisation, the second normalisation the reference's
-// sample_from_probs applies, and argmax(w / E) with first-index ties, which is
-// torch.multinomial(w, 1) given the same Exp(1) draws E.
+// Launch 1 (skipped when the target rows already are probabilities): softmax
+// statistics of logits[b][i][:V] / T. Each row is split into 8192-element
+// chunks, one 256-thread workgroup per (row, chunk), every element loaded once
+// into registers with 16-byte vector loads; the workgroup writes its chunk's
+// max, sum of exp(x - max) and first argmax of the raw logits.
+// Launches 2-4 (one workgroup per (row, 4096-element chunk)): the first
+// combines the chunk statistics of the row's K+1 target positions and runs the
+// sequential accept loop over the K candidates in one lane, in double
+// precision, exactly the reference's arithmetic; then the vocabulary passes of
+// the final draw -- the residual max(p - q, 0) and its sum, the weights and
+// their sum (the second normalisation the reference's sample_from_probs
+// applies), and argmax(w / E) with first-index ties, which is
+// torch.multinomial(w, 1) given the same Exp(1) draws E. Launch 5 combines the
+// chunk winners.
 // (memforge_ml/speculative/rejection_sampler.py:12-83,
 //  memforge_ml/runtime/batched_speculative.py:112-124, 731-777)
 #include <cfloat>
 #include <climits>
+#include <type_traits>
 
 #include "mf_common.h"
 
 namespace mf {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kStatThreads = 256;
+constexpr int kStatVec = 8;                             // float4 groups per thread per chunk
+constexpr int kChunk = kStatThreads * 4 * kStatVec;    // elements per statistics workgroup
+constexpr int kPassThreads = 256;
+constexpr int kPassVec = 4;                             // float4 groups per thread per pass chunk
+constexpr int kPassChunk = kPassThreads * 4 * kPassVec;  // elements per draw-pass workgroup
+constexpr int kMaxPositions = 64;                       // K + 1 target positions per row
 
 struct VerifyArgs {
     int B, K, V;
@@ -38,19 +50,112 @@ struct VerifyArgs {
     uint8_t* out_is_draft;
     int32_t* out_count;
     int32_t* out_num_accepted;
-    float* row_max;
-    float* row_sum;
-    int32_t* row_argmax;
+    int nchunk;           // statistics chunks per row
+    float* st_max;        // [rows][nchunk]
+    float* st_sum;
+    int32_t* st_arg;
+    float* pos_max;       // [rows] combined statistics of each target position
+    float* pos_sum;
+    int32_t* pos_arg;
+    int32_t* row_stop;    // [B] stop position and whether it rejected
+    int32_t* row_reject;
+    int npass;            // draw-pass chunks per row
+    float* part_diff;     // [B][npass]
+    float* part_w;
+    float* part_best;
+    int32_t* part_best_i;
+    int vec_logits, vec_q, vec_e;  // rows are aligned for vector loads
 };
 
-__device__ __forceinline__ float load_logit(const VerifyArgs& a, int b, int i, int v) {
-    const int64_t off = (int64_t)b * a.tl_sr + (int64_t)i * a.tl_sp + v;
-    if (a.ldt == MF_F32) return ((const float*)a.logits)[off];
-    const uint32_t bits = ((const uint16_t*)a.logits)[off];
+// Target probability of token v at target row `row` (= b * (K + 1) + i)
+// whose raw logit (or probability) is `raw`.
+__device__ __forceinline__ float target_prob(const VerifyArgs& a, int row, float raw, int v) {
+    if (a.target_is_probs) return raw;
+    if (a.temperature <= 0.f) return v == a.pos_arg[row] ? 1.f : 0.f;
+    const float x = a.temperature == 1.f ? raw : raw / a.temperature;
+    return expf(x - a.pos_max[row]) / a.pos_sum[row];
+}
+
+__device__ __forceinline__ const char* logit_row(const VerifyArgs& a, int b, int i) {
+    const int es = a.ldt == MF_F32 ? 4 : 2;
+    return a.logits + ((int64_t)b * a.tl_sr + (int64_t)i * a.tl_sp) * es;
+}
+
+__device__ __forceinline__ float logit_at(const VerifyArgs& a, const char* row, int v) {
+    if (a.ldt == MF_F32) return ((const float*)row)[v];
+    const uint32_t bits = ((const uint16_t*)row)[v];
     return a.ldt == MF_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
 }
 
-// Block reductions (256 threads = 4 waves).
+// Four consecutive logits starting at e (e % 4 == 0); elements >= V read as 0
+// and must be masked by the caller.
+__device__ __forceinline__ void logits4(const VerifyArgs& a, const char* row, int e, float (&x)[4]) {
+    if (a.vec_logits && e + 3 < a.V) {
+        if (a.ldt == MF_F32) {
+            const float4 f = *(const float4*)((const float*)row + e);
+            x[0] = f.x; x[1] = f.y; x[2] = f.z; x[3] = f.w;
+        } else {
+            const uint2 u = *(const uint2*)((const uint16_t*)row + e);
+            const uint32_t w[4] = {u.x & 0xffffu, u.x >> 16, u.y & 0xffffu, u.y >> 16};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                x[k] = a.ldt == MF_BF16 ? bf16_bits_to_f32(w[k]) : f16_bits_to_f32(w[k]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = e + k < a.V ? logit_at(a, row, e + k) : 0.f;
+}
+
+__device__ __forceinline__ void floats4(const float* row, int e, int V, int vec, float (&x)[4]) {
+    if (vec && e + 3 < V) {
+        const float4 f = *(const float4*)(row + e);
+        x[0] = f.x; x[1] = f.y; x[2] = f.z; x[3] = f.w;
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = e + k < V ? row[e + k] : 0.f;
+}
+
+// N groups of 4 consecutive values at e0 + u * stride, all in bounds and
+// aligned: unconditional vector loads, all issued before any is used.
+template <int DT, int N>
+__device__ __forceinline__ void vload_logits(const char* row, int e0, int stride, float (&x)[N][4]) {
+    if constexpr (DT == MF_F32) {
+        float4 f[N];
+#pragma unroll
+        for (int u = 0; u < N; ++u) f[u] = *(const float4*)((const float*)row + e0 + u * stride);
+#pragma unroll
+        for (int u = 0; u < N; ++u) { x[u][0] = f[u].x; x[u][1] = f[u].y; x[u][2] = f[u].z; x[u][3] = f[u].w; }
+    } else {
+        uint2 w[N];
+#pragma unroll
+        for (int u = 0; u < N; ++u) w[u] = *(const uint2*)((const uint16_t*)row + e0 + u * stride);
+#pragma unroll
+        for (int u = 0; u < N; ++u) {
+            x[u][0] = bits_to_f32<DT>(w[u].x & 0xffffu);
+            x[u][1] = bits_to_f32<DT>(w[u].x >> 16);
+            x[u][2] = bits_to_f32<DT>(w[u].y & 0xffffu);
+            x[u][3] = bits_to_f32<DT>(w[u].y >> 16);
+        }
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void vload_floats(const float* row, int e0, int stride, float (&x)[N][4]) {
+    float4 f[N];
+#pragma unroll
+    for (int u = 0; u < N; ++u) f[u] = *(const float4*)(row + e0 + u * stride);
+#pragma unroll
+    for (int u = 0; u < N; ++u) { x[u][0] = f[u].x; x[u][1] = f[u].y; x[u][2] = f[u].z; x[u][3] = f[u].w; }
+}
+
+// Max with the first index among equal maxima; NaN never wins.
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+
+template <int NW>
 __device__ float block_sum(float v, float* sh) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -58,13 +163,27 @@ __device__ float block_sum(float v, float* sh) {
     __syncthreads();
     if ((threadIdx.x & 63) == 0) sh[w] = v;
     __syncthreads();
-    return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) t += sh[k];
+    return t;
 }
 
-// Max with the first index among equal maxima; NaN never wins.
-__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
-    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+template <int NW>
+__device__ float block_max(float v, float* sh) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    float t = sh[0];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) t = fmaxf(t, sh[k]);
+    return t;
 }
+
+template <int NW>
 __device__ void block_argmax(float& v, int& i, float* shv, int* shi) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -77,126 +196,298 @@ __device__ void block_argmax(float& v, int& i, float* shv, int* shi) {
     if ((threadIdx.x & 63) == 0) { shv[w] = v; shi[w] = i; }
     __syncthreads();
     v = shv[0]; i = shi[0];
-    for (int k = 1; k < 4; ++k) argmax_merge(v, i, shv[k], shi[k]);
+#pragma unroll
+    for (int k = 1; k < NW; ++k) argmax_merge(v, i, shv[k], shi[k]);
 }
 
-__global__ __launch_bounds__(kThreads) void row_stats_kernel(VerifyArgs a) {
+template <int DT>
+__global__ __launch_bounds__(kStatThreads) void row_stats_kernel(VerifyArgs a) {
     __shared__ float shv[4], shs[4];
     __shared__ int shi[4];
-    const int row = blockIdx.x;  // b * (K + 1) + i
+    const int c = blockIdx.x;    // chunk of the row
+    const int row = blockIdx.y;  // b * (K + 1) + i
     const int b = row / (a.K + 1), i = row - b * (a.K + 1);
+    const char* lrow = logit_row(a, b, i);
     const float T = a.temperature;
     const float kNegInf = -__builtin_huge_valf();
-    float m = kNegInf, s = 0.f;
+    const int base = c * kChunk + threadIdx.x * 4;
+
+    float raw[kStatVec][4];
+    if (a.vec_logits && (c + 1) * kChunk <= a.V) {
+        vload_logits<DT, kStatVec>(lrow, base, kStatThreads * 4, raw);
+    } else {
+#pragma unroll
+        for (int u = 0; u < kStatVec; ++u) logits4(a, lrow, base + u * kStatThreads * 4, raw[u]);
+    }
+
+    // argmax and max of the raw logits; x = raw / T is monotone in raw for
+    // T > 0, so max(raw / T) is max(raw) / T exactly and is divided once.
     float am = kNegInf;
     int ai = INT_MAX;
-    for (int v = threadIdx.x; v < a.V; v += kThreads) {
-        const float raw = load_logit(a, b, i, v);
-        argmax_merge(am, ai, raw, v);
-        if (T > 0.f) {
-            const float x = raw / T;
-            if (x > m) { s = s * expf(m - x) + 1.f; m = x; }
-            else s += expf(x - m);
-        }
-    }
-    block_argmax(am, ai, shv, shi);
-    if (T > 0.f) {
-        // merge (m, s) across the block
-        float gm = m;
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off, 64));
-        const int w = threadIdx.x >> 6;
-        __syncthreads();
-        if ((threadIdx.x & 63) == 0) shv[w] = gm;
-        __syncthreads();
-        gm = fmaxf(fmaxf(shv[0], shv[1]), fmaxf(shv[2], shv[3]));
-        const float scaled = (m == kNegInf) ? 0.f : s * expf(m - gm);
-        const float tot = block_sum(scaled, shs);
-        if (threadIdx.x == 0) { a.row_max[row] = gm; a.row_sum[row] = tot; }
-    }
-    if (threadIdx.x == 0) a.row_argmax[row] = ai;
-}
-
-// Target probability of token v at position i of row b.
-__device__ __forceinline__ float target_prob(const VerifyArgs& a, int b, int i, int v) {
-    if (a.target_is_probs) return load_logit(a, b, i, v);
-    const int row = b * (a.K + 1) + i;
-    if (a.temperature <= 0.f) return v == a.row_argmax[row] ? 1.f : 0.f;
-    const float x = load_logit(a, b, i, v) / a.temperature;
-    return expf(x - a.row_max[row]) / a.row_sum[row];
-}
-
-__global__ __launch_bounds__(kThreads) void decide_kernel(VerifyArgs a) {
-    __shared__ float shs[4];
-    __shared__ float shv[4];
-    __shared__ int shi[4];
-    __shared__ int s_stop, s_reject;
-    const int b = blockIdx.x;
-    const int K = a.K;
-    if (threadIdx.x == 0) {
-        int stop = K, reject = 0;
-        for (int i = 0; i < K; ++i) {
-            const int tok = a.draft_tokens[(int64_t)b * K + i];
-            const double q = (double)a.draft_probs[(int64_t)b * a.dp_sr + (int64_t)i * a.dp_sp + tok];
-            const double p = (double)target_prob(a, b, i, tok);
-            const double ratio = p / (q + 1e-9);
-            const double acc = ratio < 1.0 ? ratio : 1.0;
-            const double r = (double)a.u_accept[(int64_t)b * K + i];
-            const bool ok = r <= acc;
-            a.out_tokens[(int64_t)b * (K + 1) + i] = tok;
-            a.out_is_draft[(int64_t)b * (K + 1) + i] = 1;
-            if (!ok) { stop = i; reject = 1; break; }
+    for (int u = 0; u < kStatVec; ++u) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int e = base + u * kStatThreads * 4 + k;
+            if (e < a.V) argmax_merge(am, ai, raw[u][k], e);
         }
-        s_stop = stop;
-        s_reject = reject;
+    }
+    const float raw_max = am;  // this lane's max (NaN never wins)
+    block_argmax<4>(am, ai, shv, shi);
+    if (T > 0.f) {
+        const bool unit = T == 1.f;
+        const float m = raw_max == kNegInf ? kNegInf : (unit ? raw_max : raw_max / T);
+        float s = 0.f;
+        if (m != kNegInf) {
+#pragma unroll
+            for (int u = 0; u < kStatVec; ++u) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int e = base + u * kStatThreads * 4 + k;
+                    if (e < a.V) s += expf((unit ? raw[u][k] : raw[u][k] / T) - m);
+                }
+            }
+        }
+        const float gm = block_max<4>(m, shv);
+        const float scaled = (m == kNegInf) ? 0.f : s * expf(m - gm);
+        const float tot = block_sum<4>(scaled, shs);
+        if (threadIdx.x == 0) {
+            a.st_max[(int64_t)row * a.nchunk + c] = gm;
+            a.st_sum[(int64_t)row * a.nchunk + c] = tot;
+        }
+    }
+    if (threadIdx.x == 0) a.st_arg[(int64_t)row * a.nchunk + c] = ai;
+}
+
+// Combined softmax statistics of the row's K+1 target positions (one lane
+// each, into shared memory), then the sequential accept loop (lane 0, double
+// precision). Every workgroup of the row runs this -- it reads (K+1) x chunks
+// statistics and K probabilities -- and the chunk-0 workgroup publishes the
+// result.
+__device__ void accept_row(const VerifyArgs& a, int b, float* s_max, float* s_sum, int* s_arg, int* s_stop,
+                           int* s_reject, bool publish) {
+    const int K = a.K;
+    const float T = a.temperature;
+    const float kNegInf = -__builtin_huge_valf();
+    const int lane = threadIdx.x;
+    if (!a.target_is_probs && lane < K + 1) {
+        const int row = b * (K + 1) + lane;
+        const int64_t o = (int64_t)row * a.nchunk;
+        const char* lrow = logit_row(a, b, lane);
+        float gm = kNegInf, v = kNegInf;
+        int arg = INT_MAX;
+        for (int c = 0; c < a.nchunk; ++c) {
+            if (T > 0.f) gm = fmaxf(gm, a.st_max[o + c]);
+            const int ci = a.st_arg[o + c];
+            if (ci != INT_MAX) argmax_merge(v, arg, logit_at(a, lrow, ci), ci);
+        }
+        float tot = 0.f;
+        if (T > 0.f) {
+            for (int c = 0; c < a.nchunk; ++c) {
+                const float cm = a.st_max[o + c];
+                if (cm != kNegInf) tot += a.st_sum[o + c] * expf(cm - gm);
+            }
+        }
+        s_max[lane] = gm;
+        s_sum[lane] = tot;
+        s_arg[lane] = arg;
+        if (publish) {
+            a.pos_max[row] = gm;
+            a.pos_sum[row] = tot;
+            a.pos_arg[row] = arg;
+        }
+    }
+    // lane i < K fetches candidate i's token, draft and target probabilities
+    // and uniform in parallel; lane 0 then walks them in order
+    __shared__ int s_tok[kMaxPositions];
+    __shared__ float s_q[kMaxPositions], s_p[kMaxPositions], s_u[kMaxPositions];
+    __syncthreads();
+    if (lane < K) {
+        const int tok = a.draft_tokens[(int64_t)b * K + lane];
+        const float q = a.draft_probs[(int64_t)b * a.dp_sr + (int64_t)lane * a.dp_sp + tok];
+        const float raw = logit_at(a, logit_row(a, b, lane), tok);
+        float pf;
+        if (a.target_is_probs) pf = raw;
+        else if (T <= 0.f) pf = tok == s_arg[lane] ? 1.f : 0.f;
+        else pf = expf((T == 1.f ? raw : raw / T) - s_max[lane]) / s_sum[lane];
+        s_tok[lane] = tok;
+        s_q[lane] = q;
+        s_p[lane] = pf;
+        s_u[lane] = a.u_accept[(int64_t)b * K + lane];
     }
     __syncthreads();
-    const int i = s_stop;
-    const bool reject = s_reject != 0;
-    const float* q = a.draft_probs + (int64_t)b * a.dp_sr + (int64_t)i * a.dp_sp;
-    const float* E = a.noise + (int64_t)b * a.noise_sr;
-
-    // w_v before sample_from_probs' own normalisation:
-    //   reject with positive residual: diff_v / diff_sum
-    //   otherwise: target p_v (the reject-without-residual case and the bonus)
-    float diff_sum = 0.f;
-    bool use_diff = false;
-    if (reject) {
-        float part = 0.f;
-        for (int v = threadIdx.x; v < a.V; v += kThreads)
-            part += fmaxf(target_prob(a, b, i, v) - q[v], 0.f);
-        diff_sum = block_sum(part, shs);
-        use_diff = diff_sum > 0.f;
+    if (lane == 0) {
+        int stop = K, reject = 0;
+        for (int i = 0; i < K; ++i) {
+            const int tok = s_tok[i];
+            const double q = (double)s_q[i];
+            const double p = (double)s_p[i];
+            const double ratio = p / (q + 1e-9);
+            const double acc = ratio < 1.0 ? ratio : 1.0;
+            const double r = (double)s_u[i];
+            if (publish) {
+                a.out_tokens[(int64_t)b * (K + 1) + i] = tok;
+                a.out_is_draft[(int64_t)b * (K + 1) + i] = 1;
+            }
+            if (!(r <= acc)) { stop = i; reject = 1; break; }
+        }
+        *s_stop = stop;
+        *s_reject = reject;
+        if (publish) {
+            a.row_stop[b] = stop;
+            a.row_reject[b] = reject;
+        }
     }
-    auto weight = [&](int v) -> float {
-        if (use_diff) return fmaxf(target_prob(a, b, i, v) - q[v], 0.f) / diff_sum;
-        return fmaxf(target_prob(a, b, i, v), 0.f);
+    __syncthreads();
+}
+
+// The draw's vocabulary passes, one (chunk, row) per workgroup:
+//   PASS 0: partial sum of the residual max(p - q, 0) (rows that rejected)
+//   PASS 1: partial sum of the weights w_v (residual / its sum, or p)
+//   PASS 2: partial argmax of (w_v / sum w) / E_v
+// Sums of partials are taken in chunk order, so results do not depend on
+// scheduling.
+template <int PASS, int DT>
+__global__ __launch_bounds__(kPassThreads) void draw_pass_kernel(VerifyArgs a) {
+    __shared__ float shs[kPassThreads / 64];
+    __shared__ int shi[kPassThreads / 64];
+    __shared__ float s_max[kMaxPositions], s_sum[kMaxPositions];
+    __shared__ int s_arg[kMaxPositions];
+    __shared__ int s_stop, s_reject;
+    const int c = blockIdx.x, b = blockIdx.y;
+    const int K = a.K;
+    int i;
+    bool reject;
+    if (PASS == 0) {
+        accept_row(a, b, s_max, s_sum, s_arg, &s_stop, &s_reject, c == 0);
+        i = s_stop;
+        reject = s_reject != 0;
+    } else {
+        i = a.row_stop[b];
+        reject = a.row_reject[b] != 0;
+    }
+    const int prow = b * (K + 1) + i;
+    // pass 0 reads the stop position's statistics from shared memory (the
+    // published copy is not visible until the kernel ends)
+    auto tprob = [&](float raw, int v) -> float {
+        if (PASS != 0) return target_prob(a, prow, raw, v);
+        if (a.target_is_probs) return raw;
+        if (a.temperature <= 0.f) return v == s_arg[i] ? 1.f : 0.f;
+        const float x = a.temperature == 1.f ? raw : raw / a.temperature;
+        return expf(x - s_max[i]) / s_sum[i];
     };
+    const char* lrow = logit_row(a, b, i);
+    const float* q = a.draft_probs + (int64_t)b * a.dp_sr + (int64_t)i * a.dp_sp;
+    const int64_t po = (int64_t)b * a.npass;
+    if (PASS == 0 && !reject) {
+        if (threadIdx.x == 0) a.part_diff[po + c] = 0.f;
+        return;
+    }
+    float diff_sum = 0.f, wsum = 0.f;
+    if (PASS >= 1 && reject)
+        for (int k = 0; k < a.npass; ++k) diff_sum += a.part_diff[po + k];
+    const bool use_diff = reject && diff_sum > 0.f;
+    if (PASS == 2)
+        for (int k = 0; k < a.npass; ++k) wsum += a.part_w[po + k];
+
+    const int base = c * kPassChunk + threadIdx.x * 4;
+    const float* Erow = a.noise + (int64_t)b * a.noise_sr;
+    const bool need_q = PASS == 0 || use_diff;
+    float x[kPassVec][4], qq[kPassVec][4], en[kPassVec][4];
+    if ((c + 1) * kPassChunk <= a.V && a.vec_logits && (a.vec_q || !need_q) && (a.vec_e || PASS != 2)) {
+        vload_logits<DT, kPassVec>(lrow, base, kPassThreads * 4, x);
+        if (need_q) vload_floats<kPassVec>(q, base, kPassThreads * 4, qq);
+        if (PASS == 2) vload_floats<kPassVec>(Erow, base, kPassThreads * 4, en);
+    } else {
+#pragma unroll
+        for (int u = 0; u < kPassVec; ++u) {
+            const int e = base + u * kPassThreads * 4;
+            logits4(a, lrow, e, x[u]);
+            if (need_q) floats4(q, e, a.V, a.vec_q, qq[u]);
+            if (PASS == 2) floats4(Erow, e, a.V, a.vec_e, en[u]);
+        }
+    }
     float part = 0.f;
-    for (int v = threadIdx.x; v < a.V; v += kThreads) part += weight(v);
-    const float wsum = block_sum(part, shs);
-    const float uniform = 1.f / (float)a.V;
     float best = -__builtin_huge_valf();
     int best_i = INT_MAX;
-    for (int v = threadIdx.x; v < a.V; v += kThreads) {
-        const float pv = wsum == 0.f ? uniform : weight(v) / wsum;
-        argmax_merge(best, best_i, pv / E[v], v);
-    }
-    block_argmax(best, best_i, shv, shi);
-    if (threadIdx.x == 0) {
-        a.out_tokens[(int64_t)b * (K + 1) + i] = best_i;
-        a.out_is_draft[(int64_t)b * (K + 1) + i] = 0;
-        a.out_count[b] = i + 1;
-        a.out_num_accepted[b] = i;
+    const float uniform = 1.f / (float)a.V;
+#pragma unroll
+    for (int u = 0; u < kPassVec; ++u)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int e = base + u * kPassThreads * 4 + k;
+            if (e >= a.V) continue;
+            const float p = tprob(x[u][k], e);
+            if (PASS == 0) {
+                part += fmaxf(p - qq[u][k], 0.f);
+            } else {
+                const float w = use_diff ? fmaxf(p - qq[u][k], 0.f) / diff_sum : fmaxf(p, 0.f);
+                if (PASS == 1) {
+                    part += w;
+                } else {
+                    const float pv = wsum == 0.f ? uniform : w / wsum;
+                    argmax_merge(best, best_i, pv / en[u][k], e);
+                }
+            }
+        }
+    if (PASS < 2) {
+        const float tot = block_sum<kPassThreads / 64>(part, shs);
+        if (threadIdx.x == 0) (PASS == 0 ? a.part_diff : a.part_w)[po + c] = tot;
+    } else {
+        block_argmax<kPassThreads / 64>(best, best_i, shs, shi);
+        if (threadIdx.x == 0) {
+            a.part_best[po + c] = best;
+            a.part_best_i[po + c] = best_i;
+        }
     }
 }
+
+// Combine each row's chunk winners (a kernel boundary, not a per-workgroup
+// release fence: on this multi-XCD part a device-scope fence writes back L2).
+__global__ __launch_bounds__(64) void finish_kernel(VerifyArgs a) {
+    const int b = blockIdx.x * 64 + threadIdx.x;
+    if (b >= a.B) return;
+    const int K = a.K;
+    const int i = a.row_stop[b];
+    const int64_t po = (int64_t)b * a.npass;
+    float best = -__builtin_huge_valf();
+    int best_i = INT_MAX;
+    for (int k = 0; k < a.npass; ++k) argmax_merge(best, best_i, a.part_best[po + k], a.part_best_i[po + k]);
+    a.out_tokens[(int64_t)b * (K + 1) + i] = best_i;
+    a.out_is_draft[(int64_t)b * (K + 1) + i] = 0;
+    a.out_count[b] = i + 1;
+    a.out_num_accepted[b] = i;
+}
+
+inline int chunks_for(int vocab) { return (vocab + kChunk - 1) / kChunk; }
+inline int pass_chunks_for(int vocab) { return (vocab + kPassChunk - 1) / kPassChunk; }
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
 }  // namespace mf
 
+namespace {
+struct Layout {
+    int64_t st, pos, rows, pass;  // float/int slots of each section
+    int64_t total_bytes;
+};
+inline Layout layout_for(int64_t num_rows, int num_draft) {
+    // sized for a vocabulary of up to 2^20 entries
+    const int64_t rows = num_rows * (num_draft + 1);
+    Layout l;
+    l.st = rows * mf::chunks_for(1 << 20);
+    l.pos = rows;
+    l.rows = num_rows;
+    l.pass = num_rows * mf::pass_chunks_for(1 << 20);
+    l.total_bytes = (3 * l.st + 3 * l.pos + 2 * l.rows + 4 * l.pass) * 4 + 256;
+    return l;
+}
+}  // namespace
+
 extern "C" int64_t mf_spec_verify_workspace_size(int num_rows, int num_draft) {
     if (num_rows < 0 || num_draft < 0) return 0;
-    return (int64_t)num_rows * (num_draft + 1) * 3 * 4 + 256;
+    return layout_for(num_rows, num_draft).total_bytes;
 }
 
 extern "C" int mf_spec_verify(int num_rows, int num_draft, int vocab, const int32_t* draft_tokens,
@@ -208,7 +499,9 @@ extern "C" int mf_spec_verify(int num_rows, int num_draft, int vocab, const int3
                               uint8_t* out_is_draft, int32_t* out_count, int32_t* out_num_accepted,
                               void* workspace, int64_t workspace_bytes, mf_stream_t stream) {
     using namespace mf;
-    if (num_rows < 0 || num_draft < 0 || vocab <= 0 || !dtype_ok(target_dtype)) return MF_ERR_ARG;
+    if (num_rows < 0 || num_draft < 0 || vocab <= 0 || vocab > (1 << 20) || !dtype_ok(target_dtype))
+        return MF_ERR_ARG;
+    if (num_draft + 1 > kMaxPositions) return MF_ERR_UNSUPPORTED;
     if (num_rows == 0) return MF_OK;
     if (!target_logits || !exp_noise || !out_tokens || !out_is_draft || !out_count || !out_num_accepted)
         return MF_ERR_ARG;
@@ -216,18 +509,56 @@ extern "C" int mf_spec_verify(int num_rows, int num_draft, int vocab, const int3
     if (!workspace || workspace_bytes < mf_spec_verify_workspace_size(num_rows, num_draft))
         return MF_ERR_WORKSPACE;
     const int64_t nrow = (int64_t)num_rows * (num_draft + 1);
-    // The residual needs draft probabilities at the stop position; with no
-    // candidates the bonus row is the only draw and q is never read.
+    const int nchunk = chunks_for(vocab);
+    // a vector load covers 4 elements: 16 bytes of fp32, 8 bytes of bf16/f16
+    const int es = target_dtype == MF_F32 ? 4 : 2;
+    const bool vec_logits = ((uintptr_t)target_logits % (4 * es)) == 0 && (tl_stride_row % 4) == 0 &&
+                            (tl_stride_pos % 4) == 0;
+    const bool vec_q = num_draft == 0 ||
+                       (aligned16(draft_probs) && (dp_stride_row % 4) == 0 && (dp_stride_pos % 4) == 0);
+    const bool vec_e = aligned16(exp_noise) && (noise_stride_row % 4) == 0;
+    const Layout l = layout_for(num_rows, num_draft);
+    const int npass = pass_chunks_for(vocab);
+    float* ws = (float*)workspace;
+    float* p = ws;
+    auto take = [&](int64_t n) { float* r = p; p += n; return r; };
+    float* st_max = take(l.st);
+    float* st_sum = take(l.st);
+    int32_t* st_arg = (int32_t*)take(l.st);
+    float* pos_max = take(l.pos);
+    float* pos_sum = take(l.pos);
+    int32_t* pos_arg = (int32_t*)take(l.pos);
+    int32_t* row_stop = (int32_t*)take(l.rows);
+    int32_t* row_reject = (int32_t*)take(l.rows);
+    float* part_diff = take(l.pass);
+    float* part_w = take(l.pass);
+    float* part_best = take(l.pass);
+    int32_t* part_best_i = (int32_t*)take(l.pass);
     VerifyArgs a{num_rows, num_draft, vocab, draft_tokens, draft_probs, dp_stride_row, dp_stride_pos,
                  (const char*)target_logits, target_dtype, tl_stride_row, tl_stride_pos, temperature,
                  target_is_probs, u_accept, exp_noise, noise_stride_row, out_tokens, out_is_draft, out_count,
-                 out_num_accepted, (float*)workspace, (float*)workspace + nrow,
-                 (int32_t*)((float*)workspace + 2 * nrow)};
+                 out_num_accepted, nchunk, st_max, st_sum, st_arg, pos_max, pos_sum, pos_arg, row_stop,
+                 row_reject, npass, part_diff, part_w, part_best, part_best_i,
+                 vec_logits ? 1 : 0, vec_q ? 1 : 0, vec_e ? 1 : 0};
     hipStream_t st = (hipStream_t)stream;
-    if (!target_is_probs) {
-        hipLaunchKernelGGL(row_stats_kernel, dim3((unsigned)nrow), dim3(kThreads), 0, st, a);
+    auto run = [&](auto dt_tag) -> int {
+        constexpr int DT = decltype(dt_tag)::value;
+        if (!target_is_probs) {
+            hipLaunchKernelGGL(row_stats_kernel<DT>, dim3((unsigned)nchunk, (unsigned)nrow), dim3(kStatThreads), 0,
+                               st, a);
+            if (int e = check_launch()) return e;
+        }
+        const dim3 grid((unsigned)npass, (unsigned)num_rows);
+        hipLaunchKernelGGL((draw_pass_kernel<0, DT>), grid, dim3(kPassThreads), 0, st, a);
         if (int e = check_launch()) return e;
-    }
-    hipLaunchKernelGGL(decide_kernel, dim3((unsigned)num_rows), dim3(kThreads), 0, st, a);
-    return check_launch();
+        hipLaunchKernelGGL((draw_pass_kernel<1, DT>), grid, dim3(kPassThreads), 0, st, a);
+        if (int e = check_launch()) return e;
+        hipLaunchKernelGGL((draw_pass_kernel<2, DT>), grid, dim3(kPassThreads), 0, st, a);
+        if (int e = check_launch()) return e;
+        hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((num_rows + 63) / 64)), dim3(64), 0, st, a);
+        return check_launch();
+    };
+    if (target_dtype == MF_F32) return run(std::integral_constant<int, MF_F32>{});
+    if (target_dtype == MF_BF16) return run(std::integral_constant<int, MF_BF16>{});
+    return run(std::integral_constant<int, MF_F16>{});
 }
