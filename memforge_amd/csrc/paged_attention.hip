@@ -263,7 +263,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int row0 = a.cu_seqlens[s];
     const int ncols = (a.cu_seqlens[s + 1] - row0) * a.G;
     const int kv_len = a.kv_lens[s];
-    const int pool_len = (FAST || a.pool_lens == nullptr) ? kv_len : a.pool_lens[s];
+    const int pool_len = a.pool_lens == nullptr ? kv_len : a.pool_lens[s];
     const int D = a.head_dim;
 
     // ---- columns owned by this lane (one per tile)
@@ -334,11 +334,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 
     // K: lane (g, j) loads key j's head_dim chunks (c*4 + g).
     // V: lane (g, j) loads keys 4g..4g+3, head_dim elements [j*VCH, j*VCH+VCH).
-    // FAST path (16-token blocks, no in-flight keys, head_dim == DP): every
+    // FAST path (16-token blocks, head_dim == DP): every
     // load is unconditional, so the compiler can keep the next tile's loads in
     // flight while the current tile is processed; the item's block-table
     // entries (at most kMaxItemTiles = 64) are fetched once, one per lane, and
     // read back with readlane.
+    // Tiles [kt0, fast_end) run through the pipelined loop. On the fast path
+    // with in-flight keys (a verify pass) that is only the tiles lying wholly
+    // in the pool; the one or two tiles holding the boundary and the in-flight
+    // candidates follow through the general per-key loads.
+    int fast_end = kt_end;
+    if constexpr (FAST) {
+        if (a.pool_lens != nullptr) fast_end = max(kt0, min(kt_end, pool_len >> 4));
+    }
     int tbl = 0;
     const int tbl_base = kt0;
     // byte offsets of this lane's K chunk (key j, chunk g) and V chunk (keys
@@ -348,8 +356,26 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const uint32_t v_lane_off = (uint32_t)(((int64_t)(4 * g) * a.p_ss + j * VCH) * ES);
     if constexpr (FAST) {
         const int idx = kt0 + lane;
-        tbl = idx < kt_end ? a.block_tables[(int64_t)s * a.bt_stride + idx] : 0;
+        tbl = idx < fast_end ? a.block_tables[(int64_t)s * a.bt_stride + idx] : 0;
     }
+    auto load_general = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
+        const char* kp = key_row(a.k_pool, a.new_k, kt * 16 + j);
+#pragma unroll
+        for (int c = 0; c < NL; ++c) {
+            const int d0 = (c * 4 + g) * EPL;
+            kf[c] = (kp && d0 < D) ? *(const uint4*)(kp + (int64_t)d0 * ES) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const char* vp = key_row(a.v_pool, a.new_v, kt * 16 + 4 * g + r);
+            if (vp && j * VCH < D) {
+                ld_words<VB>(vp + (int64_t)j * VCH * ES, vf[r]);
+            } else {
+#pragma unroll
+                for (int w = 0; w < VWD; ++w) vf[r][w] = 0;
+            }
+        }
+    };
     auto load_tile = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
         if constexpr (FAST) {
             // block base is wave-uniform (scalar registers); the lane's byte
@@ -363,22 +389,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) ld_words<VB>(vb + v_lane_off + r * v_row_bytes, vf[r]);
         } else {
-            const char* kp = key_row(a.k_pool, a.new_k, kt * 16 + j);
-#pragma unroll
-            for (int c = 0; c < NL; ++c) {
-                const int d0 = (c * 4 + g) * EPL;
-                kf[c] = (kp && d0 < D) ? *(const uint4*)(kp + (int64_t)d0 * ES) : make_uint4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const char* vp = key_row(a.v_pool, a.new_v, kt * 16 + 4 * g + r);
-                if (vp && j * VCH < D) {
-                    ld_words<VB>(vp + (int64_t)j * VCH * ES, vf[r]);
-                } else {
-#pragma unroll
-                    for (int w = 0; w < VWD; ++w) vf[r][w] = 0;
-                }
-            }
+            load_general(kt, kf, vf);
         }
     };
 
@@ -472,8 +483,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     // outstanding load at the join and serialises the pipeline.
     uint4 kA[NL], kB[NL];
     uint32_t vA[4][VWD], vB[4][VWD];
-    if (kt0 < kt_end) {
-        const int last = kt_end - 1;
+    if (kt0 < fast_end) {
+        const int last = fast_end - 1;
         int kt = kt0;
         load_tile(kt, kA, vA);
         if constexpr (FAST && NT == 1) {
@@ -500,6 +511,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 process(kt, kB, vB);
                 if (++kt > last) break;
             }
+        }
+    }
+
+    if constexpr (FAST) {
+        for (int kt = fast_end; kt < kt_end; ++kt) {
+            load_general(kt, kA, vA);
+            process(kt, kA, vA);
         }
     }
 
@@ -869,7 +887,7 @@ extern "C" int mf_paged_attention(
     a.part_dstride = part_dstride_for(head_dim);
     a.merges = plan_merges;
     a.counters = num_merges > 0 ? merge_counters : nullptr;
-    const bool fast = block_size == 16 && pool_lens == nullptr && head_dim == DP;
+    const bool fast = block_size == 16 && head_dim == DP;
     hipStream_t st = (hipStream_t)stream;
 
 #define MF_ATTN_CASE(DT, DPV)                                                                  \
