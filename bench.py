@@ -62,6 +62,8 @@ def parse_args():
     ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end continuous-batching run")
     ap.add_argument("--e2e-requests", type=int, default=64)
     ap.add_argument("--e2e-tokens", type=int, default=128)
+    ap.add_argument("--e2e-eager", action="store_true",
+                    help="run decode steps eagerly instead of replaying the captured decode graph")
     ap.add_argument("--no-mixed", action="store_true", help="skip the C2 mixed-step and C3 verify measurements")
     return ap.parse_args()
 
@@ -445,7 +447,8 @@ def run_e2e(args, dev):
     model = model.to(torch.bfloat16).eval()
     n_params = sum(p.numel() for p in model.parameters())
     engine = ContinuousBatchingEngine(model, _NullTokenizer(), block_size=BS, kv_budget_mb=E2E_KV_MB,
-                                      max_num_seqs=64, max_model_len=2048, dtype=torch.bfloat16)
+                                      max_num_seqs=64, max_model_len=2048, dtype=torch.bfloat16,
+                                      paged_cuda_graph=not args.e2e_eager)
     params = SamplingParams(max_new_tokens=args.e2e_tokens, temperature=0.0, top_p=1.0, stop_on_eos=False)
     arrivals, prompts = e2e_workload(args.e2e_requests)
 
@@ -469,6 +472,7 @@ def run_e2e(args, dev):
         "workload": (f"C4: {args.e2e_requests} requests, Poisson {E2E_RATE:g} req/s (virtual time), prompts "
                      f"U[32,1024], {args.e2e_tokens} greedy tokens, SmolLM2-360M-shaped Llama bf16 random "
                      f"init, KV {E2E_KV_MB} MB in 16-token blocks, max_num_seqs 64"),
+        "decode_steps": "eager" if args.e2e_eager else "HIP graph replay (paged_cuda_graph)",
         "poisson_tok_s": round(tok_p / max(clock_p - arrivals[0], 1e-9), 1),
         "poisson_steps": steps_p,
         "poisson_virtual_s": round(clock_p - arrivals[0], 3),

@@ -167,6 +167,34 @@ int mf_paged_attention(const void* q, int64_t q_stride_row, int64_t q_stride_hea
                        int64_t num_merges, float* partials, int64_t partials_floats,
                        int32_t* merge_counters, mf_stream_t stream);
 
+/* mf_paged_attention with the work counts read from device memory, for a
+ * caller that captures the launch in a HIP graph and replays it with a new
+ * plan each step. No counterpart in the reference: it serves callers that
+ * capture the decode step (the grid must be fixed at capture time).
+ * The grids are sized by the capacities: plan_items holds capacity_narrow
+ * narrow items followed by capacity_wide wide items (wide items always start
+ * at plan_items + capacity_narrow * MF_PLAN_ITEM_INTS), plan_merges holds
+ * capacity_merges records, and device_counts (device, int32[3]) gives the
+ * live numbers of narrow items, wide items and merges -- each at most its
+ * capacity; workgroups past them exit at once. Split-K partitions are merged
+ * by the separate merge kernel. Everything else is as in mf_paged_attention.
+ */
+int mf_paged_attention_counted(const void* q, int64_t q_stride_row, int64_t q_stride_head,
+                               void* out, int64_t out_stride_row, int64_t out_stride_head,
+                               int dtype, const void* k_pool, const void* v_pool,
+                               int64_t pool_stride_block, int64_t pool_stride_slot,
+                               int64_t pool_stride_head, int block_size,
+                               const int32_t* block_tables, int64_t block_table_stride,
+                               const int32_t* cu_seqlens, const int32_t* kv_lens,
+                               const int64_t* positions, const int32_t* row_map,
+                               const int32_t* pool_lens, const void* new_k, const void* new_v,
+                               int64_t new_stride_row, int64_t new_stride_head,
+                               int num_q_heads, int num_kv_heads, int head_dim, float scale,
+                               const int32_t* plan_items, int64_t capacity_narrow,
+                               int64_t capacity_wide, const int32_t* plan_merges,
+                               int64_t capacity_merges, const int32_t* device_counts,
+                               float* partials, int64_t partials_floats, mf_stream_t stream);
+
 /* Host-side planner for mf_paged_attention. Inputs are HOST arrays:
  * cu_seqlens[B+1] and kv_lens[B]. Splits every (sequence, kv head, column
  * tile) over key partitions of `partition_tiles` 16-key tiles (0 = chosen
@@ -174,10 +202,12 @@ int mf_paged_attention(const void* q, int64_t q_stride_row, int64_t q_stride_hea
  * items (narrow items -- one 16-column tile -- first, then wide ones) and
  * MF_PLAN_MERGE_INTS ints per split-K merge to merges. counts receives
  * [num_items_narrow, num_items_wide, num_merges, partials_floats].
- * A plan is valid for the dtype and head_dim it was made for.
+ * A plan is valid for the dtype and head_dim it was made for and carries the
+ * sequences' first rows, row counts and kv lengths: the cu_seqlens / kv_lens
+ * later passed to mf_paged_attention must hold the same values.
  * Returns MF_ERR_WORKSPACE if a capacity is too small (counts still holds
  * the required sizes). */
-#define MF_PLAN_ITEM_INTS 8
+#define MF_PLAN_ITEM_INTS 12
 #define MF_PLAN_MERGE_INTS 8
 int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const int32_t* kv_lens,
                       int num_q_heads, int num_kv_heads, int head_dim, int dtype,

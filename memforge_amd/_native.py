@@ -23,7 +23,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libmemforge_hip.so")
 MF_F32, MF_F16, MF_BF16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: MF_F32, torch.float16: MF_F16, torch.bfloat16: MF_BF16}
 
-PLAN_ITEM_INTS = 8
+PLAN_ITEM_INTS = 12
 PLAN_MERGE_INTS = 8
 ENTRY_INTS = 6
 
@@ -48,6 +48,10 @@ _SIGNATURES = {
         _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
         _c_int, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int,
         _c_int, _c_f32, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _vp]),
+    "mf_paged_attention_counted": (_c_int, [
+        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
+        _c_int, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int,
+        _c_int, _c_f32, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _vp]),
     "mf_attention_plan": (_c_int, [_c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                    _vp, _c_i64, _vp, _c_i64, _vp]),
     "mf_spec_verify_workspace_size": (_c_i64, [_c_int, _c_int]),
@@ -217,9 +221,11 @@ class AttentionPlan:
     merges_host: np.ndarray
 
 
-def plan_attention(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int,
-                   num_kv_heads: int, head_dim: int, dtype: torch.dtype, device,
-                   partition_tiles: int = 0) -> AttentionPlan:
+def plan_attention_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int,
+                        num_kv_heads: int, head_dim: int, dtype: torch.dtype,
+                        partition_tiles: int = 0) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """mf_attention_plan on host arrays: (items [n, PLAN_ITEM_INTS], merges
+    [m, PLAN_MERGE_INTS], counts [n_narrow, n_wide, n_merges, partials_floats])."""
     cu = np.ascontiguousarray(np.asarray(cu_seqlens, dtype=np.int32))
     kv = np.ascontiguousarray(np.asarray(kv_lens, dtype=np.int32))
     B = kv.shape[0]
@@ -238,10 +244,64 @@ def plan_attention(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_head
     merges = np.zeros((max(n_merges, 1), PLAN_MERGE_INTS), dtype=np.int32)
     _check(L.mf_attention_plan(*args, items.ctypes.data, n_items, merges.ctypes.data, n_merges,
                                counts.ctypes.data), "mf_attention_plan")
-    dev_items = torch.from_numpy(items).to(device, non_blocking=False)
-    dev_merges = torch.from_numpy(merges).to(device, non_blocking=False)
-    return AttentionPlan(dev_items, dev_merges, int(counts[0]), int(counts[1]), n_merges,
-                         int(counts[3]), items[:n_items], merges[:n_merges])
+    return items[:n_items], merges[:n_merges], counts
+
+
+def plan_attention(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int,
+                   num_kv_heads: int, head_dim: int, dtype: torch.dtype, device,
+                   partition_tiles: int = 0) -> AttentionPlan:
+    items, merges, counts = plan_attention_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim,
+                                                dtype, partition_tiles)
+    dev_items = torch.from_numpy(np.ascontiguousarray(items if items.shape[0] else
+                                                      np.zeros((1, PLAN_ITEM_INTS), np.int32))).to(device)
+    dev_merges = torch.from_numpy(np.ascontiguousarray(merges if merges.shape[0] else
+                                                       np.zeros((1, PLAN_MERGE_INTS), np.int32))).to(device)
+    return AttentionPlan(dev_items, dev_merges, int(counts[0]), int(counts[1]), int(counts[2]),
+                         int(counts[3]), items, merges)
+
+
+class CountedPlan:
+    """Fixed device buffers for a plan whose counts live in device memory
+    (mf_paged_attention_counted): the shapes and addresses a captured HIP
+    graph recorded stay valid while ``update`` swaps in each step's plan.
+
+    Items hold ``cap_narrow`` narrow then ``cap_wide`` wide rows; ``update``
+    raises if a plan does not fit. Host staging is pinned; each update waits
+    for the previous one's copies before reusing it."""
+
+    def __init__(self, cap_narrow: int, cap_wide: int, cap_merges: int, partials_floats: int, device):
+        self.cap_narrow, self.cap_wide, self.cap_merges = cap_narrow, cap_wide, cap_merges
+        rows = max(cap_narrow + cap_wide, 1)
+        self.items = torch.zeros((rows, PLAN_ITEM_INTS), dtype=torch.int32, device=device)
+        self.merges = torch.zeros((max(cap_merges, 1), PLAN_MERGE_INTS), dtype=torch.int32, device=device)
+        self.counts = torch.zeros(3, dtype=torch.int32, device=device)
+        self.partials = torch.empty(max(partials_floats, 1), dtype=torch.float32, device=device)
+        self._h_items = torch.zeros((rows, PLAN_ITEM_INTS), dtype=torch.int32).pin_memory()
+        self._h_merges = torch.zeros((max(cap_merges, 1), PLAN_MERGE_INTS), dtype=torch.int32).pin_memory()
+        self._h_counts = torch.zeros(3, dtype=torch.int32).pin_memory()
+        self._copied = None
+
+    def update(self, items: np.ndarray, merges: np.ndarray, counts: np.ndarray) -> None:
+        n_narrow, n_wide, n_merges, floats = (int(x) for x in counts)
+        if n_narrow > self.cap_narrow or n_wide > self.cap_wide or n_merges > self.cap_merges:
+            raise ValueError(f"plan ({n_narrow}, {n_wide}, {n_merges}) exceeds the capacity "
+                             f"({self.cap_narrow}, {self.cap_wide}, {self.cap_merges})")
+        if floats > self.partials.numel():
+            raise ValueError(f"plan needs {floats} partial floats, the buffer holds {self.partials.numel()}")
+        if self._copied is not None:
+            self._copied.synchronize()
+        hi = self._h_items.numpy()
+        hi[:n_narrow] = items[:n_narrow]
+        hi[self.cap_narrow:self.cap_narrow + n_wide] = items[n_narrow:n_narrow + n_wide]
+        if n_merges:
+            self._h_merges.numpy()[:n_merges] = merges[:n_merges]
+        self._h_counts.numpy()[:] = (n_narrow, n_wide, n_merges)
+        self.items.copy_(self._h_items, non_blocking=True)
+        if n_merges:
+            self.merges[:n_merges].copy_(self._h_merges[:n_merges], non_blocking=True)
+        self.counts.copy_(self._h_counts, non_blocking=True)
+        self._copied = torch.cuda.Event()
+        self._copied.record()
 
 
 class Workspace:
@@ -303,6 +363,9 @@ def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView
         if t.dtype != dt or not t.is_contiguous():
             raise TypeError(f"{name} must be a contiguous {dt} tensor")
     Hq, D = q_rows.shape[1], q_rows.shape[2]
+    if isinstance(plan, CountedPlan):
+        return _paged_attention_counted(q_rows, out_rows, pool, block_tables, cu_seqlens, kv_lens, positions,
+                                        plan, scale, num_kv_heads, row_map, pool_lens, new_k_rows, new_v_rows)
     if partials is None:
         partials = _WORKSPACE.partials(plan.partials_floats, q_rows.device)
     if fused_merge and counters is None:
@@ -332,6 +395,28 @@ def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView
     ), "mf_paged_attention")
 
 
+def _paged_attention_counted(q_rows, out_rows, pool, block_tables, cu_seqlens, kv_lens, positions,
+                             plan: CountedPlan, scale, num_kv_heads, row_map, pool_lens, nk, nv) -> None:
+    if pool_lens is not None:
+        if nk is None or nv is None:
+            raise ValueError("pool_lens needs the in-flight new_k_rows/new_v_rows")
+        require_device(pool_lens, nk, nv)
+    Hq, D = q_rows.shape[1], q_rows.shape[2]
+    bt_stride = block_tables.shape[1] if block_tables.dim() == 2 else 0
+    _check(lib().mf_paged_attention_counted(
+        _ptr(q_rows), q_rows.stride(0), q_rows.stride(1),
+        _ptr(out_rows), out_rows.stride(0), out_rows.stride(1),
+        dtype_code(q_rows.dtype), _ptr(pool.k), _ptr(pool.v),
+        pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size,
+        _ptr(block_tables), bt_stride, _ptr(cu_seqlens), _ptr(kv_lens), _ptr(positions),
+        _ptr(row_map), _ptr(pool_lens), _ptr(nk), _ptr(nv),
+        nk.stride(0) if nk is not None else 0, nk.stride(1) if nk is not None else 0,
+        Hq, num_kv_heads, D, float(scale),
+        _ptr(plan.items), plan.cap_narrow, plan.cap_wide, _ptr(plan.merges), plan.cap_merges,
+        _ptr(plan.counts), _ptr(plan.partials), plan.partials.numel(), _stream(),
+    ), "mf_paged_attention_counted")
+
+
 # -------------------------------------------------------------- ragged pack
 
 @dataclass
@@ -345,24 +430,36 @@ class PackedStep:
     block_tables: torch.Tensor  # int32 [B, max_blocks]
     status: torch.Tensor        # int32 [4]
 
+    @classmethod
+    def allocate(cls, total_tokens: int, num_entries: int, max_blocks: int, device) -> "PackedStep":
+        return cls(
+            token_ids=torch.empty(total_tokens, dtype=torch.int64, device=device),
+            positions=torch.empty(total_tokens, dtype=torch.int64, device=device),
+            seq_slot=torch.empty(total_tokens, dtype=torch.int32, device=device),
+            slot_mapping=torch.empty(total_tokens, dtype=torch.int64, device=device),
+            cu_seqlens=torch.empty(num_entries + 1, dtype=torch.int32, device=device),
+            kv_lens=torch.empty(num_entries, dtype=torch.int32, device=device),
+            block_tables=torch.empty((num_entries, max_blocks), dtype=torch.int32, device=device),
+            status=torch.empty(4, dtype=torch.int32, device=device),
+        )
+
 
 def ragged_pack(entries: torch.Tensor, tables: torch.Tensor, tokens: torch.Tensor,
                 total_tokens: int, block_size: int, max_blocks: int,
-                slot_bitmap: Optional[torch.Tensor] = None, num_slots: int = 0) -> PackedStep:
-    """Run mf_ragged_pack on device descriptors (int32 tensors already on the GPU)."""
+                slot_bitmap: Optional[torch.Tensor] = None, num_slots: int = 0,
+                out: Optional[PackedStep] = None) -> PackedStep:
+    """Run mf_ragged_pack on device descriptors (int32 tensors already on the
+    GPU), into ``out``'s buffers when given (they must be sized for
+    ``total_tokens`` rows, ``entries.shape[0]`` entries and ``max_blocks``)."""
     require_device(entries, tables, tokens)
     dev = entries.device
     B = entries.shape[0]
-    out = PackedStep(
-        token_ids=torch.empty(total_tokens, dtype=torch.int64, device=dev),
-        positions=torch.empty(total_tokens, dtype=torch.int64, device=dev),
-        seq_slot=torch.empty(total_tokens, dtype=torch.int32, device=dev),
-        slot_mapping=torch.empty(total_tokens, dtype=torch.int64, device=dev),
-        cu_seqlens=torch.empty(B + 1, dtype=torch.int32, device=dev),
-        kv_lens=torch.empty(B, dtype=torch.int32, device=dev),
-        block_tables=torch.empty((B, max_blocks), dtype=torch.int32, device=dev),
-        status=torch.empty(4, dtype=torch.int32, device=dev),
-    )
+    if out is not None:
+        if (out.token_ids.numel() != total_tokens or out.cu_seqlens.numel() != B + 1
+                or tuple(out.block_tables.shape) != (B, max_blocks)):
+            raise ValueError("preallocated pack buffers do not match the step")
+    else:
+        out = PackedStep.allocate(total_tokens, B, max_blocks, dev)
     _check(lib().mf_ragged_pack(
         _ptr(entries), B, _ptr(tables), _ptr(tokens), block_size, max_blocks, total_tokens,
         _ptr(out.token_ids), _ptr(out.positions), _ptr(out.seq_slot), _ptr(out.slot_mapping),

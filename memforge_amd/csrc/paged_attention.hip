@@ -68,6 +68,7 @@ struct AttnArgs {
     float scale_log2;
     const int32_t* items;
     int num_items;
+    const int32_t* dev_count;  // when set, the live item / merge count (the grid is a capacity)
     float* partials;
     int part_dstride;  // floats per column of a partial slot's output block
     const int32_t* merges;  // plan merge records (fused split-K merge)
@@ -210,9 +211,12 @@ __device__ __forceinline__ void merge_range(const AttnArgs& a, const int32_t* mg
 }
 
 // Output row/head of column tile ct's column j, or false for a padding column.
-__device__ __forceinline__ bool merge_column(const AttnArgs& a, int s, int h, int ct, int j, int& prow, int& qhead) {
-    const int row0 = a.cu_seqlens[s];
-    const int ncols = (a.cu_seqlens[s + 1] - row0) * a.G;
+// mg: a merge record (s, h, column tile, parts, slot0, slot stride, first row,
+// rows)
+__device__ __forceinline__ bool merge_column(const AttnArgs& a, const int32_t* mg, int j, int& prow, int& qhead) {
+    const int h = mg[1], ct = mg[2];
+    const int row0 = mg[6];
+    const int ncols = mg[7] * a.G;
     const int cidx = ct * 16 + j;
     if (cidx >= ncols) return false;
     const int r = cidx / a.G;
@@ -229,7 +233,7 @@ __device__ __forceinline__ void merge_tile(const AttnArgs& a, const int32_t* mg,
     constexpr int ES = DT == MF_F32 ? 4 : 2;
     int prow, qhead;
     const int dbase = 4 * g * VCH;
-    if (!merge_column(a, mg[0], mg[1], mg[2], j, prow, qhead) || dbase >= a.head_dim) return;
+    if (!merge_column(a, mg, j, prow, qhead) || dbase >= a.head_dim) return;
     float mx, L, o[4 * VCH];
     merge_range<DP>(a, mg, 0, 1, j, dbase, mx, L, o);
     const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -252,17 +256,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int item = blockIdx.x * kWaves + wave;
-    if (item >= a.num_items) return;
+    if (item >= (a.dev_count ? *a.dev_count : a.num_items)) return;
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4;  // 16-lane group: MFMA k-group / output row group
     const int j = lane & 15;  // MFMA column (query column) and A-row (key) index
 
+    // The item carries its sequence's first row, row count and kv length (the
+    // planner's copies of cu_seqlens / kv_lens), so nothing waits on loading
+    // them before the row positions and block table are fetched.
     const int32_t* it = a.items + (int64_t)item * MF_PLAN_ITEM_INTS;
     const int s = it[0], h = it[1], c0 = it[2], nct = it[3];
     const int kt0 = it[4], kt1 = it[5], pslot = it[6];
-    const int row0 = a.cu_seqlens[s];
-    const int ncols = (a.cu_seqlens[s + 1] - row0) * a.G;
-    const int kv_len = a.kv_lens[s];
+    const int row0 = it[8];
+    const int ncols = it[9] * a.G;
+    const int kv_len = it[10];
     const int pool_len = a.pool_lens == nullptr ? kv_len : a.pool_lens[s];
     const int D = a.head_dim;
 
@@ -586,14 +593,14 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnArgs a, const int32_t* m
     __shared__ float s_m[kWaves][16], s_l[kWaves][16];
     __shared__ float s_o[kWaves][16][DP];
     const int mi = blockIdx.x;
-    if (mi >= num_merges) return;
+    if (mi >= (a.dev_count ? *a.dev_count : num_merges)) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15;
     const int32_t* mg = merges + (int64_t)mi * MF_PLAN_MERGE_INTS;
     int prow = 0, qhead = 0;
     const int dbase = 4 * g * VCH;
-    const bool active = merge_column(a, mg[0], mg[1], mg[2], j, prow, qhead) && dbase < a.head_dim;
+    const bool active = merge_column(a, mg, j, prow, qhead) && dbase < a.head_dim;
     float mx = kNegInf, L = 0.f, o[4 * VCH];
 #pragma unroll
     for (int e = 0; e < 4 * VCH; ++e) o[e] = 0.f;
@@ -628,13 +635,15 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnArgs a, const int32_t* m
 
 template <int DT, int DP>
 int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t n_wide,
-                     const int32_t* merges, int64_t n_merges, bool fast, hipStream_t stream) {
+                     const int32_t* merges, int64_t n_merges, bool fast, const int32_t* dev_counts,
+                     hipStream_t stream) {
     // With arrival counters the attention kernel merges its own partitions;
     // a merges-only call (no items) still runs the separate merge kernel.
     const bool fused = a.counters != nullptr && (n_narrow + n_wide) > 0;
     if (n_narrow > 0) {
         a.items = items;
         a.num_items = (int)n_narrow;
+        a.dev_count = dev_counts ? dev_counts + 0 : nullptr;
         const dim3 grid((unsigned)((n_narrow + kWaves - 1) / kWaves));
         if (fast) hipLaunchKernelGGL((attn_kernel<DT, DP, 1, true>), grid, dim3(256), 0, stream, a);
         else hipLaunchKernelGGL((attn_kernel<DT, DP, 1, false>), grid, dim3(256), 0, stream, a);
@@ -645,6 +654,7 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
         if (n_wide > 0) {
             a.items = items + n_narrow * MF_PLAN_ITEM_INTS;
             a.num_items = (int)n_wide;
+            a.dev_count = dev_counts ? dev_counts + 1 : nullptr;
             const dim3 grid((unsigned)((n_wide + kWaves - 1) / kWaves));
             if (fast) hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, true>), grid, dim3(256), 0, stream, a);
             else hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, false>), grid, dim3(256), 0, stream, a);
@@ -654,6 +664,7 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
         if (n_wide > 0) return MF_ERR_ARG;  // the plan was made for another dtype
     }
     if (n_merges > 0 && !fused) {
+        a.dev_count = dev_counts ? dev_counts + 2 : nullptr;
         const dim3 grid((unsigned)n_merges);
         hipLaunchKernelGGL((merge_kernel<DT, DP>), grid, dim3(256), 0, stream, a, merges, (int)n_merges);
         if (int st = check_launch()) return st;
@@ -769,6 +780,10 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
                         o[5] = std::min(tiles, (p + 1) * P);
                         o[6] = nparts > 1 ? (int32_t)(group_base + ((int64_t)h * nparts + p) * w) : -1;
                         o[7] = nparts > 1 ? (int32_t)(merge_base + (int64_t)h * w) : -1;
+                        o[8] = cu_seqlens[s];
+                        o[9] = cu_seqlens[s + 1] - cu_seqlens[s];
+                        o[10] = kv_lens[s];
+                        o[11] = 0;
                         ++wi;
                     }
                 }
@@ -782,8 +797,8 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
                             o[3] = nparts;
                             o[4] = (int32_t)(group_base + (int64_t)h * nparts * w + o2);
                             o[5] = w;
-                            o[6] = 0;
-                            o[7] = 0;
+                            o[6] = cu_seqlens[s];
+                            o[7] = cu_seqlens[s + 1] - cu_seqlens[s];
                             ++wm;
                         }
                     }
@@ -815,7 +830,8 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     return MF_OK;
 }
 
-extern "C" int mf_paged_attention(
+namespace {
+int paged_attention_impl(
     const void* q, int64_t q_stride_row, int64_t q_stride_head, void* out, int64_t out_stride_row,
     int64_t out_stride_head, int dtype, const void* k_pool, const void* v_pool,
     int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head, int block_size,
@@ -825,7 +841,7 @@ extern "C" int mf_paged_attention(
     int64_t new_stride_head, int num_q_heads, int num_kv_heads, int head_dim, float scale,
     const int32_t* plan_items, int64_t num_items_narrow, int64_t num_items_wide,
     const int32_t* plan_merges, int64_t num_merges, float* partials, int64_t partials_floats,
-    int32_t* merge_counters, mf_stream_t stream) {
+    int32_t* merge_counters, const int32_t* device_counts, mf_stream_t stream) {
     using namespace mf;
     if (!dtype_ok(dtype) || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
         block_size <= 0 || num_items_narrow < 0 || num_items_wide < 0 || num_merges < 0)
@@ -893,7 +909,7 @@ extern "C" int mf_paged_attention(
 #define MF_ATTN_CASE(DT, DPV)                                                                  \
     if (dtype == DT && DP == DPV)                                                              \
         return launch_attention<DT, DPV>(a, plan_items, num_items_narrow, num_items_wide,      \
-                                         plan_merges, num_merges, fast, st);
+                                         plan_merges, num_merges, fast, device_counts, st);
     MF_ATTN_CASE(MF_F32, 16)
     MF_ATTN_CASE(MF_F32, 32)
     MF_ATTN_CASE(MF_F32, 64)
@@ -908,4 +924,46 @@ extern "C" int mf_paged_attention(
     MF_ATTN_CASE(MF_F16, 256)
 #undef MF_ATTN_CASE
     return MF_ERR_UNSUPPORTED;
+}
+}  // namespace
+
+extern "C" int mf_paged_attention(
+    const void* q, int64_t q_stride_row, int64_t q_stride_head, void* out, int64_t out_stride_row,
+    int64_t out_stride_head, int dtype, const void* k_pool, const void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head, int block_size,
+    const int32_t* block_tables, int64_t block_table_stride, const int32_t* cu_seqlens,
+    const int32_t* kv_lens, const int64_t* positions, const int32_t* row_map,
+    const int32_t* pool_lens, const void* new_k, const void* new_v, int64_t new_stride_row,
+    int64_t new_stride_head, int num_q_heads, int num_kv_heads, int head_dim, float scale,
+    const int32_t* plan_items, int64_t num_items_narrow, int64_t num_items_wide,
+    const int32_t* plan_merges, int64_t num_merges, float* partials, int64_t partials_floats,
+    int32_t* merge_counters, mf_stream_t stream) {
+    return paged_attention_impl(q, q_stride_row, q_stride_head, out, out_stride_row, out_stride_head, dtype,
+                                k_pool, v_pool, pool_stride_block, pool_stride_slot, pool_stride_head,
+                                block_size, block_tables, block_table_stride, cu_seqlens, kv_lens, positions,
+                                row_map, pool_lens, new_k, new_v, new_stride_row, new_stride_head, num_q_heads,
+                                num_kv_heads, head_dim, scale, plan_items, num_items_narrow, num_items_wide,
+                                plan_merges, num_merges, partials, partials_floats, merge_counters, nullptr,
+                                stream);
+}
+
+extern "C" int mf_paged_attention_counted(
+    const void* q, int64_t q_stride_row, int64_t q_stride_head, void* out, int64_t out_stride_row,
+    int64_t out_stride_head, int dtype, const void* k_pool, const void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head, int block_size,
+    const int32_t* block_tables, int64_t block_table_stride, const int32_t* cu_seqlens,
+    const int32_t* kv_lens, const int64_t* positions, const int32_t* row_map,
+    const int32_t* pool_lens, const void* new_k, const void* new_v, int64_t new_stride_row,
+    int64_t new_stride_head, int num_q_heads, int num_kv_heads, int head_dim, float scale,
+    const int32_t* plan_items, int64_t capacity_narrow, int64_t capacity_wide,
+    const int32_t* plan_merges, int64_t capacity_merges, const int32_t* device_counts, float* partials,
+    int64_t partials_floats, mf_stream_t stream) {
+    if (!device_counts) return MF_ERR_ARG;
+    return paged_attention_impl(q, q_stride_row, q_stride_head, out, out_stride_row, out_stride_head, dtype,
+                                k_pool, v_pool, pool_stride_block, pool_stride_slot, pool_stride_head,
+                                block_size, block_tables, block_table_stride, cu_seqlens, kv_lens, positions,
+                                row_map, pool_lens, new_k, new_v, new_stride_row, new_stride_head, num_q_heads,
+                                num_kv_heads, head_dim, scale, plan_items, capacity_narrow, capacity_wide,
+                                plan_merges, capacity_merges, partials, partials_floats, nullptr,
+                                device_counts, stream);
 }

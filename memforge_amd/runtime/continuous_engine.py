@@ -49,6 +49,7 @@ from memforge_amd.runtime.batched_speculative import (
     scatter_accepted_kv,
     verify_candidates_batched,
 )
+from memforge_amd.runtime.graphed_paged_decode import GraphedPagedDecoder
 from memforge_amd.runtime.kv_pool import ModelKVSpec, PagedKVPool
 from memforge_amd.runtime.prefix_sharing import block_owners, copy_block, sharing_telemetry
 from memforge_amd.runtime.sampling import SamplingParams, sample_logits
@@ -224,6 +225,15 @@ class ContinuousBatchingEngine:
         if not attention_backend.register():
             raise RuntimeError("the transformers attention registry is required")
         self._staging = _Staging(self.device)
+        # Pure-decode steps replay a captured HIP graph of the packed pass
+        # (False | True | "auto", as the reference's paged_cuda_graph; "auto"
+        # is on whenever the model's head grouping allows it).
+        self._paged_graph = None
+        if paged_cuda_graph:
+            hq, hkv = model.config.num_attention_heads, self.spec.num_kv_heads
+            if paged_cuda_graph != "auto" or (hq % hkv == 0 and hq // hkv <= 16):
+                self._paged_graph = GraphedPagedDecoder(model, self.pool, max_batch=max_num_seqs,
+                                                        max_model_len=max_model_len)
 
         self.eos_token_ids = self._resolve_eos_ids()
         self.runtimes: Dict[int, SequenceRuntime] = {}
@@ -277,6 +287,7 @@ class ContinuousBatchingEngine:
             "prefix_sharing": self.prefix_cache is not None,
             "decode_view_cache": False,
             "block_attention": True,
+            "paged_cuda_graph": self._paged_graph is not None,
             "max_prefill_tokens_per_step": self.max_prefill_tokens_per_step,
             "chunked_prefill": self.max_prefill_tokens_per_step > 0,
             "eos_token_ids": sorted(self.eos_token_ids),
@@ -382,7 +393,9 @@ class ContinuousBatchingEngine:
             else:
                 plan.append({"rt": rt, "kind": "decode", "tokens": [rt.tokens[-1]],
                              "start": rt.cache.position, "table": rt.cache.block_table})
-        if plan:
+        if plan and n_prefill == 0 and self._paged_graph is not None:
+            events.extend(self._run_graphed(plan))
+        elif plan:
             events.extend(self._run_packed(plan))
             if n_prefill and len(plan) > n_prefill:
                 self.total_fused_steps += 1
@@ -516,10 +529,27 @@ class ContinuousBatchingEngine:
         self.total_attended_kv_tokens += int(sum(kv_lens))
         self.total_packed_rows += T
 
-        logits = out.logits[0]  # (len(emit), vocab)
+        return self._emit(plan, emit, out.logits[0])
+
+    def _run_graphed(self, plan: List[dict]) -> List[TokenEvent]:
+        """A decode-only step as one replay of the captured packed pass."""
+        ctx = [e["start"] for e in plan]
+        logits = self._paged_graph.logits_view([e["tokens"][0] for e in plan], ctx, [e["table"] for e in plan])
+        self.total_forward_passes += 1
+        self.total_blockwise_layers += self.spec.num_layers
+        self.total_fused_tokens += len(plan)
+        self.total_attended_kv_tokens += sum(c + 1 for c in ctx)
+        self.total_packed_rows += len(plan)
+        return self._emit(plan, list(range(len(plan))), logits)
+
+    def _emit(self, plan: List[dict], emit: List[int], logits: torch.Tensor) -> List[TokenEvent]:
+        """Sample one token for each entry in ``emit`` (indices into ``plan``,
+        rows of ``logits``) and do every entry's bookkeeping."""
         greedy = [j for j, i in enumerate(emit) if plan[i]["rt"].params.temperature <= 0.0]
         tokens: Dict[int, int] = {}
-        if greedy:
+        if len(greedy) == len(emit):  # one device argmax, one copy to the host
+            tokens = dict(enumerate(logits.argmax(dim=-1).tolist()))
+        elif greedy:
             idx = torch.tensor(greedy, dtype=torch.long).to(self.device)
             for j, tok in zip(greedy, logits.index_select(0, idx).argmax(dim=-1).tolist()):
                 tokens[j] = int(tok)
@@ -741,6 +771,9 @@ class ContinuousBatchingEngine:
                                       if self.total_draft_tokens_proposed else 0.0),
             "decode_view_cache_enabled": False,
             "block_attention_enabled": True,
+            "paged_cuda_graph_enabled": self._paged_graph is not None,
+            "graph_replays": self._paged_graph.replays if self._paged_graph is not None else 0,
+            "graph_captures": self._paged_graph.captures if self._paged_graph is not None else 0,
             "blockwise_layer_calls": self.total_blockwise_layers,
             "blockwise_fallbacks": self.total_blockwise_fallbacks,
             "attended_kv_tokens": self.total_attended_kv_tokens,

@@ -264,3 +264,73 @@ def test_speculative_output_is_identical_to_plain_greedy(model, draft, tok):
     spec.step()
     assert spec.allocator.get_num_free_blocks() == spec.allocator.get_total_blocks()
     assert spec.total_speculative_sequence_rounds >= spec.total_speculative_rounds
+
+
+# ------------------------------------------------------------- graphed decode
+
+
+def test_graphed_decoder_step_equals_the_eager_packed_pass(model, device):
+    """GraphedPagedDecoder.step against the same decode run eagerly through
+    the varlen path, over many replays of two batch buckets with eager work
+    (pool writes, other replays) in between."""
+    from memforge_amd.kernels import attention_backend
+    from memforge_amd.runtime.graphed_paged_decode import GraphedPagedDecoder
+    from memforge_amd.runtime.kv_pool import ModelKVSpec, PagedKVPool
+    from memforge_amd.runtime.varlen_cache import VarlenPackedCache
+
+    spec = ModelKVSpec.from_config(model.config, torch.float32, "cuda:0")
+    pool = PagedKVPool(spec, num_blocks=96, block_size=16)
+    gen = torch.Generator().manual_seed(5)
+    pool.key_pool.copy_(torch.randn(pool.key_pool.shape, generator=gen).to(device))
+    pool.value_pool.copy_(torch.randn(pool.value_pool.shape, generator=gen).to(device))
+    dec = GraphedPagedDecoder(model, pool, max_batch=8, max_model_len=256)
+    perm = torch.randperm(96, generator=gen).tolist()
+    tables = [perm[i * 12:(i + 1) * 12] for i in range(6)]
+    for step in range(6):
+        n = 3 if step % 2 == 0 else 6
+        ctx = [20 + 7 * i + step for i in range(n)]
+        toks = [(11 * i + step) % 250 + 2 for i in range(n)]
+        want_pool_k = pool.key_pool.clone()
+        want_pool_v = pool.value_pool.clone()
+        got = dec.step(toks, ctx, tables[:n])
+        # eager reference on a copy of the pool as it was before the step
+        got_pool_k, got_pool_v = pool.key_pool.clone(), pool.value_pool.clone()
+        pool.key_pool.copy_(want_pool_k)
+        pool.value_pool.copy_(want_pool_v)
+        cache = VarlenPackedCache(pool, 2, [torch.tensor(t) for t in tables[:n]], list(range(n)), ctx)
+        with attention_backend.backend_enabled_on(model):
+            with attention_backend.varlen_attention_context(pool, [torch.tensor(t) for t in tables[:n]],
+                                                            list(range(n)), ctx):
+                with torch.no_grad():
+                    ref = model(input_ids=torch.tensor([toks], device=device),
+                                position_ids=torch.tensor([ctx], device=device), past_key_values=cache,
+                                use_cache=True).logits[0]
+        torch.testing.assert_close(got, ref, atol=2e-5, rtol=1e-4)
+        assert torch.equal(got_pool_k, pool.key_pool) and torch.equal(got_pool_v, pool.value_pool)
+    assert dec.captures == 2 and dec.replays == 6
+
+
+def test_graphed_engine_output_equals_eager(model, tok):
+    prompts = PROMPTS + ["five", "a sixth prompt that is rather long indeed, for padding"]
+    eager = make_engine(model, tok, num_blocks=128, max_num_seqs=8)
+    graphed = make_engine(model, tok, num_blocks=128, max_num_seqs=8, paged_cuda_graph=True)
+    a = eager.generate(prompts, greedy(12, stop_on_eos=False))
+    b = graphed.generate(prompts, greedy(12, stop_on_eos=False))
+    for x, y, exp in zip(a, b, expected(model, tok, prompts, 12, stop_on_eos=False)):
+        assert x["token_ids"] == y["token_ids"] == exp
+    t = graphed.telemetry()
+    assert t["paged_cuda_graph_enabled"] and t["graph_replays"] > 5 and t["graph_captures"] >= 1
+    # staggered arrivals: graph replays interleave with eager prefill steps
+    from memforge_amd.runtime.sampling import SamplingParams
+
+    g2 = make_engine(model, tok, num_blocks=128, max_num_seqs=8, paged_cuda_graph="auto")
+    ids = []
+    for p in prompts:
+        ids.append(g2.submit(p, SamplingParams(max_new_tokens=10, temperature=0.0, stop_on_eos=False)))
+        g2.step()
+        g2.step()
+    g2.run_until_idle()
+    for i, p in zip(ids, prompts):
+        assert g2.runtimes[i].generated == hf_greedy(model, tok(p)["input_ids"], 10, stop_on_eos=False)
+    g2.step()
+    assert g2.allocator.get_num_free_blocks() == g2.allocator.get_total_blocks()

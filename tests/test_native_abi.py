@@ -63,7 +63,8 @@ def test_plan_covers_every_tile_exactly_once_and_merges_line_up(dtype, d, pt):
     cover = {}
     slots = {}
     for it in items:
-        s, h, c0, nct, kt0, kt1, slot, merge = (int(x) for x in it)
+        s, h, c0, nct, kt0, kt1, slot, merge, row0, nrows, kvl = (int(x) for x in it[:11])
+        assert (row0, nrows, kvl) == (cu[s], q_lens[s], kv[s]), "item carries its sequence's bounds"
         assert kt1 > kt0 and kt1 - kt0 <= 64
         for c in range(c0, c0 + nct):
             for kt in range(kt0, kt1):
@@ -87,7 +88,8 @@ def test_plan_covers_every_tile_exactly_once_and_merges_line_up(dtype, d, pt):
     # each merge record reads exactly the partial slots of its (s, h, column)
     seen = set()
     for m in merges:
-        s, h, c, nparts, slot0, stride = (int(x) for x in m[:6])
+        s, h, c, nparts, slot0, stride, row0, nrows = (int(x) for x in m[:8])
+        assert (row0, nrows) == (cu[s], q_lens[s])
         want = sorted(sl for sl, owner in slots.items() if owner == (s, h, c))
         got = sorted(slot0 + j * stride for j in range(nparts))
         assert got == want and nparts > 1
