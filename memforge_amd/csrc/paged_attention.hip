@@ -35,6 +35,9 @@ typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
 
+#ifndef MF_DECODE_DEPTH
+#define MF_DECODE_DEPTH 3  // key tiles in flight per decode wave (3 or 4)
+#endif
 constexpr int kWaves = 4;  // waves per workgroup; each wave runs its own item
 constexpr int kMaxItemTiles = 64;  // key tiles per work item (one block-table entry per lane)
 
@@ -121,6 +124,31 @@ __device__ __forceinline__ void ld_words(const char* p, uint32_t* w) {
 #pragma unroll
         for (int k = 0; k < N / 16; ++k) {
             const uint4 v = *(const uint4*)(p + 16 * k);
+            w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
+        }
+    }
+}
+
+// The same loads marked non-temporal (streamed, not kept in cache): pool
+// tiles of single-column-tile items are read by exactly one wave.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_nt16(const char* p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <int N>
+__device__ __forceinline__ void ld_words_nt(const char* p, uint32_t* w) {
+    if constexpr (N == 4) {
+        w[0] = __builtin_nontemporal_load((const uint32_t*)p);
+    } else if constexpr (N == 8) {
+        const u32x2 v = __builtin_nontemporal_load((const u32x2*)p);
+        w[0] = v.x; w[1] = v.y;
+    } else {
+        static_assert(N % 16 == 0, "chunk");
+#pragma unroll
+        for (int k = 0; k < N / 16; ++k) {
+            const uint4 v = ld_nt16(p + 16 * k);
             w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
         }
     }
@@ -391,10 +419,17 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
             const char* kb = a.k_pool + boff;
             const char* vb = a.v_pool + boff;
+            if constexpr (NT == 1) {
 #pragma unroll
-            for (int c = 0; c < NL; ++c) kf[c] = *(const uint4*)(kb + k_lane_off + c * 4 * 16);
+                for (int c = 0; c < NL; ++c) kf[c] = ld_nt16(kb + k_lane_off + c * 4 * 16);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) ld_words<VB>(vb + v_lane_off + r * v_row_bytes, vf[r]);
+                for (int r = 0; r < 4; ++r) ld_words_nt<VB>(vb + v_lane_off + r * v_row_bytes, vf[r]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < NL; ++c) kf[c] = *(const uint4*)(kb + k_lane_off + c * 4 * 16);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ld_words<VB>(vb + v_lane_off + r * v_row_bytes, vf[r]);
+            }
         } else {
             load_general(kt, kf, vf);
         }
@@ -495,6 +530,26 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         int kt = kt0;
         load_tile(kt, kA, vA);
         if constexpr (FAST && NT == 1) {
+#if MF_DECODE_DEPTH == 4
+            uint4 kC[NL], kD[NL];
+            uint32_t vC[4][VWD], vD[4][VWD];
+            load_tile(min(kt + 1, last), kB, vB);
+            load_tile(min(kt + 2, last), kC, vC);
+            for (;;) {
+                load_tile(min(kt + 3, last), kD, vD);
+                process(kt, kA, vA);
+                if (++kt > last) break;
+                load_tile(min(kt + 3, last), kA, vA);
+                process(kt, kB, vB);
+                if (++kt > last) break;
+                load_tile(min(kt + 3, last), kB, vB);
+                process(kt, kC, vC);
+                if (++kt > last) break;
+                load_tile(min(kt + 3, last), kC, vC);
+                process(kt, kD, vD);
+                if (++kt > last) break;
+            }
+#else
             uint4 kC[NL];
             uint32_t vC[4][VWD];
             load_tile(min(kt + 1, last), kB, vB);
@@ -509,6 +564,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 process(kt, kC, vC);
                 if (++kt > last) break;
             }
+#endif
         } else {
             for (;;) {
                 load_tile(min(kt + 1, last), kB, vB);
