@@ -280,8 +280,17 @@ def run_kv_write_large(dev, tokens=33792, reps=20):
     torch.cuda.synchronize()
     us = _event_us(evs)
     nbytes = tokens * SM_HKV * SM_D * 2 * 2 * 2 + tokens * 8
+    kg, vg = torch.empty_like(k), torch.empty_like(v)
+    gevs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in gevs:
+        a.record()
+        nat.kv_gather(view, perm, kg, vg)
+        b.record()
+    torch.cuda.synchronize()
+    gus = _event_us(gevs)
     return {"tokens": tokens, "us": round(us, 2), "gbps": round(nbytes / us / 1e3, 1),
-            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4)}
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4),
+            "gather_us": round(gus, 2), "gather_gbps": round(nbytes / gus / 1e3, 1)}
 
 
 def run_c3(dev, layers=SM_LAYERS, reps=3):

@@ -11,42 +11,54 @@
 namespace mf {
 namespace {
 
-// Loads N bytes (N in {2,4,8,16,32}) into 32-bit words.
-template <int N>
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Loads N bytes (N in {2,4,8,16,32}) into 32-bit words; NT marks the loads
+// non-temporal (measured slower for the 128-byte pool rows of a gather, so
+// the gather does not use it).
+template <int N, bool NT = false>
 __device__ __forceinline__ void load_words(const char* p, uint32_t* w) {
     if constexpr (N == 2) {
-        w[0] = *(const uint16_t*)p;
+        w[0] = NT ? __builtin_nontemporal_load((const uint16_t*)p) : *(const uint16_t*)p;
     } else if constexpr (N == 4) {
-        w[0] = *(const uint32_t*)p;
+        w[0] = NT ? __builtin_nontemporal_load((const uint32_t*)p) : *(const uint32_t*)p;
     } else if constexpr (N == 8) {
-        uint2 v = *(const uint2*)p;
+        const u32x2 v = NT ? __builtin_nontemporal_load((const u32x2*)p) : *(const u32x2*)p;
         w[0] = v.x; w[1] = v.y;
-    } else if constexpr (N == 16) {
-        uint4 v = *(const uint4*)p;
-        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
     } else {
-        static_assert(N == 32, "chunk size");
-        uint4 a = *(const uint4*)p;
-        uint4 b = *(const uint4*)(p + 16);
-        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-        w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+        static_assert(N == 16 || N == 32, "chunk size");
+#pragma unroll
+        for (int k = 0; k < N / 16; ++k) {
+            const u32x4 v = NT ? __builtin_nontemporal_load((const u32x4*)(p + 16 * k)) : *(const u32x4*)(p + 16 * k);
+            w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
+        }
     }
 }
 
-template <int N>
+// Stores 32-bit words as N bytes; NT marks the stores non-temporal (measured
+// slower for the pool side of a write on MI355X, so the write path does not
+// use it).
+template <int N, bool NT = false>
 __device__ __forceinline__ void store_words(char* p, const uint32_t* w) {
     if constexpr (N == 2) {
-        *(uint16_t*)p = (uint16_t)w[0];
+        if (NT) __builtin_nontemporal_store((uint16_t)w[0], (uint16_t*)p);
+        else *(uint16_t*)p = (uint16_t)w[0];
     } else if constexpr (N == 4) {
-        *(uint32_t*)p = w[0];
+        if (NT) __builtin_nontemporal_store(w[0], (uint32_t*)p);
+        else *(uint32_t*)p = w[0];
     } else if constexpr (N == 8) {
-        *(uint2*)p = make_uint2(w[0], w[1]);
-    } else if constexpr (N == 16) {
-        *(uint4*)p = make_uint4(w[0], w[1], w[2], w[3]);
+        const u32x2 v = {w[0], w[1]};
+        if (NT) __builtin_nontemporal_store(v, (u32x2*)p);
+        else *(u32x2*)p = v;
     } else {
-        static_assert(N == 32, "chunk size");
-        *(uint4*)p = make_uint4(w[0], w[1], w[2], w[3]);
-        *(uint4*)(p + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+        static_assert(N == 16 || N == 32, "chunk size");
+#pragma unroll
+        for (int k = 0; k < N / 16; ++k) {
+            const u32x4 v = {w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]};
+            if (NT) __builtin_nontemporal_store(v, (u32x4*)(p + 16 * k));
+            else *(u32x4*)(p + 16 * k) = v;
+        }
     }
 }
 
@@ -65,15 +77,16 @@ __device__ __forceinline__ void set_elem(uint32_t* w, int e, uint32_t v) {
     }
 }
 
-// Copies VW elements from `src` (dtype SDT) to `dst` (dtype DDT).
-template <int SDT, int DDT, int VW>
+// Copies VW elements from `src` (dtype SDT) to `dst` (dtype DDT); NT_LOAD /
+// NT_STORE mark the pool side non-temporal.
+template <int SDT, int DDT, int VW, bool NT_LOAD, bool NT_STORE>
 __device__ __forceinline__ void copy_chunk(const char* src, char* dst) {
     constexpr int SES = SDT == MF_F32 ? 4 : 2;
     constexpr int DES = DDT == MF_F32 ? 4 : 2;
     uint32_t in[(VW * SES + 3) / 4];
-    load_words<VW * SES>(src, in);
+    load_words<VW * SES, NT_LOAD>(src, in);
     if constexpr (SDT == DDT) {
-        store_words<VW * DES>(dst, in);
+        store_words<VW * DES, NT_STORE>(dst, in);
     } else {
         uint32_t out[(VW * DES + 3) / 4] = {};
 #pragma unroll
@@ -81,7 +94,7 @@ __device__ __forceinline__ void copy_chunk(const char* src, char* dst) {
             const float f = bits_to_f32<SDT>(get_elem<SES>(in, e));
             set_elem<DES>(out, e, f32_to_bits<DDT>(f));
         }
-        store_words<VW * DES>(dst, out);
+        store_words<VW * DES, NT_STORE>(dst, out);
     }
 }
 
@@ -118,11 +131,11 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(CopyArgs a) {
         const int64_t pe = blk * a.p_sb + off * a.p_ss + (int64_t)h * a.p_sh + (int64_t)c * VW;
         const int64_t re = t * a.row_st + (int64_t)h * a.row_sh + (int64_t)c * VW;
         if constexpr (!GATHER) {
-            copy_chunk<RDT, PDT, VW>(a.row_k + re * RES, a.pool_k + pe * PES);
-            copy_chunk<RDT, PDT, VW>(a.row_v + re * RES, a.pool_v + pe * PES);
+            copy_chunk<RDT, PDT, VW, false, false>(a.row_k + re * RES, a.pool_k + pe * PES);
+            copy_chunk<RDT, PDT, VW, false, false>(a.row_v + re * RES, a.pool_v + pe * PES);
         } else {
-            copy_chunk<PDT, RDT, VW>(a.pool_k + pe * PES, (char*)a.row_k + re * RES);
-            copy_chunk<PDT, RDT, VW>(a.pool_v + pe * PES, (char*)a.row_v + re * RES);
+            copy_chunk<PDT, RDT, VW, false, false>(a.pool_k + pe * PES, (char*)a.row_k + re * RES);
+            copy_chunk<PDT, RDT, VW, false, false>(a.pool_v + pe * PES, (char*)a.row_v + re * RES);
         }
     }
 }

@@ -419,7 +419,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
             const char* kb = a.k_pool + boff;
             const char* vb = a.v_pool + boff;
-            if constexpr (NT == 1) {
+            if constexpr (NT == 1 && DP * ES >= 256) {
+                // non-temporal only for rows of 256 bytes or more: measured
+                // faster there (bf16 D 128) and slower for 128-byte rows
 #pragma unroll
                 for (int c = 0; c < NL; ++c) kf[c] = ld_nt16(kb + k_lane_off + c * 4 * 16);
 #pragma unroll
