@@ -52,8 +52,22 @@ __device__ __forceinline__ uint32_t f32_to_bits(float f) {
 }
 
 // ------------------------------------------------------------ wave helpers
-__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
-    return __shfl_xor(v, mask, 64);
+// Reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32,
+// l^48) in registers, with gfx950's lane-swap instructions instead of an LDS
+// permute. With both operands equal to x, v_permlane16_swap returns
+// (x.g0, x.g0, x.g2, x.g2) and (x.g1, x.g1, x.g3, x.g3) -- each lane's
+// xor-16 pair -- and v_permlane32_swap likewise each lane's xor-32 pair.
+__device__ __forceinline__ float group_max4(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float group_sum4(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 }  // namespace mf

@@ -468,8 +468,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                     sv[r] = vis ? st[r] * a.scale_log2 : kNegInf;
                     bm = fmaxf(bm, sv[r]);
                 }
-                bm = fmaxf(bm, shfl_xor_f(bm, 16));
-                bm = fmaxf(bm, shfl_xor_f(bm, 32));
+                bm = group_max4(bm);
                 const float mn = fmaxf(m[nt], bm);
                 const float mu = mn == kNegInf ? 0.f : mn;
                 const float alpha = exp2f(m[nt] - mu);
@@ -591,8 +590,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int dbase = 4 * g * VCH;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        float lt = l[nt] + shfl_xor_f(l[nt], 16);
-        lt += shfl_xor_f(lt, 32);
+        const float lt = group_sum4(l[nt]);
         if (nt >= nct || qpos[nt] < 0) continue;
         if (pslot < 0) {
             if (dbase < D) {
