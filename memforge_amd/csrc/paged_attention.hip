@@ -21,6 +21,7 @@
 // (max, sum, unnormalised output) triples go to fp32 scratch and a merge
 // kernel combines them with the log-sum-exp rule.
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <vector>
 
@@ -30,21 +31,23 @@ namespace mf {
 namespace {
 
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
 
-#ifndef MF_DECODE_DEPTH
-#define MF_DECODE_DEPTH 3  // key tiles in flight per decode wave (3 or 4)
-#endif
 constexpr int kWaves = 4;  // waves per workgroup; each wave runs its own item
 constexpr int kMaxItemTiles = 64;  // key tiles per work item (one block-table entry per lane)
+constexpr float kLazyLog2 = 8.f;  // running-max slack of the online softmax (log2 units)
 
 // 16-column tiles one wave carries for multi-tile (prefill / wide verify)
 // items: as many as fit in registers without spilling.
 __host__ __device__ constexpr int wide_tiles(int dt, int dp) {
-    return dt == MF_F32 ? (dp >= 128 ? 2 : 4) : (dp >= 256 ? 1 : 4);
+    // measured on MI355X: 2 tiles beat 4 for 16-bit head_dim 64 (more waves
+    // per SIMD outweigh the K/V reuse across columns)
+    return dt == MF_F32 ? (dp >= 128 ? 2 : 4) : (dp >= 256 ? 1 : (dp == 64 ? 2 : 4));
 }
 
 struct AttnArgs {
@@ -271,8 +274,18 @@ __device__ __forceinline__ void merge_tile(const AttnArgs& a, const int32_t* mg,
 }
 
 // -------------------------------------------------------------- main kernel
+// Waves per SIMD the register allocator must leave room for: two where the
+// kernel fits in 256 registers without spilling (key rows up to 128 bytes,
+// or up to 256 bytes for single-tile items), else one.
+template <int DT, int DP, int NT>
+constexpr int attn_waves_per_eu() {
+    constexpr int row_bytes = DP * (DT == MF_F32 ? 4 : 2);
+    return (row_bytes <= 128 || (row_bytes <= 256 && NT == 1)) ? 2 : 1;
+}
+
 template <int DT, int DP, int NT, bool FAST>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<DT, DP, NT>())))
+void attn_kernel(AttnArgs a) {
     constexpr int ES = DT == MF_F32 ? 4 : 2;
     constexpr int EPL = 16 / ES;      // elements per 16-byte chunk
     constexpr int NL = DP * ES / 64;  // 16-byte K/Q chunks per lane
@@ -304,6 +317,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     // ---- columns owned by this lane (one per tile)
     int prow[NT], qhead[NT], qpos[NT];
     int maxpos = -1;
+    int minpos = INT_MAX;  // over the item's real columns
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const int cidx = (c0 + nt) * 16 + j;
@@ -320,9 +334,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         qhead[nt] = h * a.G + gq;
         qpos[nt] = pos;
         maxpos = max(maxpos, pos);
+        if (valid) minpos = min(minpos, pos);
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) maxpos = max(maxpos, __shfl_xor(maxpos, off, 64));
+    for (int off = 32; off >= 1; off >>= 1) {
+        maxpos = max(maxpos, __shfl_xor(maxpos, off, 64));
+        minpos = min(minpos, __shfl_xor(minpos, off, 64));
+    }
     // Tiles past the last key any column may see are never read.
     int kt_end = min(kt1, (min(maxpos, kv_len - 1) >> 4) + 1);
     if (maxpos < 0 || kv_len <= 0) kt_end = kt0;
@@ -452,36 +470,71 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
         uint2 p16[NT];
         float p32[NT][4];
+        // Every key of a tile wholly inside the context and at or before every
+        // column's position is visible to all columns: no mask to apply.
+        const bool open = kt * 16 + 15 <= minpos && (kt + 1) * 16 <= kv_len;
+        // Phases over all column tiles at once (QK MFMAs, then scores and
+        // maxima, one rescale decision, then exponentials) so the scheduler
+        // can overlap one tile's MFMAs with another tile's vector work.
+        f32x4 st[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            st[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (nt < nct) {
+#pragma unroll
+                for (int c = 0; c < NL; ++c) st[nt] = mfma_qk<DT>(kf[c], qf[nt][c], st[nt]);
+            }
+        }
+        // lane (g, j) holds S^T[keys 4g..4g+3][column j] of every tile
+        float sv[NT][4], bm[NT];
+        bool grow = false;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            bm[nt] = kNegInf;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = kt * 16 + 4 * g + r;
+                const bool vis = open || (key <= qpos[nt] && key < kv_len);
+                sv[nt][r] = vis ? st[nt][r] * a.scale_log2 : kNegInf;
+                bm[nt] = fmaxf(bm[nt], sv[nt][r]);
+            }
+            bm[nt] = group_max4(bm[nt]);
+            grow |= nt < nct && bm[nt] > m[nt] + kLazyLog2;
+        }
+        // Lazy rescaling: the running max m moves (and l, acc are rescaled)
+        // only when some column's tile max exceeds it by more than
+        // kLazyLog2, so p = 2^(s - m) stays below 2^kLazyLog2; l and acc
+        // always share the m they were built with, so the result is the same
+        // softmax.
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                if (nt < nct) {
+                    const float mn = fmaxf(m[nt], bm[nt]);
+                    const float alpha = __builtin_amdgcn_exp2f(m[nt] - (mn == kNegInf ? 0.f : mn));
+                    l[nt] *= alpha;
+#pragma unroll
+                    for (int c = 0; c < VCH; ++c) acc[nt][c] *= alpha;
+                    m[nt] = mn;
+                }
+            }
+        }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             if (nt < nct) {
-                f32x4 st = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int c = 0; c < NL; ++c) st = mfma_qk<DT>(kf[c], qf[nt][c], st);
-                // lane (g, j) now holds S^T[keys 4g..4g+3][column j]
-                float sv[4];
-                float bm = kNegInf;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int key = kt * 16 + 4 * g + r;
-                    const bool vis = key <= qpos[nt] && key < kv_len;
-                    sv[r] = vis ? st[r] * a.scale_log2 : kNegInf;
-                    bm = fmaxf(bm, sv[r]);
-                }
-                bm = group_max4(bm);
-                const float mn = fmaxf(m[nt], bm);
-                const float mu = mn == kNegInf ? 0.f : mn;
-                const float alpha = exp2f(m[nt] - mu);
+                const float mu = m[nt] == kNegInf ? 0.f : m[nt];
                 float p[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) p[r] = exp2f(sv[r] - mu);
-                l[nt] = l[nt] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-                m[nt] = mn;
-#pragma unroll
-                for (int c = 0; c < VCH; ++c) acc[nt][c] *= alpha;
+                for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(sv[nt][r] - mu);
+                l[nt] += (p[0] + p[1]) + (p[2] + p[3]);
                 if constexpr (DT == MF_F32) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) p32[nt][r] = p[r];
+                } else if constexpr (DT == MF_BF16) {
+                    // hardware round-to-nearest-even pack (v_cvt_pk_bf16_f32)
+                    p16[nt] = make_uint2(
+                        __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){p[0], p[1]}, bf16x2)),
+                        __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){p[2], p[3]}, bf16x2)));
                 } else {
                     p16[nt] = make_uint2(f32_to_bits<DT>(p[0]) | (f32_to_bits<DT>(p[1]) << 16),
                                          f32_to_bits<DT>(p[2]) | (f32_to_bits<DT>(p[3]) << 16));
@@ -531,26 +584,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         int kt = kt0;
         load_tile(kt, kA, vA);
         if constexpr (FAST && NT == 1) {
-#if MF_DECODE_DEPTH == 4
-            uint4 kC[NL], kD[NL];
-            uint32_t vC[4][VWD], vD[4][VWD];
-            load_tile(min(kt + 1, last), kB, vB);
-            load_tile(min(kt + 2, last), kC, vC);
-            for (;;) {
-                load_tile(min(kt + 3, last), kD, vD);
-                process(kt, kA, vA);
-                if (++kt > last) break;
-                load_tile(min(kt + 3, last), kA, vA);
-                process(kt, kB, vB);
-                if (++kt > last) break;
-                load_tile(min(kt + 3, last), kB, vB);
-                process(kt, kC, vC);
-                if (++kt > last) break;
-                load_tile(min(kt + 3, last), kC, vC);
-                process(kt, kD, vD);
-                if (++kt > last) break;
-            }
-#else
             uint4 kC[NL];
             uint32_t vC[4][VWD];
             load_tile(min(kt + 1, last), kB, vB);
@@ -565,7 +598,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                 process(kt, kC, vC);
                 if (++kt > last) break;
             }
-#endif
         } else {
             for (;;) {
                 load_tile(min(kt + 1, last), kB, vB);
