@@ -57,11 +57,14 @@ __device__ __forceinline__ uint32_t f32_to_bits(float f) {
 // permute. With both operands equal to x, v_permlane16_swap returns
 // (x.g0, x.g0, x.g2, x.g2) and (x.g1, x.g1, x.g3, x.g3) -- each lane's
 // xor-16 pair -- and v_permlane32_swap likewise each lane's xor-32 pair.
+// The maxima use the NaN-propagating maximum (one v_maximum3_f32, no
+// operand canonicalisation), as a softmax over a NaN score is NaN anyway.
+__device__ __forceinline__ float fmax_prop(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float group_max4(float v) {
     auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    v = fmax_prop(__uint_as_float(a[0]), __uint_as_float(a[1]));
     auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    return fmax_prop(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float group_sum4(float v) {
     auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);

@@ -21,6 +21,7 @@
 // (max, sum, unnormalised output) triples go to fp32 scratch and a merge
 // kernel combines them with the log-sum-exp rule.
 #include <algorithm>
+#include <array>
 #include <climits>
 #include <cmath>
 #include <vector>
@@ -40,7 +41,16 @@ typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
 
 constexpr int kWaves = 4;  // waves per workgroup; each wave runs its own item
 constexpr int kMaxItemTiles = 64;  // key tiles per work item (one block-table entry per lane)
+#ifndef MF_NARROW_ITEMS
+#define MF_NARROW_ITEMS 8192  // planner: target item count that sets the narrow key partition
+#endif
+#ifndef MF_WIDE_ITEMS
+#define MF_WIDE_ITEMS 4096  // planner: most wide items before partitions grow
+#endif
 constexpr float kLazyLog2 = 8.f;  // running-max slack of the online softmax (log2 units)
+// Running maximum before any key is seen: finite, so exponent arguments never
+// need a -inf guard; 2^(kMinM - x) is 0 for every score x.
+constexpr float kMinM = -1e30f;
 
 // 16-column tiles one wave carries for multi-tile (prefill / wide verify)
 // items: as many as fit in registers without spilling.
@@ -71,7 +81,9 @@ struct AttnArgs {
     int64_t n_sr, n_sh;
     int G;
     int head_dim;
-    float scale_log2;
+    float scale_log2;    // |scale| * log2(e), > 0
+    float inv_scale_log2;
+    uint32_t q_sign;     // xor applied to every Q word: flips the sign for a negative scale
     const int32_t* items;
     int num_items;
     const int32_t* dev_count;  // when set, the live item / merge count (the grid is a capacity)
@@ -115,6 +127,7 @@ __device__ __forceinline__ f32x4 mfma_pv16(uint2 a, uint2 b, f32x4 c) {
 }
 
 // ---------------------------------------------------------- memory helpers
+
 template <int N>
 __device__ __forceinline__ void ld_words(const char* p, uint32_t* w) {
     if constexpr (N == 4) {
@@ -297,7 +310,8 @@ void attn_kernel(AttnArgs a) {
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int item = blockIdx.x * kWaves + wave;
-    if (item >= (a.dev_count ? *a.dev_count : a.num_items)) return;
+    const int num_items = a.dev_count ? *a.dev_count : a.num_items;
+    if (item >= num_items) return;
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4;  // 16-lane group: MFMA k-group / output row group
     const int j = lane & 15;  // MFMA column (query column) and A-row (key) index
@@ -341,6 +355,11 @@ void attn_kernel(AttnArgs a) {
         maxpos = max(maxpos, __shfl_xor(maxpos, off, 64));
         minpos = min(minpos, __shfl_xor(minpos, off, 64));
     }
+    minpos = __builtin_amdgcn_readfirstlane(minpos);
+    // last key each lane's column may see (-1 for padding columns)
+    int lim[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) lim[nt] = qpos[nt] >= 0 ? min(qpos[nt], kv_len - 1) : -1;
     // Tiles past the last key any column may see are never read.
     int kt_end = min(kt1, (min(maxpos, kv_len - 1) >> 4) + 1);
     if (maxpos < 0 || kv_len <= 0) kt_end = kt0;
@@ -357,15 +376,18 @@ void attn_kernel(AttnArgs a) {
             uint4 v = make_uint4(0, 0, 0, 0);
             if (qpos[nt] >= 0 && d0 < D)
                 v = *(const uint4*)(a.q + ((int64_t)prow[nt] * a.q_sr + (int64_t)qhead[nt] * a.q_sh + d0) * ES);
-            qf[nt][c] = v;
+            qf[nt][c] = make_uint4(v.x ^ a.q_sign, v.y ^ a.q_sign, v.z ^ a.q_sign, v.w ^ a.q_sign);
         }
     }
 
-    float m[NT], l[NT];
+    // m: running max of the scaled scores (log2 units); thr: the raw score
+    // above which a column's running max must move, (m + kLazyLog2) / scale.
+    float m[NT], l[NT], thr[NT];
     f32x4 acc[NT][VCH];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        m[nt] = kNegInf;
+        m[nt] = kMinM;
+        thr[nt] = (kMinM + kLazyLog2) * a.inv_scale_log2;
         l[nt] = 0.f;
 #pragma unroll
         for (int c = 0; c < VCH; ++c) acc[nt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -455,90 +477,93 @@ void attn_kernel(AttnArgs a) {
         }
     };
 
+    // Per-tile work is branch-free apart from wave-uniform decisions: every
+    // column tile's MFMAs run (tiles past nct hold zero queries and are never
+    // stored), and masking is a select, so the scheduler sees one straight
+    // block per tile.
     auto process = [&](int kt, const uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
         if constexpr (FAST) {
             // Slots past the context in the last block may hold anything,
             // NaN included; p = 0 there, but 0 * NaN is NaN, so clear them.
             if ((kt + 1) * 16 > kv_len) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (kt * 16 + 4 * g + r >= kv_len) {
+                for (int r = 0; r < 4; ++r) {
+                    const bool live = kt * 16 + 4 * g + r < kv_len;
 #pragma unroll
-                        for (int w = 0; w < VWD; ++w) vf[r][w] = 0;
-                    }
+                    for (int w = 0; w < VWD; ++w) vf[r][w] = live ? vf[r][w] : 0u;
+                }
             }
         }
-        uint2 p16[NT];
-        float p32[NT][4];
-        // Every key of a tile wholly inside the context and at or before every
-        // column's position is visible to all columns: no mask to apply.
-        const bool open = kt * 16 + 15 <= minpos && (kt + 1) * 16 <= kv_len;
-        // Phases over all column tiles at once (QK MFMAs, then scores and
-        // maxima, one rescale decision, then exponentials) so the scheduler
-        // can overlap one tile's MFMAs with another tile's vector work.
+        // QK MFMAs of all column tiles first, then the rescale decision, then
+        // exponentials, so one tile's MFMAs overlap another tile's vector work.
+        // Scores stay raw; the scale is applied inside the exponent,
+        // p = 2^(s * scale - m), one fma.
         f32x4 st[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             st[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (nt < nct) {
 #pragma unroll
-                for (int c = 0; c < NL; ++c) st[nt] = mfma_qk<DT>(kf[c], qf[nt][c], st[nt]);
-            }
+            for (int c = 0; c < NL; ++c) st[nt] = mfma_qk<DT>(kf[c], qf[nt][c], st[nt]);
         }
         // lane (g, j) holds S^T[keys 4g..4g+3][column j] of every tile
-        float sv[NT][4], bm[NT];
+        float sv[NT][4];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sv[nt][r] = st[nt][r];
+        // Every key of a tile wholly inside the context and at or before every
+        // column's position is visible to all columns: no mask to apply.
+        if (!(kt * 16 + 15 <= minpos && (kt + 1) * 16 <= kv_len)) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sv[nt][r] = kt * 16 + 4 * g + r <= lim[nt] ? sv[nt][r] : kNegInf;
+        }
+        // Lazy rescaling: a column's running max m moves (and l, acc are
+        // rescaled) only when one of its scores exceeds m by more than
+        // kLazyLog2, so p = 2^(s - m) stays below 2^kLazyLog2; l and acc always
+        // share the m they were built with, so the result is the same softmax.
+        // Each lane tests its own four scores; the max across the column's
+        // four lane groups is only formed when some lane asks for a move.
+        float lmax[NT];
         bool grow = false;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            bm[nt] = kNegInf;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = kt * 16 + 4 * g + r;
-                const bool vis = open || (key <= qpos[nt] && key < kv_len);
-                sv[nt][r] = vis ? st[nt][r] * a.scale_log2 : kNegInf;
-                bm[nt] = fmaxf(bm[nt], sv[nt][r]);
-            }
-            bm[nt] = group_max4(bm[nt]);
-            grow |= nt < nct && bm[nt] > m[nt] + kLazyLog2;
+            lmax[nt] = fmax_prop(fmax_prop(sv[nt][0], sv[nt][1]), fmax_prop(sv[nt][2], sv[nt][3]));
+            grow |= lmax[nt] > thr[nt];
         }
-        // Lazy rescaling: the running max m moves (and l, acc are rescaled)
-        // only when some column's tile max exceeds it by more than
-        // kLazyLog2, so p = 2^(s - m) stays below 2^kLazyLog2; l and acc
-        // always share the m they were built with, so the result is the same
-        // softmax.
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-                if (nt < nct) {
-                    const float mn = fmaxf(m[nt], bm[nt]);
-                    const float alpha = __builtin_amdgcn_exp2f(m[nt] - (mn == kNegInf ? 0.f : mn));
-                    l[nt] *= alpha;
+                const float mn = fmaxf(m[nt], group_max4(lmax[nt]) * a.scale_log2);
+                const float alpha = __builtin_amdgcn_exp2f(m[nt] - mn);
+                l[nt] *= alpha;
 #pragma unroll
-                    for (int c = 0; c < VCH; ++c) acc[nt][c] *= alpha;
-                    m[nt] = mn;
-                }
+                for (int c = 0; c < VCH; ++c) acc[nt][c] *= alpha;
+                m[nt] = mn;
+                thr[nt] = (mn + kLazyLog2) * a.inv_scale_log2;
             }
         }
+        uint2 p16[NT];
+        float p32[NT][4];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            if (nt < nct) {
-                const float mu = m[nt] == kNegInf ? 0.f : m[nt];
-                float p[4];
+            float p[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(sv[nt][r] - mu);
-                l[nt] += (p[0] + p[1]) + (p[2] + p[3]);
-                if constexpr (DT == MF_F32) {
+            for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[nt][r], a.scale_log2, -m[nt]));
+            l[nt] += (p[0] + p[1]) + (p[2] + p[3]);
+            if constexpr (DT == MF_F32) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) p32[nt][r] = p[r];
-                } else if constexpr (DT == MF_BF16) {
-                    // hardware round-to-nearest-even pack (v_cvt_pk_bf16_f32)
-                    p16[nt] = make_uint2(
-                        __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){p[0], p[1]}, bf16x2)),
-                        __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){p[2], p[3]}, bf16x2)));
-                } else {
-                    p16[nt] = make_uint2(f32_to_bits<DT>(p[0]) | (f32_to_bits<DT>(p[1]) << 16),
-                                         f32_to_bits<DT>(p[2]) | (f32_to_bits<DT>(p[3]) << 16));
-                }
+                for (int r = 0; r < 4; ++r) p32[nt][r] = p[r];
+            } else if constexpr (DT == MF_BF16) {
+                // hardware round-to-nearest-even pack (v_cvt_pk_bf16_f32)
+                p16[nt] = make_uint2(
+                    __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){p[0], p[1]}, bf16x2)),
+                    __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){p[2], p[3]}, bf16x2)));
+            } else {
+                p16[nt] = make_uint2(f32_to_bits<DT>(p[0]) | (f32_to_bits<DT>(p[1]) << 16),
+                                     f32_to_bits<DT>(p[2]) | (f32_to_bits<DT>(p[3]) << 16));
             }
         }
         // O^T += V^T P^T, one MFMA per 16-row head_dim tile c: row i of tile c
@@ -551,22 +576,17 @@ void attn_kernel(AttnArgs a) {
                     const float va = __uint_as_float(vf[r][c]);
 #pragma unroll
                     for (int nt = 0; nt < NT; ++nt)
-                        if (nt < nct)
-                            acc[nt][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, p32[nt][r], acc[nt][c], 0, 0, 0);
+                        acc[nt][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, p32[nt][r], acc[nt][c], 0, 0, 0);
                 }
             } else {
+                // element c of keys 4g..4g+3: the low (c even) or high
+                // halves of word c/2, paired by byte permutes
                 const int wd = c >> 1;
-                uint2 va;
-                if ((c & 1) == 0) {
-                    va.x = (vf[0][wd] & 0xffffu) | (vf[1][wd] << 16);
-                    va.y = (vf[2][wd] & 0xffffu) | (vf[3][wd] << 16);
-                } else {
-                    va.x = (vf[0][wd] >> 16) | (vf[1][wd] & 0xffff0000u);
-                    va.y = (vf[2][wd] >> 16) | (vf[3][wd] & 0xffff0000u);
-                }
+                const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+                const uint2 va = make_uint2(__builtin_amdgcn_perm(vf[1][wd], vf[0][wd], sel),
+                                            __builtin_amdgcn_perm(vf[3][wd], vf[2][wd], sel));
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-                    if (nt < nct) acc[nt][c] = mfma_pv16<DT>(va, p16[nt], acc[nt][c]);
+                for (int nt = 0; nt < NT; ++nt) acc[nt][c] = mfma_pv16<DT>(va, p16[nt], acc[nt][c]);
             }
         }
     };
@@ -577,9 +597,118 @@ void attn_kernel(AttnArgs a) {
     // prefetch is unconditional -- the last iterations re-read the final tile,
     // an L2 hit -- because a conditional load makes the compiler drain every
     // outstanding load at the join and serialises the pipeline.
+    // ---- workgroup-shared key loop (16-bit wide items on the fast path).
+    // When the workgroup's four items cover one (sequence, kv head, key
+    // range) -- the planner packs wide items that way, one column group per
+    // wave -- every 16-key K/V tile is fetched once for the workgroup (a
+    // quarter per wave, 16 bytes per lane) and staged in LDS, and each wave
+    // reads its MFMA fragments from LDS. That takes the four-fold re-reads of
+    // each tile off the texture path, which is what limits the per-wave loop
+    // on prefill. Loads run one tile ahead in registers; LDS holds two tiles
+    // (written after the barrier that retires the previous reads of that
+    // buffer). Each K row's 16-byte chunks are stored xor-swizzled by key, so
+    // the fragment reads (16 keys x one chunk) hit distinct banks; V rows are
+    // read 16 lanes to a row, conflict-free. One barrier per tile.
+    bool wg_shared = false;
+    if constexpr (FAST && DT != MF_F32 && NT > 1) {
+        if ((int)(blockIdx.x + 1) * kWaves <= num_items) {
+            const int32_t* i0 = a.items + (int64_t)blockIdx.x * kWaves * MF_PLAN_ITEM_INTS;
+            wg_shared = true;
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) {
+                const int32_t* iw = i0 + w * MF_PLAN_ITEM_INTS;
+                wg_shared = wg_shared && iw[0] == i0[0] && iw[1] == i0[1] && iw[4] == i0[4] && iw[5] == i0[5];
+            }
+        }
+    }
+    if constexpr (FAST && DT != MF_F32 && NT > 1) {
+        if (wg_shared) {
+            constexpr int RB = DP * ES;             // bytes of one key row
+            constexpr int NCH = RB / 16;            // 16-byte chunks per row
+            constexpr int STAGE = 32 * RB;          // K tile, then V tile
+            constexpr int NI = (STAGE + kWaves * 1024 - 1) / (kWaves * 1024);  // 16-byte loads per lane per tile
+            __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+            __shared__ int s_end[kWaves];
+            if (lane == 0) s_end[wave] = fast_end;
+            __syncthreads();
+            const int wg_end = __builtin_amdgcn_readfirstlane(
+                max(max(s_end[0], s_end[1]), max(s_end[2], s_end[3])));
+            const int n = wg_end - kt0;
+            const int idx = kt0 + lane;
+            const int tblw = idx < wg_end ? a.block_tables[(int64_t)s * a.bt_stride + idx] : 0;
+            // this lane's 16 bytes of each tile: LDS byte base + lane*16 of
+            // piece (i*4 + wave) mod STAGE, and the matching pool offset inside
+            // the block
+            uint32_t src_off[NI];
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int base = ((i * kWaves + wave) * 1024) % STAGE;
+                const bool isv = base >= 16 * RB;
+                const int p2 = (isv ? base - 16 * RB : base) + lane * 16;
+                const int key = p2 / RB, slot = (p2 % RB) >> 4;
+                const int q = isv ? slot : (slot ^ (key & (NCH - 1)));
+                src_off[i] = (uint32_t)key * v_row_bytes + (uint32_t)q * 16;
+            }
+            // Loads are unconditional (a wave without a piece of a small tile
+            // re-reads another wave's piece and does not store it): a
+            // conditional load would make every later wait drain all loads.
+            auto fetch = [&](int t, uint4 (&r)[NI]) {
+                const int phys = __builtin_amdgcn_readlane(tblw, t - kt0);
+                const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    const int base = ((i * kWaves + wave) * 1024) % STAGE;
+                    r[i] = *(const uint4*)((base >= 16 * RB ? a.v_pool : a.k_pool) + boff + src_off[i]);
+                }
+            };
+            auto stash = [&](const uint4 (&r)[NI], int buf) {
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    const int base = (i * kWaves + wave) * 1024;
+                    if (base < STAGE) *(uint4*)(smem + buf * STAGE + base + lane * 16) = r[i];
+                }
+            };
+            auto sync = [&]() {
+                // this wave's LDS reads and writes are done, then all waves'
+                __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+            };
+            // One register set in flight: tile i+1 arrives during tile i's
+            // compute, is stored to the other LDS buffer, and the set is
+            // refilled with tile i+2 (the last ones re-read tile n-1).
+            if (n > 0) {
+                uint4 rs[NI];
+                fetch(kt0, rs);
+                stash(rs, 0);
+                fetch(min(kt0 + 1, wg_end - 1), rs);
+                sync();
+                for (int i = 0; i < n; ++i) {
+                    const int t = kt0 + i;
+                    if (t < fast_end) {
+                        const char* stg = smem + (i & 1) * STAGE;
+                        uint4 kf[NL];
+                        uint32_t vf[4][VWD];
+#pragma unroll
+                        for (int c = 0; c < NL; ++c)
+                            kf[c] = *(const uint4*)(stg + j * RB + (((c * 4 + g) ^ (j & (NCH - 1))) << 4));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) ld_words<VB>(stg + 16 * RB + (4 * g + r) * RB + j * VB, vf[r]);
+                        process(t, kf, vf);
+                    }
+                    if (i + 1 < n) {
+                        stash(rs, (i + 1) & 1);
+                        fetch(min(t + 2, wg_end - 1), rs);
+                    }
+                    sync();
+                }
+            }
+        }
+    }
     uint4 kA[NL], kB[NL];
     uint32_t vA[4][VWD], vB[4][VWD];
-    if (kt0 < fast_end) {
+    if (kt0 < fast_end && !wg_shared) {
         const int last = fast_end - 1;
         int kt = kt0;
         load_tile(kt, kA, vA);
@@ -796,41 +925,79 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
         return (qlen * G + 15) / 16;
     };
 
-    // Total (kv head, column group, key tile) units decide the partition size:
-    // enough items to keep every CU busy, few enough that partials stay small.
-    int64_t work = 0;
+    // Key partition sizes, per item class. Single-column-tile (narrow)
+    // items get their parallelism from splitting keys: enough items to keep
+    // every CU busy, few enough that partials stay small. Wide items already
+    // come as many column groups, and each split of one costs a 16-column fp32
+    // partial per tile written and merged again, so they are split only as far
+    // as it takes to reach kWideItems items.
+    int64_t work = 0, wide_units = 0;
+    int wide_max_tiles = 0;
     for (int s = 0; s < num_seqs; ++s) {
         const int nct = col_tiles(s);
         if (!nct) continue;
-        const int groups = (nct == 1 || WT == 1) ? nct : (nct + WT - 1) / WT;
-        work += (int64_t)Hkv * groups * ((kv_lens[s] + 15) / 16);
+        const bool narrow = nct == 1 || WT == 1;
+        const int groups = narrow ? nct : (nct + WT - 1) / WT;
+        const int tiles = (kv_lens[s] + 15) / 16;
+        work += (int64_t)Hkv * groups * tiles;
+        if (!narrow) {
+            wide_units += (int64_t)Hkv * groups;
+            wide_max_tiles = std::max(wide_max_tiles, tiles);
+        }
     }
     int P = std::min(partition_tiles, mf::kMaxItemTiles);
+    int PW = P;
     if (P <= 0) {
-        const int64_t target_items = 8192;
+        const int64_t target_items = MF_NARROW_ITEMS;
         int64_t want = (work + target_items - 1) / target_items;
         P = 4;
         while (P < want && P < mf::kMaxItemTiles) P *= 2;
+        // wide: the smallest partition (a power of two, at least P) whose
+        // item count stays within the target
+        PW = P;
+        if (wide_units > 0) {
+            auto wide_items = [&](int q) {
+                int64_t n = 0;
+                for (int s = 0; s < num_seqs; ++s) {
+                    const int nct = col_tiles(s);
+                    if (!nct || nct == 1 || WT == 1) continue;
+                    n += (int64_t)Hkv * ((nct + WT - 1) / WT) * (((kv_lens[s] + 15) / 16 + q - 1) / q);
+                }
+                return n;
+            };
+            while (PW < mf::kMaxItemTiles && PW < wide_max_tiles && wide_items(PW) > MF_WIDE_ITEMS) PW *= 2;
+        }
     }
 
+    // Wide items are launched in workgroups of kWaves (one item per wave).
+    // A (sequence, kv head, partition) run of at least kWaves column groups
+    // fills whole workgroups of its own -- consecutive column groups, the last
+    // one padded with empty items (no column tiles) -- so the workgroup shares
+    // each K/V tile through LDS. Shorter runs are pooled and packed kWaves to
+    // a workgroup, each wave on its own keys.
+    const int U = mf::kWaves;
+    auto round_up = [&](int64_t n) { return (n + U - 1) / U * U; };
+
     // First walk: sizes only.
-    int64_t n_narrow = 0, n_wide = 0, n_merges = 0, n_slots = 0;
+    int64_t n_narrow = 0, n_wide = 0, n_loose = 0, n_merges = 0, n_slots = 0;
     for (int s = 0; s < num_seqs; ++s) {
         const int nct = col_tiles(s);
         if (!nct) continue;
         const bool narrow = nct == 1 || WT == 1;
         const int tiles = (kv_lens[s] + 15) / 16;
-        const int nparts = (tiles + P - 1) / P;
+        const int Q = narrow ? P : PW;
+        const int nparts = (tiles + Q - 1) / Q;
         const int width = narrow ? 1 : WT;
-        for (int cg0 = 0; cg0 < nct; cg0 += width) {
-            const int w = std::min(width, nct - cg0);
-            (narrow ? n_narrow : n_wide) += (int64_t)nparts * Hkv;
-            if (nparts > 1) {
-                n_slots += (int64_t)Hkv * nparts * w;
-                n_merges += (int64_t)Hkv * w;
-            }
+        const int ngroups = (nct + width - 1) / width;
+        if (narrow) n_narrow += (int64_t)nparts * Hkv * ngroups;
+        else if (ngroups >= U) n_wide += (int64_t)nparts * Hkv * round_up(ngroups);
+        else n_loose += (int64_t)nparts * Hkv * ngroups;
+        if (nparts > 1) {
+            n_slots += (int64_t)Hkv * nparts * nct;
+            n_merges += (int64_t)Hkv * nct;
         }
     }
+    n_wide += round_up(n_loose);
     const int64_t pstride = 16 * (int64_t)(mf::part_dstride_for(head_dim) + 2);
     counts[0] = n_narrow;
     counts[1] = n_wide;
@@ -840,81 +1007,127 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     if ((n_narrow + n_wide) > 0 && !items) return MF_ERR_ARG;
     if (n_merges > 0 && !merges) return MF_ERR_ARG;
 
-    // Second walk: write items (narrow block first) and merges.
-    int64_t wi_narrow = 0, wi_wide = n_narrow, wm = 0, slots = 0;
-    for (int pass = 0; pass < 2; ++pass) {
-        for (int s = 0; s < num_seqs; ++s) {
-            const int nct = col_tiles(s);
-            if (!nct) continue;
-            const bool narrow = nct == 1 || WT == 1;
-            if ((pass == 0) != narrow) continue;
-            const int tiles = (kv_lens[s] + 15) / 16;
-            const int nparts = (tiles + P - 1) / P;
-            const int width = narrow ? 1 : WT;
-            for (int cg0 = 0; cg0 < nct; cg0 += width) {
-                const int w = std::min(width, nct - cg0);
-                const int64_t group_base = slots;
-                const int64_t merge_base = wm;
-                if (nparts > 1) slots += (int64_t)Hkv * nparts * w;
-                for (int p = 0; p < nparts; ++p) {
+    // Second walk: write narrow items in place and stage wide ones, and write
+    // the merges. Column group gi of a sequence owns partial slots from
+    // slot0 + gi*Hkv*nparts*width (head-major, then partition, then its w
+    // tiles) and merge records from merge0 + gi*Hkv*width.
+    typedef std::array<int32_t, MF_PLAN_ITEM_INTS> Item;
+    std::vector<Item> shared_items, loose_items;
+    int64_t wi_narrow = 0, wm = 0, slots = 0;
+    for (int s = 0; s < num_seqs; ++s) {
+        const int nct = col_tiles(s);
+        if (!nct) continue;
+        const bool narrow = nct == 1 || WT == 1;
+        const int tiles = (kv_lens[s] + 15) / 16;
+        const int Q = narrow ? P : PW;
+        const int nparts = (tiles + Q - 1) / Q;
+        const int width = narrow ? 1 : WT;
+        const int ngroups = (nct + width - 1) / width;
+        const int64_t slot0 = slots, merge0 = wm;
+        auto make = [&](int gi, int p, int h) {
+            const int cg0 = gi * width;
+            const int w = std::min(width, nct - cg0);
+            Item o;
+            o[0] = s;
+            o[1] = h;
+            o[2] = cg0;
+            o[3] = w;
+            o[4] = p * Q;
+            o[5] = std::min(tiles, (p + 1) * Q);
+            o[6] = nparts > 1 ? (int32_t)(slot0 + (int64_t)gi * Hkv * nparts * width + ((int64_t)h * nparts + p) * w)
+                              : -1;
+            o[7] = nparts > 1 ? (int32_t)(merge0 + (int64_t)gi * Hkv * width + (int64_t)h * w) : -1;
+            o[8] = cu_seqlens[s];
+            o[9] = cu_seqlens[s + 1] - cu_seqlens[s];
+            o[10] = kv_lens[s];
+            o[11] = 0;
+            return o;
+        };
+        if (narrow) {
+            for (int gi = 0; gi < ngroups; ++gi)
+                for (int p = 0; p < nparts; ++p)
                     for (int h = 0; h < Hkv; ++h) {
-                        int64_t& wi = narrow ? wi_narrow : wi_wide;
-                        int32_t* o = items + wi * MF_PLAN_ITEM_INTS;
-                        o[0] = s;
-                        o[1] = h;
-                        o[2] = cg0;
-                        o[3] = w;
-                        o[4] = p * P;
-                        o[5] = std::min(tiles, (p + 1) * P);
-                        o[6] = nparts > 1 ? (int32_t)(group_base + ((int64_t)h * nparts + p) * w) : -1;
-                        o[7] = nparts > 1 ? (int32_t)(merge_base + (int64_t)h * w) : -1;
-                        o[8] = cu_seqlens[s];
-                        o[9] = cu_seqlens[s + 1] - cu_seqlens[s];
-                        o[10] = kv_lens[s];
-                        o[11] = 0;
-                        ++wi;
+                        const Item o = make(gi, p, h);
+                        std::copy(o.begin(), o.end(), items + wi_narrow * MF_PLAN_ITEM_INTS);
+                        ++wi_narrow;
+                    }
+        } else {
+            for (int p = 0; p < nparts; ++p)
+                for (int h = 0; h < Hkv; ++h) {
+                    if (ngroups >= U) {
+                        for (int gi = 0; gi < round_up(ngroups); ++gi) {
+                            Item o = make(std::min(gi, ngroups - 1), p, h);
+                            if (gi >= ngroups) {  // padding: same keys, no columns, no partial slot
+                                o[3] = 0;
+                                o[6] = -1;
+                                o[7] = -1;
+                            }
+                            shared_items.push_back(o);
+                        }
+                    } else {
+                        for (int gi = 0; gi < ngroups; ++gi) loose_items.push_back(make(gi, p, h));
                     }
                 }
-                if (nparts > 1) {
-                    for (int h = 0; h < Hkv; ++h) {
-                        for (int o2 = 0; o2 < w; ++o2) {
-                            int32_t* o = merges + wm * MF_PLAN_MERGE_INTS;
-                            o[0] = s;
-                            o[1] = h;
-                            o[2] = cg0 + o2;
-                            o[3] = nparts;
-                            o[4] = (int32_t)(group_base + (int64_t)h * nparts * w + o2);
-                            o[5] = w;
-                            o[6] = cu_seqlens[s];
-                            o[7] = cu_seqlens[s + 1] - cu_seqlens[s];
-                            ++wm;
-                        }
+        }
+        if (nparts > 1) {
+            for (int gi = 0; gi < ngroups; ++gi) {
+                const int cg0 = gi * width;
+                const int w = std::min(width, nct - cg0);
+                const int64_t group_base = slot0 + (int64_t)gi * Hkv * nparts * width;
+                for (int h = 0; h < Hkv; ++h) {
+                    for (int o2 = 0; o2 < w; ++o2) {
+                        int32_t* o = merges + wm * MF_PLAN_MERGE_INTS;
+                        o[0] = s;
+                        o[1] = h;
+                        o[2] = cg0 + o2;
+                        o[3] = nparts;
+                        o[4] = (int32_t)(group_base + (int64_t)h * nparts * w + o2);
+                        o[5] = w;
+                        o[6] = cu_seqlens[s];
+                        o[7] = cu_seqlens[s + 1] - cu_seqlens[s];
+                        ++wm;
                     }
                 }
             }
+            slots += (int64_t)Hkv * nparts * nct;
         }
     }
-    // Longest items first within each class: the hardware hands out
-    // workgroups in order as slots free up, so the last round of the grid is
-    // made of the short remainder partitions instead of a few long ones.
-    // Stable, so equal-length items keep their heads-adjacent order.
-    auto by_length = [&](int64_t first, int64_t count) {
-        if (count < 2) return;
-        std::vector<int64_t> idx(count);
-        for (int64_t i = 0; i < count; ++i) idx[i] = first + i;
-        std::stable_sort(idx.begin(), idx.end(), [&](int64_t x, int64_t y) {
-            const int32_t* a = items + x * MF_PLAN_ITEM_INTS;
-            const int32_t* b = items + y * MF_PLAN_ITEM_INTS;
-            return (a[5] - a[4]) > (b[5] - b[4]);
-        });
-        std::vector<int32_t> tmp((size_t)count * MF_PLAN_ITEM_INTS);
-        for (int64_t i = 0; i < count; ++i)
-            std::copy(items + idx[i] * MF_PLAN_ITEM_INTS, items + (idx[i] + 1) * MF_PLAN_ITEM_INTS,
-                      tmp.begin() + i * MF_PLAN_ITEM_INTS);
-        std::copy(tmp.begin(), tmp.end(), items + first * MF_PLAN_ITEM_INTS);
+    // Longest first: the hardware hands out workgroups in order as slots free
+    // up, so the last round of the grid is made of the short remainder
+    // partitions instead of a few long ones. Stable, so equal lengths keep
+    // their heads-adjacent order.
+    auto len = [](const Item& o) { return o[5] - o[4]; };
+    auto longer = [&](const Item& x, const Item& y) { return len(x) > len(y); };
+    {
+        std::vector<Item> nar((size_t)n_narrow);
+        for (int64_t i = 0; i < n_narrow; ++i)
+            std::copy(items + i * MF_PLAN_ITEM_INTS, items + (i + 1) * MF_PLAN_ITEM_INTS, nar[i].begin());
+        std::stable_sort(nar.begin(), nar.end(), longer);
+        for (int64_t i = 0; i < n_narrow; ++i)
+            std::copy(nar[i].begin(), nar[i].end(), items + i * MF_PLAN_ITEM_INTS);
+    }
+    // wide: loose items sorted, then cut into workgroups (the last padded
+    // with empty items); all workgroups ordered by their longest item
+    std::stable_sort(loose_items.begin(), loose_items.end(), longer);
+    while (loose_items.size() % U) {
+        Item o{};
+        o[6] = -1;
+        o[7] = -1;
+        loose_items.push_back(o);
+    }
+    std::vector<const Item*> units;
+    for (size_t i = 0; i < shared_items.size(); i += U) units.push_back(&shared_items[i]);
+    for (size_t i = 0; i < loose_items.size(); i += U) units.push_back(&loose_items[i]);
+    auto unit_len = [&](const Item* u) {
+        int l = 0;
+        for (int w = 0; w < U; ++w) l = std::max(l, len(u[w]));
+        return l;
     };
-    by_length(0, n_narrow);
-    by_length(n_narrow, n_wide);
+    std::stable_sort(units.begin(), units.end(),
+                     [&](const Item* x, const Item* y) { return unit_len(x) > unit_len(y); });
+    int64_t wi = n_narrow;
+    for (const Item* u : units)
+        for (int w = 0; w < U; ++w, ++wi) std::copy(u[w].begin(), u[w].end(), items + wi * MF_PLAN_ITEM_INTS);
     return MF_OK;
 }
 
@@ -986,7 +1199,14 @@ int paged_attention_impl(
     a.n_sh = new_stride_head;
     a.G = num_q_heads / num_kv_heads;
     a.head_dim = head_dim;
-    a.scale_log2 = scale * 1.4426950408889634f;
+    // Scores are scaled inside the exponent, which needs a positive factor:
+    // a negative scale flips the sign of Q instead (exact), and a zero scale
+    // becomes 2^-100, for which every 2^(s * scale - m) rounds to exactly 1,
+    // the uniform weights a zero scale gives.
+    if (!(std::fabs(scale) < INFINITY)) return MF_ERR_ARG;
+    a.q_sign = scale < 0.f ? (es == 4 ? 0x80000000u : 0x80008000u) : 0u;
+    a.scale_log2 = scale == 0.f ? 0x1p-100f : std::fabs(scale) * 1.4426950408889634f;
+    a.inv_scale_log2 = 1.f / a.scale_log2;
     a.partials = partials;
     a.part_dstride = part_dstride_for(head_dim);
     a.merges = plan_merges;

@@ -236,3 +236,68 @@ def test_split_k_merge_fused_and_separate_agree(device, fused):
 
     for buf in nat._WORKSPACE._counters.values():
         assert int(buf.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("hq,hkv,d", [(15, 5, 64), (40, 8, 128), (8, 2, 32)])
+@pytest.mark.parametrize("partition_tiles,fused", [(0, False), (3, False), (3, True)])
+def test_wide_items_shared_workgroups(device, dtype, hq, hkv, d, partition_tiles, fused):
+    """Prefill chunks wide enough for whole workgroups (four column groups
+    sharing each K/V tile through LDS, the last workgroup padded), packed with
+    short multi-row entries that the planner pools four to a workgroup, and
+    decodes -- one launch, checked against the oracle."""
+    from memforge_amd import _native as nat
+
+    dt = DT[dtype]
+    gen = torch.Generator().manual_seed(23 + d)
+    bs = 16
+    G = hq // hkv
+    prefill = [(0, 300), (517, 129), (1000, 64)]   # (prior, chunk)
+    short = [(40, 10), (260, 20)]                   # under four column groups each
+    decodes = [5, 333]
+    entries = prefill + short + [(c - 1, 1) for c in decodes]
+    lengths = [p + c for p, c in entries]
+    tables = random_tables(gen, sum((x + bs - 1) // bs for x in lengths) + 2, lengths, bs)
+    kp, vp = _pool(gen, max(max(t) for t in tables) + 1, bs, hkv, d, dt, device)
+    seq_ids, positions = [], []
+    for s, (p, c) in enumerate(entries):
+        seq_ids += [s] * c
+        positions += list(range(p, p + c))
+    q = torch.randn((hq, len(seq_ids), d), generator=gen).to(dt).to(device)
+    cu = [0]
+    for _, c in entries:
+        cu.append(cu[-1] + c)
+    items, _, counts = nat.plan_attention_host(cu, lengths, hq, hkv, d, dt, partition_tiles)
+    wide = items[int(counts[0]):]
+    units = [wide[u:u + 4] for u in range(0, len(wide), 4)]
+    shared = [u for u in units if len({(int(r[0]), int(r[1]), int(r[4]), int(r[5])) for r in u}) == 1]
+    assert shared and len(shared) < len(units), "want both workgroup-shared and pooled units"
+    got = gpu_varlen(q, kp, vp, tables, seq_ids, positions, partition_tiles=partition_tiles, fused=fused)
+    want = oatt.varlen_attention(to_np64(q), to_np64(kp), to_np64(vp), tables, seq_ids, positions, bs)
+    _check(to_np64(got), want, dt)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_long_verify_through_shared_workgroups(device, dtype):
+    """A verify pass with enough in-flight rows for whole workgroups: the
+    pool-only tiles go through the shared LDS loop, the boundary and in-flight
+    tiles through each wave's general loads; the pool is left untouched."""
+    dt = DT[dtype]
+    gen = torch.Generator().manual_seed(29)
+    bs, hq, hkv, d, k1, B = 16, 40, 8, 128, 40, 3
+    ctx = [131, 700, 1024]
+    tables = random_tables(gen, sum((c + k1 + bs - 1) // bs for c in ctx) + 1, [c + k1 for c in ctx], bs)
+    kp, vp = _pool(gen, max(max(t) for t in tables) + 1, bs, hkv, d, dt, device)
+    pool_before = kp.clone()
+    seq_ids = [s for s in range(B) for _ in range(k1)]
+    positions = [ctx[s] + j for s in range(B) for j in range(k1)]
+    T = len(seq_ids)
+    q = torch.randn((hq, T, d), generator=gen).to(dt).to(device)
+    nk = torch.randn((T, hkv, d), generator=gen).to(dt).to(device)
+    nv = torch.randn((T, hkv, d), generator=gen).to(dt).to(device)
+    got = gpu_varlen(q, kp, vp, tables, seq_ids, positions, pool_lens=ctx, new_k=nk, new_v=nv)
+    new_rows = [[s * k1 + j for j in range(k1)] for s in range(B)]
+    want = oatt.varlen_attention(to_np64(q), to_np64(kp), to_np64(vp), tables, seq_ids, positions, bs,
+                                 pool_lens=ctx, new_k=to_np64(nk), new_v=to_np64(nv), new_rows=new_rows)
+    _check(to_np64(got), want, dt)
+    assert torch.equal(kp, pool_before)

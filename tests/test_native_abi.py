@@ -62,8 +62,20 @@ def test_plan_covers_every_tile_exactly_once_and_merges_line_up(dtype, d, pt):
     assert items.shape[0] == p.n_narrow + p.n_wide
     cover = {}
     slots = {}
+    # wide items come in workgroups of four: either one (sequence, head, key
+    # range) with distinct column groups (shared K/V tiles), or four
+    # independent items; padding items carry no columns and no partial slot
+    assert p.n_wide % 4 == 0
+    for u in range(p.n_narrow, p.n_narrow + p.n_wide, 4):
+        unit = [tuple(int(x) for x in it[:11]) for it in items[u:u + 4]]
+        if len({(it[0], it[1], it[4], it[5]) for it in unit}) == 1:
+            real = [it[2] for it in unit if it[3] > 0]
+            assert len(real) == len(set(real)), "shared workgroup repeats a column group"
     for it in items:
         s, h, c0, nct, kt0, kt1, slot, merge, row0, nrows, kvl = (int(x) for x in it[:11])
+        if nct == 0:
+            assert slot == -1 and merge == -1, "padding item owns a partial slot"
+            continue
         assert (row0, nrows, kvl) == (cu[s], q_lens[s], kv[s]), "item carries its sequence's bounds"
         assert kt1 > kt0 and kt1 - kt0 <= 64
         for c in range(c0, c0 + nct):
