@@ -210,47 +210,57 @@ __device__ __forceinline__ void store_out_chunk(char* p, const float* vals) {
 // output is sum_p w_p acc_p / sum_p w_p l_p with w_p = 2^(m_p - max_p m_p).
 //
 // merge_range accumulates partitions p0, p0+pinc, ... relative to their own
-// maximum `mx` (lane (g, j): column j, head_dim range [4g*VCH, 4g*VCH+4*VCH)),
-// issuing the loads of two partitions before using them so the loop is not a
-// memory round trip per partition.
+// maximum `mx` (lane (g, j): column j, head_dim range [4g*VCH, 4g*VCH+4*VCH)).
+// Partitions go four at a time with every load of a batch issued before any
+// is used (a batch past the last partition loads only what exists; the
+// condition is wave-uniform), and the running maximum moves batch to batch:
+// a merge of n partitions per wave costs ceil(n/4) memory round trips.
 template <int DP>
 __device__ __forceinline__ void merge_range(const AttnArgs& a, const int32_t* mg, int p0, int pinc, int j,
                                             int dbase, float& mx, float& L, float (&o)[DP / 4]) {
     constexpr int VCH = DP / 16;
-    constexpr float kNegInf = -__builtin_huge_valf();
+    constexpr int B = 4;
     const int np = mg[3], slot0 = mg[4], sstride = mg[5];
     const int64_t stride = 16 * (int64_t)(a.part_dstride + 2);
     const float* base = a.partials + (int64_t)slot0 * stride;
     const int64_t pstep = (int64_t)sstride * stride;
     const int moff = 16 * a.part_dstride + j;
-    mx = kNegInf;
-    for (int p = p0; p < np; p += pinc) mx = fmaxf(mx, base[p * pstep + moff]);
+    mx = kMinM;
     L = 0.f;
 #pragma unroll
     for (int e = 0; e < 4 * VCH; ++e) o[e] = 0.f;
-    auto absorb = [&](const uint32_t* raw, float mp, float lp) {
-        const float w = (mp == kNegInf) ? 0.f : exp2f(mp - mx);
-        L += lp * w;
+    for (int p = p0; p < np; p += B * pinc) {
+        uint32_t raw[B][4 * VCH];
+        float mb[B], lb[B];
 #pragma unroll
-        for (int e = 0; e < 4 * VCH; ++e) o[e] += w * __uint_as_float(raw[e]);
-    };
-    int p = p0;
-    for (; p + pinc < np; p += 2 * pinc) {
-        uint32_t r0[4 * VCH], r1[4 * VCH];
-        const float* q0 = base + p * pstep;
-        const float* q1 = q0 + pinc * pstep;
-        ld_words<16 * VCH>((const char*)(q0 + j * a.part_dstride + dbase), r0);
-        ld_words<16 * VCH>((const char*)(q1 + j * a.part_dstride + dbase), r1);
-        const float m0 = q0[moff], l0 = q0[moff + 16];
-        const float m1 = q1[moff], l1 = q1[moff + 16];
-        absorb(r0, m0, l0);
-        absorb(r1, m1, l1);
-    }
-    if (p < np) {
-        uint32_t r0[4 * VCH];
-        const float* q0 = base + p * pstep;
-        ld_words<16 * VCH>((const char*)(q0 + j * a.part_dstride + dbase), r0);
-        absorb(r0, q0[moff], q0[moff + 16]);
+        for (int b = 0; b < B; ++b) {
+            if (p + b * pinc < np) {
+                const float* q = base + (int64_t)(p + b * pinc) * pstep;
+                ld_words<16 * VCH>((const char*)(q + j * a.part_dstride + dbase), raw[b]);
+                mb[b] = q[moff];
+                lb[b] = q[moff + 16];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4 * VCH; ++e) raw[b][e] = 0u;
+                mb[b] = kMinM;
+                lb[b] = 0.f;
+            }
+        }
+        float bm = mx;
+#pragma unroll
+        for (int b = 0; b < B; ++b) bm = fmaxf(bm, mb[b]);
+        const float keep = __builtin_amdgcn_exp2f(mx - bm);
+        L *= keep;
+#pragma unroll
+        for (int e = 0; e < 4 * VCH; ++e) o[e] *= keep;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float w = __builtin_amdgcn_exp2f(mb[b] - bm);
+            L += lb[b] * w;
+#pragma unroll
+            for (int e = 0; e < 4 * VCH; ++e) o[e] += w * __uint_as_float(raw[b][e]);
+        }
+        mx = bm;
     }
 }
 
@@ -328,10 +338,27 @@ void attn_kernel(AttnArgs a) {
     const int pool_len = a.pool_lens == nullptr ? kv_len : a.pool_lens[s];
     const int D = a.head_dim;
 
+    // The loads that need nothing but the item go out together -- block-table
+    // entries first (loads retire in issue order, and the first K/V tiles
+    // wait only on them), then row positions, then Q -- so the setup costs
+    // one round trip before the K/V stream starts, not three.
+    //
+    // ---- block-table entries of the item's tiles, one per lane (fast path;
+    // at most kMaxItemTiles = 64), read back with readlane. On a verify pass
+    // that is every tile holding a pool key (the boundary tile included);
+    // pool_end is the end of the tiles lying wholly in the pool.
+    const int tbl_end = a.pool_lens != nullptr ? max(kt0, min(kt1, (pool_len + 15) >> 4)) : kt1;
+    const int pool_end = a.pool_lens != nullptr ? max(kt0, min(kt1, pool_len >> 4)) : kt1;
+    int tbl = 0;
+    const int tbl_base = kt0;
+    if constexpr (FAST) {
+        const int idx = kt0 + lane;
+        tbl = idx < tbl_end ? a.block_tables[(int64_t)s * a.bt_stride + idx] : 0;
+    }
+
     // ---- columns owned by this lane (one per tile)
     int prow[NT], qhead[NT], qpos[NT];
-    int maxpos = -1;
-    int minpos = INT_MAX;  // over the item's real columns
+    bool qvalid[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const int cidx = (c0 + nt) * 16 + j;
@@ -347,23 +374,8 @@ void attn_kernel(AttnArgs a) {
         prow[nt] = pr;
         qhead[nt] = h * a.G + gq;
         qpos[nt] = pos;
-        maxpos = max(maxpos, pos);
-        if (valid) minpos = min(minpos, pos);
+        qvalid[nt] = valid;
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        maxpos = max(maxpos, __shfl_xor(maxpos, off, 64));
-        minpos = min(minpos, __shfl_xor(minpos, off, 64));
-    }
-    minpos = __builtin_amdgcn_readfirstlane(minpos);
-    // last key each lane's column may see (-1 for padding columns)
-    int lim[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) lim[nt] = qpos[nt] >= 0 ? min(qpos[nt], kv_len - 1) : -1;
-    // Tiles past the last key any column may see are never read.
-    int kt_end = min(kt1, (min(maxpos, kv_len - 1) >> 4) + 1);
-    if (maxpos < 0 || kv_len <= 0) kt_end = kt0;
-    kt_end = __builtin_amdgcn_readfirstlane(kt_end);
 
     // ---- Q fragments (MFMA B operand of S^T = K Q^T): lane (g, j) holds
     // column j's head_dim chunk (c*4 + g) for c < NL.
@@ -374,23 +386,10 @@ void attn_kernel(AttnArgs a) {
         for (int c = 0; c < NL; ++c) {
             const int d0 = (c * 4 + g) * EPL;
             uint4 v = make_uint4(0, 0, 0, 0);
-            if (qpos[nt] >= 0 && d0 < D)
+            if (qvalid[nt] && d0 < D)
                 v = *(const uint4*)(a.q + ((int64_t)prow[nt] * a.q_sr + (int64_t)qhead[nt] * a.q_sh + d0) * ES);
             qf[nt][c] = make_uint4(v.x ^ a.q_sign, v.y ^ a.q_sign, v.z ^ a.q_sign, v.w ^ a.q_sign);
         }
-    }
-
-    // m: running max of the scaled scores (log2 units); thr: the raw score
-    // above which a column's running max must move, (m + kLazyLog2) / scale.
-    float m[NT], l[NT], thr[NT];
-    f32x4 acc[NT][VCH];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        m[nt] = kMinM;
-        thr[nt] = (kMinM + kLazyLog2) * a.inv_scale_log2;
-        l[nt] = 0.f;
-#pragma unroll
-        for (int c = 0; c < VCH; ++c) acc[nt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
     // General path: address of key `key`'s row for this kv head, or null.
@@ -407,34 +406,30 @@ void attn_kernel(AttnArgs a) {
         return inflight + ((int64_t)nr * a.n_sr + (int64_t)h * a.n_sh) * ES;
     };
 
-    // K: lane (g, j) loads key j's head_dim chunks (c*4 + g).
-    // V: lane (g, j) loads keys 4g..4g+3, head_dim elements [j*VCH, j*VCH+VCH).
-    // FAST path (16-token blocks, head_dim == DP): every
-    // load is unconditional, so the compiler can keep the next tile's loads in
-    // flight while the current tile is processed; the item's block-table
-    // entries (at most kMaxItemTiles = 64) are fetched once, one per lane, and
-    // read back with readlane.
-    // Tiles [kt0, fast_end) run through the pipelined loop. On the fast path
-    // with in-flight keys (a verify pass) that is only the tiles lying wholly
-    // in the pool; the one or two tiles holding the boundary and the in-flight
-    // candidates follow through the general per-key loads.
-    int fast_end = kt_end;
-    if constexpr (FAST) {
-        if (a.pool_lens != nullptr) fast_end = max(kt0, min(kt_end, pool_len >> 4));
-    }
-    int tbl = 0;
-    const int tbl_base = kt0;
     // byte offsets of this lane's K chunk (key j, chunk g) and V chunk (keys
     // 4g.., head_dim j*VCH..) inside one block of one kv head
     const uint32_t k_lane_off = (uint32_t)(((int64_t)j * a.p_ss + g * EPL) * ES);
     const uint32_t v_row_bytes = (uint32_t)(a.p_ss * ES);
     const uint32_t v_lane_off = (uint32_t)(((int64_t)(4 * g) * a.p_ss + j * VCH) * ES);
-    if constexpr (FAST) {
-        const int idx = kt0 + lane;
-        tbl = idx < fast_end ? a.block_tables[(int64_t)s * a.bt_stride + idx] : 0;
-    }
+    // Per-key loads of tile kt (the verify boundary and in-flight tiles, and
+    // every tile off the fast path). On the fast path a tile's pool keys all
+    // lie in one block, whose entry is already in tbl.
     auto load_general = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
-        const char* kp = key_row(a.k_pool, a.new_k, kt * 16 + j);
+        int phys = 0;
+        if constexpr (FAST) phys = kt < tbl_end ? __builtin_amdgcn_readlane(tbl, kt - tbl_base) : 0;
+        auto row = [&](const char* pool, const char* inflight, int key) -> const char* {
+            if constexpr (FAST) {
+                if (key >= kv_len) return nullptr;
+                if (key < pool_len)
+                    return pool + ((int64_t)phys * a.p_sb + (int64_t)(key & 15) * a.p_ss + (int64_t)h * a.p_sh) * ES;
+                int nr = row0 + (key - pool_len);
+                if (a.row_map) nr = a.row_map[nr];
+                return inflight + ((int64_t)nr * a.n_sr + (int64_t)h * a.n_sh) * ES;
+            } else {
+                return key_row(pool, inflight, key);
+            }
+        };
+        const char* kp = row(a.k_pool, a.new_k, kt * 16 + j);
 #pragma unroll
         for (int c = 0; c < NL; ++c) {
             const int d0 = (c * 4 + g) * EPL;
@@ -442,7 +437,7 @@ void attn_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const char* vp = key_row(a.v_pool, a.new_v, kt * 16 + 4 * g + r);
+            const char* vp = row(a.v_pool, a.new_v, kt * 16 + 4 * g + r);
             if (vp && j * VCH < D) {
                 ld_words<VB>(vp + (int64_t)j * VCH * ES, vf[r]);
             } else {
@@ -477,6 +472,66 @@ void attn_kernel(AttnArgs a) {
         }
     };
 
+    // The first two tiles of a single-column-tile (decode) item go out with
+    // the setup loads: positions only trim the item's key range, and these
+    // tiles lie in it whenever the item has any.
+    uint4 kA[NL], kB[NL];
+    uint32_t vA[4][VWD], vB[4][VWD];
+    if constexpr (FAST && NT == 1) {
+        if (kt0 < pool_end) {
+            load_tile(kt0, kA, vA);
+            load_tile(min(kt0 + 1, pool_end - 1), kB, vB);
+        }
+    }
+
+    int maxpos = -1;
+    int minpos = INT_MAX;  // over the item's real columns
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        maxpos = max(maxpos, qpos[nt]);
+        if (qvalid[nt]) minpos = min(minpos, qpos[nt]);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        maxpos = max(maxpos, __shfl_xor(maxpos, off, 64));
+        minpos = min(minpos, __shfl_xor(minpos, off, 64));
+    }
+    minpos = __builtin_amdgcn_readfirstlane(minpos);
+    // last key each lane's column may see (-1 for padding columns)
+    int lim[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) lim[nt] = qpos[nt] >= 0 ? min(qpos[nt], kv_len - 1) : -1;
+    // Tiles past the last key any column may see are never read.
+    int kt_end = min(kt1, (min(maxpos, kv_len - 1) >> 4) + 1);
+    if (maxpos < 0 || kv_len <= 0) kt_end = kt0;
+    kt_end = __builtin_amdgcn_readfirstlane(kt_end);
+
+    // m: running max of the scaled scores (log2 units); thr: the raw score
+    // above which a column's running max must move, (m + kLazyLog2) / scale.
+    float m[NT], l[NT], thr[NT];
+    f32x4 acc[NT][VCH];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        m[nt] = kMinM;
+        thr[nt] = (kMinM + kLazyLog2) * a.inv_scale_log2;
+        l[nt] = 0.f;
+#pragma unroll
+        for (int c = 0; c < VCH; ++c) acc[nt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // K: lane (g, j) loads key j's head_dim chunks (c*4 + g).
+    // V: lane (g, j) loads keys 4g..4g+3, head_dim elements [j*VCH, j*VCH+VCH).
+    // FAST path (16-token blocks, head_dim == DP): every
+    // load is unconditional, so the compiler can keep the next tile's loads in
+    // flight while the current tile is processed.
+    // Tiles [kt0, fast_end) run through the pipelined loop. On the fast path
+    // with in-flight keys (a verify pass) that is only the tiles lying wholly
+    // in the pool; the one or two tiles holding the boundary and the in-flight
+    // candidates follow through the general per-key loads.
+    int fast_end = kt_end;
+    if constexpr (FAST) {
+        if (a.pool_lens != nullptr) fast_end = max(kt0, min(kt_end, pool_len >> 4));
+    }
     // Per-tile work is branch-free apart from wave-uniform decisions: every
     // column tile's MFMAs run (tiles past nct hold zero queries and are never
     // stored), and masking is a select, so the scheduler sees one straight
@@ -634,12 +689,12 @@ void attn_kernel(AttnArgs a) {
             const int wg_end = __builtin_amdgcn_readfirstlane(
                 max(max(s_end[0], s_end[1]), max(s_end[2], s_end[3])));
             const int n = wg_end - kt0;
-            const int idx = kt0 + lane;
-            const int tblw = idx < wg_end ? a.block_tables[(int64_t)s * a.bt_stride + idx] : 0;
             // this lane's 16 bytes of each tile: LDS byte base + lane*16 of
             // piece (i*4 + wave) mod STAGE, and the matching pool offset inside
-            // the block
-            uint32_t src_off[NI];
+            // the block (vector types rather than arrays keep them in registers)
+            typedef uint32_t offs_t __attribute__((ext_vector_type(NI)));
+            typedef uint32_t regs_t __attribute__((ext_vector_type(4 * NI)));
+            offs_t src_off;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const int base = ((i * kWaves + wave) * 1024) % STAGE;
@@ -652,20 +707,26 @@ void attn_kernel(AttnArgs a) {
             // Loads are unconditional (a wave without a piece of a small tile
             // re-reads another wave's piece and does not store it): a
             // conditional load would make every later wait drain all loads.
-            auto fetch = [&](int t, uint4 (&r)[NI]) {
-                const int phys = __builtin_amdgcn_readlane(tblw, t - kt0);
+            auto fetch = [&](int t, regs_t& r) __attribute__((always_inline)) {
+                const int phys = __builtin_amdgcn_readlane(tbl, t - kt0);
                 const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
 #pragma unroll
                 for (int i = 0; i < NI; ++i) {
                     const int base = ((i * kWaves + wave) * 1024) % STAGE;
-                    r[i] = *(const uint4*)((base >= 16 * RB ? a.v_pool : a.k_pool) + boff + src_off[i]);
+                    const uint4 v = *(const uint4*)((base >= 16 * RB ? a.v_pool : a.k_pool) + boff + src_off[i]);
+                    r[4 * i] = v.x;
+                    r[4 * i + 1] = v.y;
+                    r[4 * i + 2] = v.z;
+                    r[4 * i + 3] = v.w;
                 }
             };
-            auto stash = [&](const uint4 (&r)[NI], int buf) {
+            auto stash = [&](const regs_t& r, int buf) __attribute__((always_inline)) {
 #pragma unroll
                 for (int i = 0; i < NI; ++i) {
                     const int base = (i * kWaves + wave) * 1024;
-                    if (base < STAGE) *(uint4*)(smem + buf * STAGE + base + lane * 16) = r[i];
+                    if (base < STAGE)
+                        *(uint4*)(smem + buf * STAGE + base + lane * 16) =
+                            make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
                 }
             };
             auto sync = [&]() {
@@ -679,7 +740,7 @@ void attn_kernel(AttnArgs a) {
             // compute, is stored to the other LDS buffer, and the set is
             // refilled with tile i+2 (the last ones re-read tile n-1).
             if (n > 0) {
-                uint4 rs[NI];
+                regs_t rs;
                 fetch(kt0, rs);
                 stash(rs, 0);
                 fetch(min(kt0 + 1, wg_end - 1), rs);
@@ -706,16 +767,21 @@ void attn_kernel(AttnArgs a) {
             }
         }
     }
-    uint4 kA[NL], kB[NL];
-    uint32_t vA[4][VWD], vB[4][VWD];
+    // The first tile past the pipelined range (a verify pass's boundary or
+    // candidate tile) is fetched before the loop, so its per-key loads
+    // overlap the pool tiles instead of following them.
+    uint4 kT[NL];
+    uint32_t vT[4][VWD];
+    if constexpr (FAST && NT == 1) {
+        if (fast_end < kt_end) load_general(fast_end, kT, vT);
+    }
     if (kt0 < fast_end && !wg_shared) {
         const int last = fast_end - 1;
         int kt = kt0;
-        load_tile(kt, kA, vA);
         if constexpr (FAST && NT == 1) {
+            // kA, kB hold tiles kt0 and kt0+1 (issued with the setup loads)
             uint4 kC[NL];
             uint32_t vC[4][VWD];
-            load_tile(min(kt + 1, last), kB, vB);
             for (;;) {
                 load_tile(min(kt + 2, last), kC, vC);
                 process(kt, kA, vA);
@@ -728,6 +794,7 @@ void attn_kernel(AttnArgs a) {
                 if (++kt > last) break;
             }
         } else {
+            load_tile(kt, kA, vA);
             for (;;) {
                 load_tile(min(kt + 1, last), kB, vB);
                 process(kt, kA, vA);
@@ -740,7 +807,11 @@ void attn_kernel(AttnArgs a) {
     }
 
     if constexpr (FAST) {
-        for (int kt = fast_end; kt < kt_end; ++kt) {
+        int kt = fast_end;
+        if constexpr (NT == 1) {
+            if (kt < kt_end) process(kt++, kT, vT);
+        }
+        for (; kt < kt_end; ++kt) {
             load_general(kt, kA, vA);
             process(kt, kA, vA);
         }
