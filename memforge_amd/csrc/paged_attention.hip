@@ -446,7 +446,7 @@ void attn_kernel(AttnArgs a) {
             }
         }
     };
-    auto load_tile = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
+    auto load_tile = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD], bool dummy = false) {
         if constexpr (FAST) {
             // block base is wave-uniform (scalar registers); the lane's byte
             // offsets inside a block never change, so they are computed once
@@ -456,11 +456,15 @@ void attn_kernel(AttnArgs a) {
             const char* vb = a.v_pool + boff;
             if constexpr (NT == 1 && DP * ES >= 256) {
                 // non-temporal only for rows of 256 bytes or more: measured
-                // faster there (bf16 D 128) and slower for 128-byte rows
+                // faster there (bf16 D 128) and slower for 128-byte rows. A
+                // dummy (clamped) prefetch reads one line with every lane.
+                const uint32_t ko = dummy ? 0u : k_lane_off;
+                const uint32_t vo = dummy ? 0u : v_lane_off;
+                const uint32_t vr = dummy ? 0u : v_row_bytes;
 #pragma unroll
-                for (int c = 0; c < NL; ++c) kf[c] = ld_nt16(kb + k_lane_off + c * 4 * 16);
+                for (int c = 0; c < NL; ++c) kf[c] = ld_nt16(kb + ko + (dummy ? 0 : c * 4 * 16));
 #pragma unroll
-                for (int r = 0; r < 4; ++r) ld_words_nt<VB>(vb + v_lane_off + r * v_row_bytes, vf[r]);
+                for (int r = 0; r < 4; ++r) ld_words_nt<VB>(vb + vo + r * vr, vf[r]);
             } else {
 #pragma unroll
                 for (int c = 0; c < NL; ++c) kf[c] = *(const uint4*)(kb + k_lane_off + c * 4 * 16);
@@ -779,17 +783,20 @@ void attn_kernel(AttnArgs a) {
         const int last = fast_end - 1;
         int kt = kt0;
         if constexpr (FAST && NT == 1) {
-            // kA, kB hold tiles kt0 and kt0+1 (issued with the setup loads)
+            // kA, kB hold tiles kt0 and kt0+1 (issued with the setup loads).
+            // Prefetches past the last tile still issue (a conditional load
+            // would make the compiler drain the pipeline), but as a single
+            // line: these loads bypass L2, so a full re-read would cost HBM.
             uint4 kC[NL];
             uint32_t vC[4][VWD];
             for (;;) {
-                load_tile(min(kt + 2, last), kC, vC);
+                load_tile(min(kt + 2, last), kC, vC, kt + 2 > last);
                 process(kt, kA, vA);
                 if (++kt > last) break;
-                load_tile(min(kt + 2, last), kA, vA);
+                load_tile(min(kt + 2, last), kA, vA, kt + 2 > last);
                 process(kt, kB, vB);
                 if (++kt > last) break;
-                load_tile(min(kt + 2, last), kB, vB);
+                load_tile(min(kt + 2, last), kB, vB, kt + 2 > last);
                 process(kt, kC, vC);
                 if (++kt > last) break;
             }
