@@ -134,8 +134,10 @@ int mf_ragged_pack(const int32_t* entries, int num_entries,
  * pool through block_tables[s][key / block_size]; keys at or above it are the
  * in-flight rows of the same sequence's new tokens (new_k/new_v row
  * cu_seqlens[s] + key - pool_lens[s], through row_map), which is how a verify
- * pass attends to candidates it has not written to the pool. Softmax
- * accumulates in fp32; out is written in `dtype` (the q/K/V dtype).
+ * pass attends to candidates it has not written to the pool. Scores are
+ * q.k * scale; any finite scale works (a negative one flips q's sign bits, a
+ * zero one gives uniform weights), a NaN or infinite one is MF_ERR_ARG.
+ * Softmax accumulates in fp32; out is written in `dtype` (the q/K/V dtype).
  * Work is described by a plan from mf_attention_plan (device copy of its
  * items/merges); `partials` is fp32 scratch of at least the planned size.
  * merge_counters (device int32[num_merges], all-zero on entry and again on
@@ -176,7 +178,8 @@ int mf_paged_attention(const void* q, int64_t q_stride_row, int64_t q_stride_hea
  * at plan_items + capacity_narrow * MF_PLAN_ITEM_INTS), plan_merges holds
  * capacity_merges records, and device_counts (device, int32[3]) gives the
  * live numbers of narrow items, wide items and merges -- each at most its
- * capacity; workgroups past them exit at once. Split-K partitions are merged
+ * capacity, the wide count a multiple of four as mf_attention_plan makes it;
+ * workgroups past them exit at once. Split-K partitions are merged
  * by the separate merge kernel. Everything else is as in mf_paged_attention.
  */
 int mf_paged_attention_counted(const void* q, int64_t q_stride_row, int64_t q_stride_head,
@@ -198,9 +201,14 @@ int mf_paged_attention_counted(const void* q, int64_t q_stride_row, int64_t q_st
 /* Host-side planner for mf_paged_attention. Inputs are HOST arrays:
  * cu_seqlens[B+1] and kv_lens[B]. Splits every (sequence, kv head, column
  * tile) over key partitions of `partition_tiles` 16-key tiles (0 = chosen
- * from the total work) and writes MF_PLAN_ITEM_INTS ints per work item to
- * items (narrow items -- one 16-column tile -- first, then wide ones) and
- * MF_PLAN_MERGE_INTS ints per split-K merge to merges. counts receives
+ * from the work: narrow and wide items separately) and writes
+ * MF_PLAN_ITEM_INTS ints per work item to items (narrow items -- one
+ * 16-column tile -- first, then wide ones) and MF_PLAN_MERGE_INTS ints per
+ * split-K merge to merges. Wide items come in workgroups of four: a run of
+ * four or more column groups over one (sequence, kv head, key range) fills
+ * whole workgroups, which then share each K/V tile through LDS (the last one
+ * padded with items that have no column tiles and no partial slot); shorter
+ * runs are packed four to a workgroup. counts receives
  * [num_items_narrow, num_items_wide, num_merges, partials_floats].
  * A plan is valid for the dtype and head_dim it was made for and carries the
  * sequences' first rows, row counts and kv lengths: the cu_seqlens / kv_lens
