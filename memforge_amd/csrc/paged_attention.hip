@@ -1222,6 +1222,7 @@ int paged_attention_impl(
     const int32_t* plan_merges, int64_t num_merges, float* partials, int64_t partials_floats,
     int32_t* merge_counters, const int32_t* device_counts, mf_stream_t stream) {
     using namespace mf;
+    if (!(std::fabs(scale) < INFINITY)) return MF_ERR_ARG;  // NaN or infinite
     if (!dtype_ok(dtype) || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
         block_size <= 0 || num_items_narrow < 0 || num_items_wide < 0 || num_merges < 0)
         return MF_ERR_ARG;
@@ -1281,7 +1282,6 @@ int paged_attention_impl(
     // a negative scale flips the sign of Q instead (exact), and a zero scale
     // becomes 2^-100, for which every 2^(s * scale - m) rounds to exactly 1,
     // the uniform weights a zero scale gives.
-    if (!(std::fabs(scale) < INFINITY)) return MF_ERR_ARG;
     a.q_sign = scale < 0.f ? (es == 4 ? 0x80000000u : 0x80008000u) : 0u;
     a.scale_log2 = scale == 0.f ? 0x1p-100f : std::fabs(scale) * 1.4426950408889634f;
     a.inv_scale_log2 = 1.f / a.scale_log2;

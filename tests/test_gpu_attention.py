@@ -301,3 +301,30 @@ def test_long_verify_through_shared_workgroups(device, dtype):
                                  pool_lens=ctx, new_k=to_np64(nk), new_v=to_np64(nv), new_rows=new_rows)
     _check(to_np64(got), want, dt)
     assert torch.equal(kp, pool_before)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+@pytest.mark.parametrize("scale", [-0.125, 0.0, 0.5])
+def test_scale_sign_and_zero(device, dtype, scale):
+    """Scores are q.k * scale for any finite scale: a negative one (applied as a
+    sign flip of q), zero (uniform weights over the visible keys) and four times
+    the default, on decode rows and on prefill rows that run as
+    workgroup-shared wide items. (The fp32 bar of 1e-5 holds at the configs'
+    scales; far larger scales amplify fp32 score rounding through the
+    exponent in any fp32 implementation.)"""
+    dt = DT[dtype]
+    gen = torch.Generator().manual_seed(31)
+    bs, hq, hkv, d = 16, 15, 5, 64
+    entries = [(0, 200), (300, 90), (77, 1), (1500, 1)]   # (first position, rows)
+    lengths = [p + c for p, c in entries]
+    tables = random_tables(gen, sum((x + bs - 1) // bs for x in lengths) + 2, lengths, bs)
+    kp, vp = _pool(gen, max(max(t) for t in tables) + 1, bs, hkv, d, dt, device)
+    seq_ids, positions = [], []
+    for s, (p, c) in enumerate(entries):
+        seq_ids += [s] * c
+        positions += list(range(p, p + c))
+    q = torch.randn((hq, len(seq_ids), d), generator=gen).to(dt).to(device)
+    got = gpu_varlen(q, kp, vp, tables, seq_ids, positions, scale=scale)
+    want = oatt.varlen_attention(to_np64(q), to_np64(kp), to_np64(vp), tables, seq_ids, positions, bs,
+                                 scale=scale)
+    _check(to_np64(got), want, dt)

@@ -146,3 +146,16 @@ def test_product_path_has_no_cpu_fallback(monkeypatch):
     with pytest.raises(Exception):
         nat.kv_write(torch.zeros((3, 2, 64)), torch.zeros((3, 2, 64)), torch.zeros(3, dtype=torch.int64),
                      nat.PoolView.from_bshd(k, k.clone()))
+
+
+@pytest.mark.parametrize("scale", [float("nan"), float("inf"), float("-inf")])
+def test_attention_rejects_a_non_finite_scale(scale):
+    """A NaN or infinite scale is an argument error, returned before any launch
+    (so this runs without a GPU). Finite scales -- negative and zero included --
+    are checked against the oracle on the GPU."""
+    L = nat.lib()
+    # the scale is the first thing checked: no pointer is needed to see it refused
+    st = L.mf_paged_attention(None, 64, 64, None, 64, 64, 2, None, None, 16 * 64, 64, 64, 16,
+                              None, 4, None, None, None, None, None, None, None, 0, 0,
+                              1, 1, 64, scale, None, 1, 0, None, 0, None, 0, None, None)
+    assert st == -1, st
