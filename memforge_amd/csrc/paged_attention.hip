@@ -28,6 +28,9 @@
 
 #include "mf_common.h"
 
+#ifndef MF_MAX_ITEM_TILES
+#define MF_MAX_ITEM_TILES 128
+#endif
 namespace mf {
 namespace {
 
@@ -40,9 +43,9 @@ typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
 
 constexpr int kWaves = 4;  // waves per workgroup; each wave runs its own item
-constexpr int kMaxItemTiles = 64;  // key tiles per work item (one block-table entry per lane)
+constexpr int kMaxItemTiles = MF_MAX_ITEM_TILES;  // key tiles per work item (two block-table entries per lane)
 #ifndef MF_NARROW_ITEMS
-#define MF_NARROW_ITEMS 8192  // planner: target item count that sets the narrow key partition
+#define MF_NARROW_ITEMS 4096  // planner: target item count that sets the narrow key partition
 #endif
 #ifndef MF_WIDE_ITEMS
 #define MF_WIDE_ITEMS 4096  // planner: most wide items before partitions grow
@@ -343,18 +346,27 @@ void attn_kernel(AttnArgs a) {
     // wait only on them), then row positions, then Q -- so the setup costs
     // one round trip before the K/V stream starts, not three.
     //
-    // ---- block-table entries of the item's tiles, one per lane (fast path;
-    // at most kMaxItemTiles = 64), read back with readlane. On a verify pass
+    // ---- block-table entries of the item's tiles, two per lane (tile kt0+l
+    // and kt0+64+l; fast path, at most kMaxItemTiles), read back with
+    // readlane. On a verify pass
     // that is every tile holding a pool key (the boundary tile included);
     // pool_end is the end of the tiles lying wholly in the pool.
     const int tbl_end = a.pool_lens != nullptr ? max(kt0, min(kt1, (pool_len + 15) >> 4)) : kt1;
     const int pool_end = a.pool_lens != nullptr ? max(kt0, min(kt1, pool_len >> 4)) : kt1;
-    int tbl = 0;
+    int tbl = 0, tbl_hi = 0;
     const int tbl_base = kt0;
     if constexpr (FAST) {
         const int idx = kt0 + lane;
         tbl = idx < tbl_end ? a.block_tables[(int64_t)s * a.bt_stride + idx] : 0;
+        if constexpr (kMaxItemTiles > 64)
+            tbl_hi = idx + 64 < tbl_end ? a.block_tables[(int64_t)s * a.bt_stride + idx + 64] : 0;
     }
+    // physical block of the item's tile i (wave-uniform i)
+    auto tbl_at = [&](int i) -> int {
+        const int lo = __builtin_amdgcn_readlane(tbl, i & 63);
+        if constexpr (kMaxItemTiles > 64) return i < 64 ? lo : __builtin_amdgcn_readlane(tbl_hi, i & 63);
+        return lo;
+    };
 
     // ---- columns owned by this lane (one per tile)
     int prow[NT], qhead[NT], qpos[NT];
@@ -416,7 +428,7 @@ void attn_kernel(AttnArgs a) {
     // lie in one block, whose entry is already in tbl.
     auto load_general = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
         int phys = 0;
-        if constexpr (FAST) phys = kt < tbl_end ? __builtin_amdgcn_readlane(tbl, kt - tbl_base) : 0;
+        if constexpr (FAST) phys = kt < tbl_end ? tbl_at(kt - tbl_base) : 0;
         auto row = [&](const char* pool, const char* inflight, int key) -> const char* {
             if constexpr (FAST) {
                 if (key >= kv_len) return nullptr;
@@ -450,7 +462,7 @@ void attn_kernel(AttnArgs a) {
         if constexpr (FAST) {
             // block base is wave-uniform (scalar registers); the lane's byte
             // offsets inside a block never change, so they are computed once
-            const int phys = __builtin_amdgcn_readlane(tbl, kt - tbl_base);
+            const int phys = tbl_at(kt - tbl_base);
             const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
             const char* kb = a.k_pool + boff;
             const char* vb = a.v_pool + boff;
@@ -712,7 +724,7 @@ void attn_kernel(AttnArgs a) {
             // re-reads another wave's piece and does not store it): a
             // conditional load would make every later wait drain all loads.
             auto fetch = [&](int t, regs_t& r) __attribute__((always_inline)) {
-                const int phys = __builtin_amdgcn_readlane(tbl, t - kt0);
+                const int phys = tbl_at(t - kt0);
                 const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
 #pragma unroll
                 for (int i = 0; i < NI; ++i) {
@@ -1004,8 +1016,10 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     };
 
     // Key partition sizes, per item class. Single-column-tile (narrow)
-    // items get their parallelism from splitting keys: enough items to keep
-    // every CU busy, few enough that partials stay small. Wide items already
+    // items get their parallelism from splitting keys: about MF_NARROW_ITEMS
+    // items (two to four waves per SIMD), few enough that partials stay
+    // small. (Measured on C5: 128-tile partitions, 4,192 items, beat 64-tile
+    // ones, 7,320 items: 539 vs 548 us and a merge of 13.5 vs 20 us.) Wide items already
     // come as many column groups, and each split of one costs a 16-column fp32
     // partial per tile written and merged again, so they are split only as far
     // as it takes to reach kWideItems items.

@@ -77,7 +77,7 @@ def test_plan_covers_every_tile_exactly_once_and_merges_line_up(dtype, d, pt):
             assert slot == -1 and merge == -1, "padding item owns a partial slot"
             continue
         assert (row0, nrows, kvl) == (cu[s], q_lens[s], kv[s]), "item carries its sequence's bounds"
-        assert kt1 > kt0 and kt1 - kt0 <= 64
+        assert kt1 > kt0 and kt1 - kt0 <= 128
         for c in range(c0, c0 + nct):
             for kt in range(kt0, kt1):
                 key = (s, h, c, kt)
