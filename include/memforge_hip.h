@@ -82,6 +82,27 @@ int mf_kv_gather(const void* k_pool, const void* v_pool, int pool_dtype,
                  int64_t dst_stride_t, int64_t dst_stride_h, int num_heads,
                  int head_dim, mf_stream_t stream);
 
+/* ---------------------------------------------------------------- block copy
+ * The data half of copy-on-write: for each (src, dst) pair in `pairs` (HOST
+ * memory, int64, num_pairs x 2), copy physical block src to block dst in every
+ * one of `num_layers` layers of both pools. One block of one layer is
+ * `block_elems` contiguous elements at layer * pool_stride_layer +
+ * block * pool_stride_block (PagedKVPool's (layers, blocks, slots, kv_heads,
+ * head_dim) layout: block_elems = slots * kv_heads * head_dim). A pair with
+ * src == dst is skipped. MF_ERR_ARG if an index is outside [0, num_blocks),
+ * a block is the destination of two pairs, or a destination is also a source
+ * (the result would depend on copy order). The pairs go in the kernel
+ * arguments (up to 32 per launch), so nothing is allocated or uploaded.
+ * Replaces prefix_sharing.copy_block
+ * (memforge_ml/runtime/prefix_sharing.py:27-42), which the engine calls when
+ * BlockAllocator::prepare_write returns a pair
+ * (memforge_ml/runtime/continuous_engine.py:974-1006).
+ */
+int mf_kv_copy_blocks(void* k_pool, void* v_pool, int pool_dtype, int num_layers,
+                      int64_t pool_stride_layer, int64_t pool_stride_block,
+                      int64_t block_elems, int64_t num_blocks,
+                      const int64_t* pairs, int num_pairs, mf_stream_t stream);
+
 /* --------------------------------------------------------------- ragged pack
  * Build one step's packed token batch on the device from the scheduler's step
  * output. `entries` (device, int32, B rows of MF_ENTRY_INTS) describes each

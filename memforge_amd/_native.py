@@ -42,6 +42,8 @@ _SIGNATURES = {
                              _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp]),
     "mf_kv_gather": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _vp, _c_i64,
                               _vp, _vp, _c_int, _c_i64, _c_i64, _c_int, _c_int, _vp]),
+    "mf_kv_copy_blocks": (_c_int, [_vp, _vp, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _vp,
+                                   _c_int, _vp]),
     "mf_ragged_pack": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_i64, _vp, _vp, _vp,
                                 _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),
     "mf_paged_attention": (_c_int, [
@@ -203,6 +205,26 @@ def kv_gather(pool: PoolView, slots: torch.Tensor, k_rows: torch.Tensor, v_rows:
         pool.stride_head, pool.block_size, _ptr(slots), T, _ptr(k_rows), _ptr(v_rows),
         dtype_code(k_rows.dtype), k_rows.stride(0), k_rows.stride(1), H, D, _stream(),
     ), "mf_kv_gather")
+
+
+def kv_copy_blocks(key_pool: torch.Tensor, value_pool: torch.Tensor,
+                   pairs: Sequence[Tuple[int, int]]) -> None:
+    """Copy block ``src`` to ``dst`` for every pair, in every layer of the
+    ``(layers, blocks, slots, heads, dim)`` K and V pools (one launch per 32
+    pairs; the pairs go in the kernel arguments)."""
+    if key_pool.dim() != 5 or key_pool.shape != value_pool.shape:
+        raise ValueError("block copy needs (layers, blocks, slots, heads, dim) K and V pools")
+    if key_pool.stride() != value_pool.stride() or key_pool.dtype != value_pool.dtype:
+        raise ValueError("K and V pools must share strides and dtype")
+    L, N, bs, H, D = key_pool.shape
+    if key_pool.stride()[2:] != (H * D, D, 1):
+        raise ValueError("each block of a pool layer must be contiguous")
+    require_device(key_pool, value_pool)
+    flat = np.ascontiguousarray(np.asarray(list(pairs), dtype=np.int64).reshape(-1, 2))
+    _check(lib().mf_kv_copy_blocks(
+        _ptr(key_pool), _ptr(value_pool), dtype_code(key_pool.dtype), L, key_pool.stride(0),
+        key_pool.stride(1), bs * H * D, N, flat.ctypes.data, flat.shape[0], _stream(),
+    ), "mf_kv_copy_blocks")
 
 
 # ---------------------------------------------------------------- attention

@@ -227,3 +227,103 @@ extern "C" int mf_kv_gather(const void* k_pool, const void* v_pool, int pool_dty
     if (num_tokens == 0) return MF_OK;
     return mf::dispatch_copy<true>(dst_dtype, pool_dtype, a, (hipStream_t)stream);
 }
+
+// ------------------------------------------------------------- block copy
+//
+// Copy-on-write data move: block `src` -> block `dst` in every layer of the K
+// and V pools (memforge_ml/runtime/prefix_sharing.py:27-42). One block of one
+// layer is `block_elems` contiguous elements, so the copy is a flat byte move
+// in 16-byte vectors (4-byte words when the block is not 16-byte aligned).
+// The pairs travel in the kernel arguments, so a call allocates nothing and
+// issues no host-to-device copy.
+namespace mf {
+namespace {
+
+constexpr int kCopyPairs = 32;
+
+struct BlockCopyArgs {
+    char* k;
+    char* v;
+    int64_t layer_bytes;  // stride between layers
+    int64_t block_bytes;  // stride between blocks
+    int64_t units;        // vector units per (block, layer)
+    int num_layers;
+    int64_t src[kCopyPairs];
+    int64_t dst[kCopyPairs];
+};
+
+template <typename U>
+__global__ __launch_bounds__(256) void block_copy_kernel(BlockCopyArgs a) {
+    const int pair = blockIdx.z;
+    const int layer = blockIdx.y >> 1;
+    char* base = (blockIdx.y & 1) ? a.v : a.k;
+    base += (int64_t)layer * a.layer_bytes;
+    const U* s = (const U*)(base + a.src[pair] * a.block_bytes);
+    U* d = (U*)(base + a.dst[pair] * a.block_bytes);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.units;
+         i += (int64_t)gridDim.x * blockDim.x)
+        d[i] = s[i];
+}
+
+}  // namespace
+}  // namespace mf
+
+extern "C" int mf_kv_copy_blocks(void* k_pool, void* v_pool, int pool_dtype, int num_layers,
+                                 int64_t pool_stride_layer, int64_t pool_stride_block,
+                                 int64_t block_elems, int64_t num_blocks, const int64_t* pairs,
+                                 int num_pairs, mf_stream_t stream) {
+    if (!mf::dtype_ok(pool_dtype) || num_layers <= 0 || num_layers > 32767 || num_blocks <= 0 ||
+        block_elems <= 0 || num_pairs < 0 || pool_stride_block < block_elems)
+        return MF_ERR_ARG;
+    if (num_layers > 1 && pool_stride_layer < num_blocks * pool_stride_block) return MF_ERR_ARG;
+    if (num_pairs == 0) return MF_OK;
+    if (!k_pool || !v_pool || !pairs) return MF_ERR_ARG;
+    // Every index in range; no block written twice; no block both read and
+    // written (the result would depend on the order of the copies).
+    for (int i = 0; i < num_pairs; ++i) {
+        const int64_t s = pairs[2 * i], d = pairs[2 * i + 1];
+        if (s < 0 || s >= num_blocks || d < 0 || d >= num_blocks) return MF_ERR_ARG;
+        if (s == d) continue;
+        for (int j = 0; j < num_pairs; ++j) {
+            if (pairs[2 * j] == pairs[2 * j + 1]) continue;
+            if (j != i && pairs[2 * j + 1] == d) return MF_ERR_ARG;
+            if (pairs[2 * j] == d) return MF_ERR_ARG;
+        }
+    }
+    const int64_t es = pool_dtype == MF_F32 ? 4 : 2;
+    mf::BlockCopyArgs a{};
+    a.k = (char*)k_pool;
+    a.v = (char*)v_pool;
+    a.layer_bytes = pool_stride_layer * es;
+    a.block_bytes = pool_stride_block * es;
+    a.num_layers = num_layers;
+    const int64_t bytes = block_elems * es;
+    const bool vec16 = bytes % 16 == 0 && a.block_bytes % 16 == 0 && a.layer_bytes % 16 == 0 &&
+                       (uintptr_t)k_pool % 16 == 0 && (uintptr_t)v_pool % 16 == 0;
+    a.units = vec16 ? bytes / 16 : bytes / 4;
+    if (!vec16 && (bytes % 4 || a.block_bytes % 4 || a.layer_bytes % 4 ||
+                   (uintptr_t)k_pool % 4 || (uintptr_t)v_pool % 4))
+        return MF_ERR_ARG;
+    int64_t gx = (a.units + 255) / 256;
+    if (gx > 1024) gx = 1024;
+    for (int first = 0; first < num_pairs;) {
+        int n = 0;
+        for (; first < num_pairs && n < mf::kCopyPairs; ++first) {
+            if (pairs[2 * first] == pairs[2 * first + 1]) continue;
+            a.src[n] = pairs[2 * first];
+            a.dst[n] = pairs[2 * first + 1];
+            ++n;
+        }
+        if (n == 0) break;
+        const dim3 grid((unsigned)gx, (unsigned)(2 * num_layers), (unsigned)n);
+        if (vec16)
+            hipLaunchKernelGGL(mf::block_copy_kernel<uint4>, grid, dim3(256), 0,
+                               (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL(mf::block_copy_kernel<uint32_t>, grid, dim3(256), 0,
+                               (hipStream_t)stream, a);
+        const int st = mf::check_launch();
+        if (st != MF_OK) return st;
+    }
+    return MF_OK;
+}

@@ -6,18 +6,29 @@ prefix_sharing.py:27-140). Which blocks are shared is decided by the C++
 
 from __future__ import annotations
 
-from typing import Any, Dict, Iterable, List, Optional, Tuple
+from typing import Any, Dict, Iterable, List, Optional, Sequence, Tuple
 
+from memforge_amd import _native
 from memforge_amd.runtime.kv_pool import PagedKVPool
 
 
 def copy_block(pool: PagedKVPool, src: int, dst: int) -> None:
-    """Copy block ``src`` to ``dst`` in every layer, K and V (one device copy
-    each over the (layers, blocks, slots, heads, dim) pool); a no-op on itself."""
+    """Copy block ``src`` to ``dst`` in every layer, K and V, with one
+    ``mf_kv_copy_blocks`` launch; a no-op on itself. Must run before the
+    write that triggered the copy-on-write."""
     if src == dst:
         return
-    pool.key_pool[:, dst].copy_(pool.key_pool[:, src])
-    pool.value_pool[:, dst].copy_(pool.value_pool[:, src])
+    copy_blocks(pool, [(src, dst)])
+
+
+def copy_blocks(pool: PagedKVPool, pairs: Sequence[Tuple[int, int]]) -> None:
+    """Several copy-on-write moves in one launch (up to 32 pairs per launch).
+    Raises if an index is out of range, a block is written twice, or a written
+    block is also read."""
+    pairs = [(int(s), int(d)) for s, d in pairs]
+    if not pairs:
+        return
+    _native.kv_copy_blocks(pool.key_pool, pool.value_pool, pairs)
 
 
 def block_owners(runtimes: Iterable[Tuple[int, List[int]]], total_blocks: int) -> Dict[str, List[int]]:

@@ -334,3 +334,32 @@ def test_graphed_engine_output_equals_eager(model, tok):
         assert g2.runtimes[i].generated == hf_greedy(model, tok(p)["input_ids"], 10, stop_on_eos=False)
     g2.step()
     assert g2.allocator.get_num_free_blocks() == g2.allocator.get_total_blocks()
+
+
+def test_copy_on_write_moves_the_shared_block(model, tok):
+    """A block another sequence also holds is copied before a write
+    (test_prefix_sharing.py:270-303): the sequence gets a private block with
+    the same K/V in every layer, and the original keeps its contents."""
+    from memforge_amd.runtime.prefix_sharing import copy_block
+
+    engine = make_engine(model, tok)
+    sid = engine.submit("a prompt to copy on write", greedy(30, stop_on_eos=False))
+    engine.step()
+    seq = engine.scheduler.get_sequence(sid)
+    table = list(seq.get_block_table())
+    target = table[0]
+    assert engine.allocator.add_ref(target)
+    before_k = engine.pool.key_pool[:, target].clone()
+    before_v = engine.pool.value_pool[:, target].clone()
+    cow = engine.allocator.prepare_write(seq, 0)
+    assert cow is not None
+    old_block, new_block = cow
+    assert old_block == target and new_block != target
+    assert seq.get_block_table()[0] == new_block
+    copy_block(engine.pool, old_block, new_block)
+    assert torch.equal(engine.pool.key_pool[:, new_block], before_k)
+    assert torch.equal(engine.pool.value_pool[:, new_block], before_v)
+    assert torch.equal(engine.pool.key_pool[:, old_block], before_k)
+    engine.pool.key_pool[:, 3].fill_(1.5)
+    copy_block(engine.pool, 3, 3)
+    assert bool((engine.pool.key_pool[:, 3] == 1.5).all())

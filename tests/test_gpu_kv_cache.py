@@ -110,3 +110,42 @@ def test_gather_inverts_write(device):
     gv = torch.empty_like(rows_v)
     nat.kv_gather(view, slots, gk, gv)
     assert torch.equal(gk, rows_k) and torch.equal(gv, rows_v)
+
+
+# ------------------------------------------------------------------ block copy
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("geom", [(3, 24, 16, 5, 64), (2, 80, 4, 2, 32), (2, 12, 2, 1, 3), (4, 9, 1, 1, 2)])
+def test_block_copy_moves_whole_blocks_in_every_layer(dt, geom):
+    """mf_kv_copy_blocks against a host copy: destination blocks take the
+    source blocks' bits in every layer of K and V, nothing else changes. The
+    geometries cover 16-byte and 4-byte vector paths and more than 32 pairs
+    (two launches)."""
+    L, N, bs, H, D = geom
+    g = torch.Generator().manual_seed(sum(geom))
+    k = torch.randn((L, N, bs, H, D), generator=g).to(DT[dt])
+    v = torch.randn((L, N, bs, H, D), generator=g).to(DT[dt])
+    perm = torch.randperm(N, generator=g).tolist()
+    half = N // 2
+    pairs = list(zip(perm[:half], perm[half:2 * half]))
+    pairs.append((perm[0], perm[0]))  # on itself: skipped
+    want_k, want_v = bits(k).copy(), bits(v).copy()
+    for s, d in pairs:
+        want_k[:, d] = bits(k)[:, s]
+        want_v[:, d] = bits(v)[:, s]
+    kd, vd = k.cuda(), v.cuda()
+    nat.kv_copy_blocks(kd, vd, pairs)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(kd), want_k)
+    assert np.array_equal(bits(vd), want_v)
+
+
+def test_block_copy_errors_surface_as_exceptions():
+    k = torch.zeros((2, 8, 1, 1, 1), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(nat.MemforgeHipError):  # 2-byte blocks: below the 4-byte unit
+        nat.kv_copy_blocks(k, k.clone(), [(0, 1)])
+    k = torch.zeros((2, 8, 4, 2, 16), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(nat.MemforgeHipError):
+        nat.kv_copy_blocks(k, k.clone(), [(0, 8)])
+    with pytest.raises(ValueError):
+        nat.kv_copy_blocks(k[:, :, :, :, :8], k.clone()[:, :, :, :, :8], [(0, 1)])

@@ -159,3 +159,38 @@ def test_attention_rejects_a_non_finite_scale(scale):
                               None, 4, None, None, None, None, None, None, None, 0, 0,
                               1, 1, 64, scale, None, 1, 0, None, 0, None, 0, None, None)
     assert st == -1, st
+
+
+@pytest.mark.parametrize("pairs", [
+    [(0, 8)],            # destination outside 8 blocks
+    [(-1, 2)],           # negative source
+    [(1, 2), (3, 2)],    # a block written twice
+    [(1, 2), (2, 3)],    # a written block is also read: order-dependent
+])
+def test_block_copy_rejects_bad_pairs_before_any_launch(pairs):
+    """mf_kv_copy_blocks checks every pair on the host first (the pool
+    pointers are never touched, so this runs without a GPU)."""
+    L = nat.lib()
+    flat = np.asarray(pairs, dtype=np.int64).reshape(-1)
+    dummy = 1 << 20  # never dereferenced: the call fails before any launch
+    st = L.mf_kv_copy_blocks(dummy, dummy, 2, 3, 8 * 16 * 4 * 64, 16 * 4 * 64, 16 * 4 * 64, 8,
+                             flat.ctypes.data, len(pairs), None)
+    assert st == -1, st
+
+
+def test_block_copy_pairs_on_themselves_are_a_no_op():
+    L = nat.lib()
+    flat = np.asarray([(3, 3), (5, 5)], dtype=np.int64).reshape(-1)
+    st = L.mf_kv_copy_blocks(1 << 20, 1 << 20, 2, 3, 8 * 1024, 1024, 1024, 8, flat.ctypes.data, 2, None)
+    assert st == 0, st
+
+
+def test_block_copy_rejects_a_bad_geometry():
+    L = nat.lib()
+    flat = np.asarray([(1, 2)], dtype=np.int64)
+    # the block stride is shorter than one block
+    assert L.mf_kv_copy_blocks(1 << 20, 1 << 20, 2, 3, 8 * 1024, 512, 1024, 8, flat.ctypes.data, 1, None) == -1
+    # layers overlap
+    assert L.mf_kv_copy_blocks(1 << 20, 1 << 20, 2, 3, 1024, 1024, 1024, 8, flat.ctypes.data, 1, None) == -1
+    # unknown dtype
+    assert L.mf_kv_copy_blocks(1 << 20, 1 << 20, 7, 3, 8 * 1024, 1024, 1024, 8, flat.ctypes.data, 1, None) == -1
