@@ -16,20 +16,27 @@ batched_speculative.py:98-124, 645-811), re-built around the varlen kernel:
 * ``scatter_accepted_kv`` writes only the confirmed prefix, so rejected
   candidates leave no trace in the pool.
 
-The draft-side proposal loop is kept minimal (one DynamicCache per sequence);
-CUDA-graph draft runners are not part of this build.
+The draft side has two forms. ``propose_draft_tokens`` feeds one sequence
+through its own DynamicCache (the reference's eager draft).
+``BatchedGraphedDraftPool`` drafts every running sequence together: the draft
+model's K/V live in a paged pool of their own, one fixed run of blocks per
+slot, and each of a round's K+1 decode steps is one replay of the captured
+packed pass, with the greedy argmax fed back to the next step on the device.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import List, Optional, Sequence, Tuple
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
 from transformers.cache_utils import DynamicCache
 
 from memforge_amd import _native as nat
 from memforge_amd.kernels import attention_backend
+from memforge_amd.runtime.graphed_paged_decode import GraphedPagedDecoder, _Bucket
+from memforge_amd.runtime.kv_pool import ModelKVSpec, PagedKVPool
+from memforge_amd.runtime.packed_pass import Staging, packed_forward
 from memforge_amd.runtime.varlen_cache import VarlenPackedCache
 from memforge_amd.speculative.rejection_sampler import RejectionSampler
 
@@ -112,6 +119,226 @@ def propose_draft_tokens(draft_model, state: DraftState, tokens: Sequence[int], 
                           past_key_values=state.cache, use_cache=True)
         state.position += 1
     return candidates, probs
+
+
+class BatchedGraphedDraftState:
+    """A sequence's handle on one slot of a ``BatchedGraphedDraftPool``
+    (batched_speculative.py:328-344): ``position`` tokens of the sequence have
+    their draft K/V in the slot's blocks."""
+
+    def __init__(self, pool: "BatchedGraphedDraftPool", slot: int):
+        self.pool = pool
+        self.slot = slot
+        self.position = 0
+
+    def reset(self) -> None:
+        self.position = 0
+
+    def rollback_to(self, position: int) -> None:
+        """Forget the draft K/V past ``position``; O(1), the stale rows are
+        overwritten by later steps and never read before that."""
+        if position < 0:
+            raise ValueError(f"cannot roll a draft back to position {position}")
+        if position > self.position:
+            raise ValueError(f"draft is at {self.position}, behind the requested {position}")
+        self.position = position
+
+
+class BatchedGraphedDraftPool:
+    """The draft model for every running sequence at once
+    (batched_speculative.py:347-577): a round of K proposals costs K+1 graph
+    replays whatever the batch size.
+
+    * The draft's K/V live in a paged pool of its own. Slot i owns the fixed
+      blocks ``[i*nb, (i+1)*nb)``, nb = ceil(max_len / 16), so a slot never
+      allocates and its table never changes.
+    * A decode step is one replay of the captured packed pass (ragged pack,
+      every layer's KV write, the counted varlen attention) over the round's
+      rows, bucketed to powers of two; padding rows write and read nothing. Rows
+      sit at their own positions, and each step's attention plan is made on the
+      host from positions it already knows, so nothing waits for the GPU.
+    * Greedy proposals never leave the GPU inside a round: each step's argmax is
+      copied into the next step's token buffer on the device, and the
+      candidates come back in one read at the end.
+    * ``unroll=True`` captures a whole greedy round -- K+1 steps and the
+      feedback -- as one graph per (bucket, K). Sampling rounds (temperature >
+      0) always go step by step.
+    * A backlog of tokens the draft has not seen (after a round that confirmed
+      several) is fed for all rows together in one eager packed pass.
+    """
+
+    def __init__(self, model, max_len: int, num_slots: int, device: str, unroll: bool = False,
+                 block_size: int = 16):
+        if not str(device).startswith("cuda"):
+            raise ValueError("a graphed draft needs a GPU device")
+        if num_slots < 1 or max_len < 1:
+            raise ValueError("a draft pool needs at least one slot and one position")
+        self.model, self.device = model, device
+        self.max_len = int(max_len)
+        self.num_slots = int(num_slots)
+        self.unroll = bool(unroll)
+        dtype = next(model.parameters()).dtype
+        self.spec = ModelKVSpec.from_config(model.config, dtype, device)
+        self.blocks_per_slot = -(-self.max_len // block_size)
+        self.kv = PagedKVPool(self.spec, num_blocks=self.num_slots * self.blocks_per_slot,
+                              block_size=block_size)
+        nb = self.blocks_per_slot
+        self._tables = [list(range(i * nb, (i + 1) * nb)) for i in range(self.num_slots)]
+        self._decoder = GraphedPagedDecoder(model, self.kv, max_batch=self.num_slots,
+                                            max_model_len=self.max_len)
+        self._staging = Staging(device)
+        self._free = list(range(self.num_slots))
+        self._ugraph: Dict[Tuple[int, int], torch.cuda.CUDAGraph] = {}
+        self._uout: Dict[Tuple[int, int], torch.Tensor] = {}
+        self._ubuckets: Dict[Tuple[int, int], List[_Bucket]] = {}
+        self.replays = 0
+
+    @property
+    def _graph(self) -> Dict[int, torch.cuda.CUDAGraph]:
+        """Captured single-step graphs by bucket size."""
+        return {b: bk.graph for b, bk in self._decoder._buckets.items() if bk.graph is not None}
+
+    # ------------------------------------------------------------- slots
+    def acquire(self) -> BatchedGraphedDraftState:
+        if not self._free:
+            raise RuntimeError("no free draft slot; raise num_slots to max_num_seqs")
+        self._free.sort(reverse=True)  # lowest slot first
+        return BatchedGraphedDraftState(self, self._free.pop())
+
+    def release(self, state: BatchedGraphedDraftState) -> None:
+        if state.slot in self._free:
+            raise ValueError(f"draft slot {state.slot} is already free")
+        state.reset()
+        self._free.append(state.slot)
+
+    # ------------------------------------------------------------- feeding
+    @torch.no_grad()
+    def prefill(self, state: BatchedGraphedDraftState, tokens: Sequence[int]) -> None:
+        """Feed several tokens into one slot eagerly."""
+        self._prefill_many([(state, list(tokens))])
+
+    def _prefill_many(self, runs: List[Tuple[BatchedGraphedDraftState, List[int]]]) -> None:
+        runs = [(st, toks) for st, toks in runs if toks]
+        if not runs:
+            return
+        for st, toks in runs:
+            if st.position + len(toks) > self.max_len:
+                raise ValueError(f"draft context {st.position + len(toks)} exceeds {self.max_len}")
+        packed_forward(self.model, self.kv, self._staging, [toks for _, toks in runs],
+                       [st.position for st, _ in runs], [self._tables[st.slot] for st, _ in runs],
+                       keep_rows=[0])
+        for st, toks in runs:
+            st.position += len(toks)
+
+    # ------------------------------------------------------------- rounds
+    @torch.no_grad()
+    def propose(self, states: Sequence[BatchedGraphedDraftState], tokens_list: Sequence[Sequence[int]],
+                lookahead: int, temperature: float):
+        """K candidates and the draft's K distributions for every state.
+
+        Any backlog but the last pending token is prefilled first; then the
+        last token and each candidate are fed one step at a time, the final
+        candidate included, so its K/V survives a fully accepted round
+        (batched_speculative.py:514-577). Every state advances by K+1."""
+        if len(states) != len(tokens_list):
+            raise ValueError(f"{len(states)} states for {len(tokens_list)} token lists")
+        if not states:
+            return []
+        k = int(lookahead)
+        backlog = []
+        for st, toks in zip(states, tokens_list):
+            if st.pool is not self:
+                raise ValueError("draft state belongs to another pool")
+            pending = list(toks[st.position:])
+            if not pending:
+                raise ValueError(f"draft is at position {st.position} with only {len(toks)} tokens")
+            if len(toks) + k > self.max_len:
+                raise ValueError(f"draft round reaches position {len(toks) + k - 1}, past {self.max_len - 1}")
+            if len(pending) > 1:
+                backlog.append((st, pending[:-1]))
+        self._prefill_many(backlog)
+
+        n = len(states)
+        pos = [st.position for st in states]
+        tables = [self._tables[st.slot] for st in states]
+        last = [int(toks[-1]) for toks in tokens_list]
+        if self.unroll and temperature <= 0.0 and k > 0:
+            cand_dev = self._unrolled_round(n, k, last, pos, tables)
+            cand = cand_dev.tolist()  # the round's one read-back
+            vocab = self.model.get_output_embeddings().weight.shape[0]
+            onehot = torch.zeros((n, k, vocab), dtype=torch.float32, device=self.device)
+            onehot.scatter_(2, cand_dev[:, :, None], 1.0)
+            for st in states:
+                st.position += k + 1
+            return [(cand[i], [onehot[i, j] for j in range(k)]) for i in range(n)]
+
+        step_tokens: List[torch.Tensor] = []
+        step_probs: List[torch.Tensor] = []
+        nxt: Optional[torch.Tensor] = None
+        for j in range(k + 1):
+            logits = self._decoder.logits_view(last, [p + j for p in pos], tables, device_tokens=nxt)
+            self.replays += 1
+            if j == k:
+                break  # the last step only caches the final candidate's K/V
+            probs = _probs_from_logits_rows(logits.float(), temperature)
+            nxt = probs.argmax(-1) if temperature <= 0.0 else torch.multinomial(probs, 1)[:, 0]
+            step_tokens.append(nxt)
+            step_probs.append(probs)
+        cand = torch.stack(step_tokens, dim=1).tolist() if k else [[] for _ in range(n)]
+        for st in states:
+            st.position += k + 1
+        return [(cand[i], [step_probs[j][i] for j in range(k)]) for i in range(n)]
+
+    def _unrolled_round(self, n: int, k: int, last: List[int], pos: List[int],
+                        tables: List[List[int]]) -> torch.Tensor:
+        """A greedy round as one replay: K+1 captured steps, each with its own
+        static inputs and plan, the argmax of step j written into step j+1's
+        token buffer inside the graph. Returns the (n, K) candidates."""
+        b = self._decoder._batch_bucket(n)
+        if b > self.num_slots:
+            raise ValueError(f"batch {n} exceeds {self.num_slots} draft slots")
+        key = (b, k)
+        buckets = self._ubuckets.get(key)
+        if buckets is None:
+            buckets = self._ubuckets[key] = [_Bucket(self._decoder, b) for _ in range(k + 1)]
+        for j, bk in enumerate(buckets):
+            self._decoder._stage(bk, last if j == 0 else [0] * n, [p + j for p in pos], tables)
+        if key not in self._ugraph:
+            self._capture_unrolled(key, buckets)
+        self._ugraph[key].replay()
+        self.replays += 1
+        return self._uout[key][:n]
+
+    def _unrolled_body(self, buckets: List[_Bucket]) -> torch.Tensor:
+        k = len(buckets) - 1
+        cands = torch.empty((buckets[0].b, k), dtype=torch.long, device=self.device)
+        for j, bk in enumerate(buckets):
+            logits = self._decoder._forward(bk)
+            if j < k:
+                nxt = logits.argmax(-1)
+                cands[:, j].copy_(nxt)
+                buckets[j + 1].tokens.copy_(nxt)
+        return cands
+
+    def _capture_unrolled(self, key: Tuple[int, int], buckets: List[_Bucket]) -> None:
+        # one eager round on a side stream first (allocator and library
+        # warm-up; it computes exactly what the replay then recomputes), then
+        # the capture
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for bk in buckets:
+                bk.binding.used = 0
+            self._unrolled_body(buckets)
+            for bk in buckets:
+                if bk.binding.used != self.spec.num_layers:
+                    raise RuntimeError(f"unrolled draft: {bk.binding.used} of {self.spec.num_layers} "
+                                       "layers used the varlen kernel")
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, pool=self._decoder._mem_pool):
+            self._uout[key] = self._unrolled_body(buckets)
+        self._ugraph[key] = graph
 
 
 @torch.no_grad()

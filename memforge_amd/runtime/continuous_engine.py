@@ -33,6 +33,7 @@ from __future__ import annotations
 import logging
 import threading
 import time
+import warnings
 from collections import deque
 from dataclasses import dataclass, field
 from typing import Any, Deque, Dict, List, Optional
@@ -43,6 +44,8 @@ import torch
 from memforge_amd import _native as nat
 from memforge_amd.kernels import attention_backend
 from memforge_amd.runtime.batched_speculative import (
+    BatchedGraphedDraftPool,
+    BatchedGraphedDraftState,
     DraftState,
     propose_draft_tokens,
     resolve_round,
@@ -51,9 +54,9 @@ from memforge_amd.runtime.batched_speculative import (
 )
 from memforge_amd.runtime.graphed_paged_decode import GraphedPagedDecoder
 from memforge_amd.runtime.kv_pool import ModelKVSpec, PagedKVPool
+from memforge_amd.runtime.packed_pass import Staging, packed_forward
 from memforge_amd.runtime.prefix_sharing import block_owners, copy_block, sharing_telemetry
 from memforge_amd.runtime.sampling import SamplingParams, sample_logits
-from memforge_amd.runtime.varlen_cache import VarlenPackedCache
 
 LOGGER = logging.getLogger(__name__)
 
@@ -152,32 +155,6 @@ class StepReport:
     events: List[TokenEvent]
 
 
-class _Staging:
-    """Grow-only pinned host buffer and its device twin for the per-step
-    descriptors, so a step's metadata crosses PCIe in one copy."""
-
-    def __init__(self, device):
-        self.device = device
-        self.host = torch.empty(0, dtype=torch.int32).pin_memory()
-        self.dev = torch.empty(0, dtype=torch.int32, device=device)
-        self.copied = None  # event recorded after the last copy out of ``host``
-
-    def upload(self, arr: np.ndarray) -> torch.Tensor:
-        n = arr.size
-        if self.copied is not None:
-            # the previous copy must have left the pinned buffer before it is rewritten
-            self.copied.synchronize()
-        if self.host.numel() < n:
-            cap = max(n, 2 * self.host.numel(), 1 << 16)
-            self.host = torch.empty(cap, dtype=torch.int32).pin_memory()
-            self.dev = torch.empty(cap, dtype=torch.int32, device=self.device)
-        self.host[:n].numpy()[:] = arr
-        self.dev[:n].copy_(self.host[:n], non_blocking=True)
-        self.copied = torch.cuda.Event()
-        self.copied.record()
-        return self.dev[:n]
-
-
 class ContinuousBatchingEngine:
     def __init__(self, model, tokenizer, *, block_size: int = 16, num_blocks: Optional[int] = None,
                  kv_budget_mb: float = 512.0, max_num_seqs: int = 16, max_model_len: int = 2048,
@@ -224,16 +201,39 @@ class ContinuousBatchingEngine:
                                               self.max_prefill_tokens_per_step, lookahead_slots)
         if not attention_backend.register():
             raise RuntimeError("the transformers attention registry is required")
-        self._staging = _Staging(self.device)
+        self._staging = Staging(self.device)
         # Pure-decode steps replay a captured HIP graph of the packed pass
         # (False | True | "auto", as the reference's paged_cuda_graph; "auto"
         # is on whenever the model's head grouping allows it).
         self._paged_graph = None
         if paged_cuda_graph:
-            hq, hkv = model.config.num_attention_heads, self.spec.num_kv_heads
-            if paged_cuda_graph != "auto" or (hq % hkv == 0 and hq // hkv <= 16):
+            if paged_cuda_graph != "auto" or self._graph_heads_ok(model):
                 self._paged_graph = GraphedPagedDecoder(model, self.pool, max_batch=max_num_seqs,
                                                         max_model_len=max_model_len)
+
+        # Draft proposals (False | "batched" | "batched-unrolled" | "auto" |
+        # True, as the reference's draft_cuda_graph): the batched forms draft
+        # every running sequence in K+1 graph replays per round (one replay
+        # when unrolled), with the greedy feedback on the device. "auto" picks
+        # "batched" whenever the draft's head grouping allows it. True, the
+        # reference's superseded per-sequence graphs, runs as "batched".
+        self._draft_pool = None
+        if draft_cuda_graph == "auto":
+            draft_cuda_graph = "batched" if (draft_model is not None
+                                             and self._graph_heads_ok(draft_model)) else False
+        if draft_cuda_graph is True:
+            warnings.warn(
+                "draft_cuda_graph=True (one graph per sequence) is superseded by 'batched', which "
+                "drafts the whole batch per replay; it runs as 'batched'. Pass draft_cuda_graph="
+                "'batched' or 'auto'.", DeprecationWarning, stacklevel=2)
+            draft_cuda_graph = "batched"
+        if draft_cuda_graph and draft_model is not None and self.lookahead_k > 0:
+            if draft_cuda_graph not in ("batched", "batched-unrolled"):
+                raise ValueError(f"draft_cuda_graph must be False, True, 'auto', 'batched' or "
+                                 f"'batched-unrolled', got {draft_cuda_graph!r}")
+            self._draft_pool = BatchedGraphedDraftPool(
+                draft_model, max_len=max_model_len, num_slots=max_num_seqs, device=self.device,
+                unroll=draft_cuda_graph == "batched-unrolled")
 
         self.eos_token_ids = self._resolve_eos_ids()
         self.runtimes: Dict[int, SequenceRuntime] = {}
@@ -264,6 +264,14 @@ class ContinuousBatchingEngine:
         self._recent_tokens: Deque[float] = deque()
 
     # ------------------------------------------------------------------ setup
+
+    @staticmethod
+    def _graph_heads_ok(model) -> bool:
+        """The captured decode pass handles up to 16 query heads per KV head."""
+        cfg = model.config
+        hq = cfg.num_attention_heads
+        hkv = getattr(cfg, "num_key_value_heads", None) or hq
+        return hq % hkv == 0 and hq // hkv <= 16
 
     def _resolve_eos_ids(self) -> set:
         ids = set()
@@ -369,6 +377,9 @@ class ContinuousBatchingEngine:
             rt = self.runtimes.get(seq_id)
             if rt is not None and rt.cache is not None:
                 rt.cache = None
+                # a waiting sequence holds no draft slot; the next round
+                # re-feeds its draft from the start
+                self._release_draft(rt)
                 rt.num_preemptions += 1
                 self.total_preemptions += 1
 
@@ -470,66 +481,22 @@ class ContinuousBatchingEngine:
 
     def _run_packed(self, plan: List[dict]) -> List[TokenEvent]:
         """One forward over every entry of ``plan`` (prefill chunks, then decodes)."""
-        bs = self.block_size
-        B = len(plan)
         q_lens = [len(e["tokens"]) for e in plan]
-        starts = [e["start"] for e in plan]
-        kv_lens = [s + q for s, q in zip(starts, q_lens)]
-        tables = [e["table"] for e in plan]
-        for e, kv, t in zip(plan, kv_lens, tables):
-            if kv > len(t) * bs:
-                raise IndexError(f"sequence {e['rt'].seq_id} needs {kv} slots but its block table "
-                                 f"has {len(t)} blocks of {bs}")
-        max_blocks = max(len(t) for t in tables)
-        T = int(sum(q_lens))
-        cu = np.zeros(B + 1, dtype=np.int64)
-        np.cumsum(q_lens, out=cu[1:])
-
-        # descriptors | tables | tokens in one int32 upload
-        ent = np.empty((B, nat.ENTRY_INTS), dtype=np.int32)
-        t_off = np.zeros(B, dtype=np.int64)
-        t_off[1:] = np.cumsum([len(t) for t in tables])[:-1]
-        ent[:, 0] = q_lens
-        ent[:, 1] = starts
-        ent[:, 2] = kv_lens
-        ent[:, 3] = t_off
-        ent[:, 4] = [len(t) for t in tables]
-        ent[:, 5] = cu[:-1]
-        flat_tables = np.fromiter((b for t in tables for b in t), dtype=np.int32)
-        flat_tokens = np.fromiter((tok for e in plan for tok in e["tokens"]), dtype=np.int32)
-        buf = np.concatenate([ent.reshape(-1), flat_tables, flat_tokens])
-        dev = self._staging.upload(buf)
-        ne, nt = ent.size, flat_tables.size
-        packed = nat.ragged_pack(dev[:ne].view(B, nat.ENTRY_INTS), dev[ne:ne + nt], dev[ne + nt:],
-                                 T, bs, max_blocks)
-        attn_plan = nat.plan_attention(cu.tolist(), kv_lens, self.model.config.num_attention_heads,
-                                       self.spec.num_kv_heads, self.spec.head_dim, self.dtype, self.device)
-        meta = {"block_tables": packed.block_tables, "cu_seqlens": packed.cu_seqlens,
-                "kv_lens": packed.kv_lens, "positions": packed.positions, "row_map": None,
-                "plan": attn_plan}
-        binding = attention_backend._VarlenBinding.from_packed(self.pool, meta, T)
-        cache = VarlenPackedCache.from_slot_mapping(self.pool, self.spec.num_layers, packed.slot_mapping)
-
+        cu = np.concatenate([[0], np.cumsum(q_lens)])
         # only rows that produce a token go through the LM head
         emit = [i for i, e in enumerate(plan) if e["kind"] == "decode" or e["is_final"]]
-        keep = torch.tensor([int(cu[i + 1]) - 1 for i in emit], dtype=torch.long).to(self.device)
-        with attention_backend.backend_enabled_on(self.model) as routed:
-            if not routed:
-                raise RuntimeError("the packed pass needs the attention registry")
-            with attention_backend.bind_varlen(binding):
-                with torch.no_grad():
-                    out = self.model(input_ids=packed.token_ids.view(1, T),
-                                     position_ids=packed.positions.view(1, T),
-                                     past_key_values=cache, use_cache=True, logits_to_keep=keep)
-        if binding.used != self.spec.num_layers:
-            raise RuntimeError(f"packed pass: {binding.used} of {self.spec.num_layers} layers used the kernel")
+        try:
+            res = packed_forward(self.model, self.pool, self._staging, [e["tokens"] for e in plan],
+                                 [e["start"] for e in plan], [e["table"] for e in plan],
+                                 [int(cu[i + 1]) - 1 for i in emit])
+        except IndexError as exc:
+            raise IndexError(f"{exc} (sequences {[e['rt'].seq_id for e in plan]})") from None
         self.total_forward_passes += 1
-        self.total_blockwise_layers += binding.used
-        self.total_fused_tokens += T
-        self.total_attended_kv_tokens += int(sum(kv_lens))
-        self.total_packed_rows += T
-
-        return self._emit(plan, emit, out.logits[0])
+        self.total_blockwise_layers += res.layers_used
+        self.total_fused_tokens += res.num_tokens
+        self.total_attended_kv_tokens += int(sum(res.kv_lens))
+        self.total_packed_rows += res.num_tokens
+        return self._emit(plan, emit, res.logits)
 
     def _run_graphed(self, plan: List[dict]) -> List[TokenEvent]:
         """A decode-only step as one replay of the captured packed pass."""
@@ -594,15 +561,27 @@ class ContinuousBatchingEngine:
         """Draft proposals, one batched verify pass, rejection, confirmed-prefix
         write (continuous_engine.py:1212-1341)."""
         k = self.lookahead_k
-        proposals, draft_probs, token_counts = [], [], []
+        proposals: List[List[int]] = [[] for _ in rts]
+        draft_probs: List[List[torch.Tensor]] = [[] for _ in rts]
+        token_counts = [len(rt.tokens) for rt in rts]
         for rt in rts:
             if rt.draft is None:
-                rt.draft = DraftState()
-            token_counts.append(len(rt.tokens))
-            cand, probs = propose_draft_tokens(self.draft_model, rt.draft, rt.tokens, k,
-                                               rt.params.temperature, self.device)
-            proposals.append(cand)
-            draft_probs.append(probs)
+                rt.draft = self._draft_pool.acquire() if self._draft_pool is not None else DraftState()
+        if self._draft_pool is not None:
+            # K+1 replays per temperature present (the reference requires a
+            # single temperature per round; rows keep their order either way)
+            groups: Dict[float, List[int]] = {}
+            for row, rt in enumerate(rts):
+                groups.setdefault(float(rt.params.temperature), []).append(row)
+            for temp, rows in groups.items():
+                out = self._draft_pool.propose([rts[r].draft for r in rows], [rts[r].tokens for r in rows],
+                                               k, temp)
+                for r, (cand, probs) in zip(rows, out):
+                    proposals[r], draft_probs[r] = cand, probs
+        else:
+            for row, rt in enumerate(rts):
+                proposals[row], draft_probs[row] = propose_draft_tokens(
+                    self.draft_model, rt.draft, rt.tokens, k, rt.params.temperature, self.device)
         ctx = [rt.cache.position for rt in rts]
         tables = [rt.cache.block_table_tensor(self.device) for rt in rts]
         queries = [[rt.tokens[-1]] + cand for rt, cand in zip(rts, proposals)]
@@ -638,6 +617,11 @@ class ContinuousBatchingEngine:
 
     # ------------------------------------------------------------ bookkeeping
 
+    def _release_draft(self, rt: SequenceRuntime) -> None:
+        if isinstance(rt.draft, BatchedGraphedDraftState):
+            self._draft_pool.release(rt.draft)
+        rt.draft = None
+
     def _accept_token(self, rt: SequenceRuntime, token_id: int, source: str) -> Optional[TokenEvent]:
         now = time.perf_counter()
         if rt.first_token_at is None:
@@ -670,7 +654,7 @@ class ContinuousBatchingEngine:
             return
         rt.finish_reason = reason
         rt.finished_at = time.perf_counter()
-        rt.draft = None
+        self._release_draft(rt)
         rt.cache = None  # the scheduler frees the physical blocks on its next step
 
     # ----------------------------------------------------------------- output
@@ -774,6 +758,8 @@ class ContinuousBatchingEngine:
             "paged_cuda_graph_enabled": self._paged_graph is not None,
             "graph_replays": self._paged_graph.replays if self._paged_graph is not None else 0,
             "graph_captures": self._paged_graph.captures if self._paged_graph is not None else 0,
+            "draft_graph_enabled": self._draft_pool is not None,
+            "draft_graph_replays": self._draft_pool.replays if self._draft_pool is not None else 0,
             "blockwise_layer_calls": self.total_blockwise_layers,
             "blockwise_fallbacks": self.total_blockwise_fallbacks,
             "attended_kv_tokens": self.total_attended_kv_tokens,

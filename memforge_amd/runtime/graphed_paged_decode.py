@@ -25,7 +25,7 @@ are never read.
 from __future__ import annotations
 
 import math
-from typing import Dict, Sequence
+from typing import Dict, Optional, Sequence
 
 import numpy as np
 import torch
@@ -95,12 +95,12 @@ class GraphedPagedDecoder:
         self.replays = 0
         self.captures = 0
 
-    @staticmethod
-    def _batch_bucket(b: int) -> int:
+    def _batch_bucket(self, b: int) -> int:
+        """Powers of two, capped at max_batch (so any max_batch is a bucket)."""
         p = 1
         while p < b:
             p *= 2
-        return p
+        return min(p, self.max_batch) if b <= self.max_batch else p
 
     def _forward(self, bk: _Bucket) -> torch.Tensor:
         nat.ragged_pack(bk.entries, bk.tables, bk.tokens, bk.b, self.bs, self.max_blocks, out=bk.packed)
@@ -165,12 +165,8 @@ class GraphedPagedDecoder:
                                                         self.pool.key_pool.dtype)
         bk.plan.update(items, merges, counts)
 
-    @torch.no_grad()
-    def logits_view(self, tokens: Sequence[int], ctx_lens: Sequence[int],
-                    block_tables: Sequence[Sequence[int]]) -> torch.Tensor:
-        """Like ``step`` but returns a view of the graph's output, valid until
-        the next call."""
-        n = len(tokens)
+    def bucket(self, n: int) -> _Bucket:
+        """The static buffers (and graph, once captured) for a batch of ``n``."""
         if n == 0:
             raise ValueError("step() needs at least one sequence")
         b = self._batch_bucket(n)
@@ -179,8 +175,24 @@ class GraphedPagedDecoder:
         bk = self._buckets.get(b)
         if bk is None:
             bk = self._buckets[b] = _Bucket(self, b)
+        return bk
+
+    @torch.no_grad()
+    def logits_view(self, tokens: Sequence[int], ctx_lens: Sequence[int],
+                    block_tables: Sequence[Sequence[int]],
+                    device_tokens: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Like ``step`` but returns a view of the graph's output, valid until
+        the next call. With ``device_tokens`` (n integers on the GPU, e.g. the
+        previous step's argmax) the input tokens are taken from there by a
+        device copy, and ``tokens`` is ignored: nothing waits for the host."""
+        n = len(ctx_lens)
+        if device_tokens is None and len(tokens) != n:
+            raise ValueError(f"{len(tokens)} tokens for {n} rows")
+        bk = self.bucket(n)
         tables = [t.tolist() if isinstance(t, torch.Tensor) else list(t) for t in block_tables]
-        self._stage(bk, tokens, ctx_lens, tables)
+        self._stage(bk, tokens if device_tokens is None else [0] * n, ctx_lens, tables)
+        if device_tokens is not None:
+            bk.tokens[:n].copy_(device_tokens.view(-1)[:n])
         if bk.graph is None:
             self._capture(bk)
         bk.graph.replay()

@@ -1,0 +1,116 @@
+"""One eager packed varlen pass of a model over a paged pool.
+
+Every contributing sequence adds a run of query tokens at consecutive
+positions ``start .. start + len - 1`` whose K/V are written through its block
+table. The descriptors, tables and token ids are staged in pinned memory and
+cross PCIe in one copy; the ragged-pack kernel builds token ids, positions,
+slot_mapping, cu_seqlens and padded tables on the device; each layer's cache
+update is the KV-write kernel and its attention the varlen kernel reading the
+pool in place. This is the reference's fused varlen step
+(memforge_ml/runtime/continuous_engine.py:782-905) with the gather, the padding
+and the Python list building moved onto the GPU.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List, Sequence
+
+import numpy as np
+import torch
+
+from memforge_amd import _native as nat
+from memforge_amd.kernels import attention_backend
+from memforge_amd.runtime.varlen_cache import VarlenPackedCache
+
+
+class Staging:
+    """Grow-only pinned host buffer and its device twin for the per-pass
+    descriptors, so a pass's metadata crosses PCIe in one copy."""
+
+    def __init__(self, device):
+        self.device = device
+        self.host = torch.empty(0, dtype=torch.int32).pin_memory()
+        self.dev = torch.empty(0, dtype=torch.int32, device=device)
+        self.copied = None  # event recorded after the last copy out of ``host``
+
+    def upload(self, arr: np.ndarray) -> torch.Tensor:
+        n = arr.size
+        if self.copied is not None:
+            # the previous copy must have left the pinned buffer before it is rewritten
+            self.copied.synchronize()
+        if self.host.numel() < n:
+            cap = max(n, 2 * self.host.numel(), 1 << 16)
+            self.host = torch.empty(cap, dtype=torch.int32).pin_memory()
+            self.dev = torch.empty(cap, dtype=torch.int32, device=self.device)
+        self.host[:n].numpy()[:] = arr
+        self.dev[:n].copy_(self.host[:n], non_blocking=True)
+        self.copied = torch.cuda.Event()
+        self.copied.record()
+        return self.dev[:n]
+
+
+@dataclass
+class PackedPassResult:
+    logits: torch.Tensor      # (len(keep_rows), vocab), rows in keep_rows order
+    cu_seqlens: np.ndarray    # (B + 1,) host prefix sums of the query lengths
+    kv_lens: List[int]        # keys each sequence's attention read
+    num_tokens: int           # packed query rows
+    layers_used: int          # layers whose attention ran through the varlen kernel
+
+
+@torch.no_grad()
+def packed_forward(model, pool, staging: Staging, tokens: Sequence[Sequence[int]],
+                   starts: Sequence[int], tables: Sequence[Sequence[int]],
+                   keep_rows: Sequence[int]) -> PackedPassResult:
+    """Run ``model`` once over every sequence's ``tokens`` (written at
+    ``starts[i]`` onward through ``tables[i]``) and return the logits of the
+    packed rows ``keep_rows``. Raises IndexError when a run does not fit its
+    table, and RuntimeError when a layer did not use the varlen kernel."""
+    bs = pool.block_size
+    spec = pool.spec
+    B = len(tokens)
+    q_lens = [len(t) for t in tokens]
+    kv_lens = [int(s) + q for s, q in zip(starts, q_lens)]
+    for i, (kv, t) in enumerate(zip(kv_lens, tables)):
+        if kv > len(t) * bs:
+            raise IndexError(f"entry {i} needs {kv} slots but its block table has {len(t)} blocks of {bs}")
+    max_blocks = max(len(t) for t in tables)
+    T = int(sum(q_lens))
+    cu = np.zeros(B + 1, dtype=np.int64)
+    np.cumsum(q_lens, out=cu[1:])
+
+    # descriptors | tables | tokens in one int32 upload
+    ent = np.empty((B, nat.ENTRY_INTS), dtype=np.int32)
+    t_off = np.zeros(B, dtype=np.int64)
+    t_off[1:] = np.cumsum([len(t) for t in tables])[:-1]
+    ent[:, 0] = q_lens
+    ent[:, 1] = starts
+    ent[:, 2] = kv_lens
+    ent[:, 3] = t_off
+    ent[:, 4] = [len(t) for t in tables]
+    ent[:, 5] = cu[:-1]
+    flat_tables = np.fromiter((b for t in tables for b in t), dtype=np.int32)
+    flat_tokens = np.fromiter((tok for run in tokens for tok in run), dtype=np.int32)
+    buf = np.concatenate([ent.reshape(-1), flat_tables, flat_tokens])
+    dev = staging.upload(buf)
+    ne, nt = ent.size, flat_tables.size
+    packed = nat.ragged_pack(dev[:ne].view(B, nat.ENTRY_INTS), dev[ne:ne + nt], dev[ne + nt:],
+                             T, bs, max_blocks)
+    attn_plan = nat.plan_attention(cu.tolist(), kv_lens, model.config.num_attention_heads,
+                                   spec.num_kv_heads, spec.head_dim, pool.key_pool.dtype, spec.device)
+    meta = {"block_tables": packed.block_tables, "cu_seqlens": packed.cu_seqlens,
+            "kv_lens": packed.kv_lens, "positions": packed.positions, "row_map": None,
+            "plan": attn_plan}
+    binding = attention_backend._VarlenBinding.from_packed(pool, meta, T)
+    cache = VarlenPackedCache.from_slot_mapping(pool, spec.num_layers, packed.slot_mapping)
+    keep = torch.tensor(list(keep_rows), dtype=torch.long).to(spec.device)
+    with attention_backend.backend_enabled_on(model) as routed:
+        if not routed:
+            raise RuntimeError("the packed pass needs the attention registry")
+        with attention_backend.bind_varlen(binding):
+            out = model(input_ids=packed.token_ids.view(1, T), position_ids=packed.positions.view(1, T),
+                        past_key_values=cache, use_cache=True, logits_to_keep=keep)
+    if binding.used != spec.num_layers:
+        raise RuntimeError(f"packed pass: {binding.used} of {spec.num_layers} layers used the kernel")
+    return PackedPassResult(out.logits[0], cu, kv_lens, T, binding.used)

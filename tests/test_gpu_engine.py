@@ -363,3 +363,181 @@ def test_copy_on_write_moves_the_shared_block(model, tok):
     engine.pool.key_pool[:, 3].fill_(1.5)
     copy_block(engine.pool, 3, 3)
     assert bool((engine.pool.key_pool[:, 3] == 1.5).all())
+
+
+# ------------------------------------------------------------ batched draft
+
+
+DRAFT_PROMPTS = ["alpha prompt", "a much longer beta prompt here, with more to say", "gamma",
+                 "the fourth one, mid length"]
+
+
+def _spec_run(model, tok, prompts, params=None, slots=4, **kw):
+    eng = make_engine(model, tok, num_blocks=256, max_num_seqs=slots, max_model_len=256, **kw)
+    res = eng.generate(prompts, params or greedy(16, stop_on_eos=False))
+    return eng, [r["token_ids"] for r in res], [r["token_sources"] for r in res]
+
+
+def test_batched_draft_matches_plain_and_the_eager_draft(model, draft, tok):
+    """Batched graphed drafting changes speed only: tokens equal plain decoding
+    and the eager draft, and the proposals (token sources) equal the eager
+    draft's (test_batched_graphed_draft.py:44-53)."""
+    _, plain, _ = _spec_run(model, tok, DRAFT_PROMPTS)
+    _, eager, eager_src = _spec_run(model, tok, DRAFT_PROMPTS, draft_model=draft, lookahead_k=4)
+    eng, got, src = _spec_run(model, tok, DRAFT_PROMPTS, draft_model=draft, lookahead_k=4,
+                              draft_cuda_graph="batched")
+    assert got == plain == eager
+    assert src == eager_src, "batched draft proposes different tokens than the eager draft"
+    eng_self, got_self, src_self = _spec_run(model, tok, DRAFT_PROMPTS, draft_model=model, lookahead_k=4,
+                                             draft_cuda_graph="batched")
+    assert got_self == plain
+    assert any(x == "draft" for seq in src_self for x in seq), "nothing was ever accepted"
+    assert eng_self.telemetry()["draft_acceptance_rate"] == 1.0
+    pool = eng._draft_pool
+    assert len(pool._free) == 4 and pool._graph
+    t = eng.telemetry()
+    assert t["draft_graph_enabled"] and t["draft_graph_replays"] > 0
+
+
+@pytest.mark.parametrize("n_prompts,slots", [(1, 4), (2, 4), (3, 8), (7, 4)])
+def test_batched_draft_any_batch_size(model, draft, tok, n_prompts, slots):
+    prompts = (DRAFT_PROMPTS * 2)[:n_prompts]
+    _, plain, _ = _spec_run(model, tok, prompts, slots=slots)
+    eng, got, _ = _spec_run(model, tok, prompts, slots=slots, draft_model=draft, lookahead_k=3,
+                            draft_cuda_graph="batched")
+    assert got == plain
+    assert len(eng._draft_pool._free) == slots
+
+
+def test_batched_draft_replays_per_round_do_not_grow_with_the_batch(model, draft, tok):
+    eng, _, _ = _spec_run(model, tok, DRAFT_PROMPTS, draft_model=draft, lookahead_k=3,
+                          draft_cuda_graph="batched")
+    before_replays, before_rounds = eng._draft_pool.replays, eng.total_speculative_rounds
+    eng.generate(DRAFT_PROMPTS, greedy(16, stop_on_eos=False))
+    replays = eng._draft_pool.replays - before_replays
+    rounds = eng.total_speculative_rounds - before_rounds
+    assert rounds > 0 and replays == rounds * (3 + 1)
+
+
+def test_batched_draft_sampling_runs_and_frees_slots(model, draft, tok):
+    from memforge_amd.runtime.sampling import SamplingParams
+
+    params = SamplingParams(max_new_tokens=16, temperature=0.8, top_p=1.0, stop_on_eos=False)
+    torch.manual_seed(0)
+    eng, got, _ = _spec_run(model, tok, DRAFT_PROMPTS, params=params, draft_model=draft, lookahead_k=3,
+                            draft_cuda_graph="batched")
+    assert all(len(g) == 16 for g in got) and len(eng._draft_pool._free) == 4
+
+
+def test_batched_draft_mixed_temperatures_keep_greedy_rows_exact(model, draft, tok):
+    """Rows with different temperatures are drafted per temperature group; the
+    greedy rows still equal plain decoding."""
+    from memforge_amd.runtime.sampling import SamplingParams
+
+    eng = make_engine(model, tok, num_blocks=256, max_num_seqs=4, max_model_len=256, draft_model=draft,
+                      lookahead_k=3, draft_cuda_graph="batched")
+    g = eng.submit(DRAFT_PROMPTS[1], greedy(16, stop_on_eos=False))
+    s = eng.submit(DRAFT_PROMPTS[3], SamplingParams(max_new_tokens=16, temperature=0.9, stop_on_eos=False))
+    eng.run_until_idle()
+    want = hf_greedy(model, tok(DRAFT_PROMPTS[1])["input_ids"], 16, stop_on_eos=False)
+    assert eng.runtimes[g].generated == want
+    assert len(eng.runtimes[s].generated) == 16 and len(eng._draft_pool._free) == 4
+
+
+@pytest.mark.parametrize("n_prompts,slots", [(1, 4), (3, 4), (4, 8), (7, 4)])
+def test_unrolled_draft_one_replay_per_round_matches_eager(model, draft, tok, n_prompts, slots):
+    prompts = (DRAFT_PROMPTS * 2)[:n_prompts]
+    _, plain, _ = _spec_run(model, tok, prompts, slots=slots)
+    _, eager, esrc = _spec_run(model, tok, prompts, slots=slots, draft_model=draft, lookahead_k=4)
+    eng, got, src = _spec_run(model, tok, prompts, slots=slots, draft_model=draft, lookahead_k=4,
+                              draft_cuda_graph="batched-unrolled")
+    assert got == plain == eager
+    assert src == esrc, "unrolled draft proposes different tokens than the eager draft"
+    pool = eng._draft_pool
+    assert pool._ugraph and len(pool._free) == slots
+    assert pool.replays == eng.total_speculative_rounds
+
+
+def test_unrolled_draft_steps_when_sampling(model, draft, tok):
+    from memforge_amd.runtime.sampling import SamplingParams
+
+    params = SamplingParams(max_new_tokens=12, temperature=0.8, top_p=1.0, stop_on_eos=False)
+    eng, got, _ = _spec_run(model, tok, DRAFT_PROMPTS, params=params, draft_model=draft, lookahead_k=3,
+                            draft_cuda_graph="batched-unrolled")
+    assert all(len(g) == 12 for g in got) and not eng._draft_pool._ugraph
+
+
+def test_draft_graph_auto_and_deprecated_true(model, draft, tok):
+    from memforge_amd.runtime.batched_speculative import BatchedGraphedDraftPool
+
+    _, plain, _ = _spec_run(model, tok, DRAFT_PROMPTS[:2], slots=2)
+    eng, got, _ = _spec_run(model, tok, DRAFT_PROMPTS[:2], slots=2, draft_model=draft, lookahead_k=3,
+                            paged_cuda_graph="auto", draft_cuda_graph="auto")
+    assert eng._paged_graph is not None and isinstance(eng._draft_pool, BatchedGraphedDraftPool)
+    assert got == plain
+    with pytest.warns(DeprecationWarning, match="batched"):
+        eng = make_engine(model, tok, max_num_seqs=2, draft_model=draft, lookahead_k=2, draft_cuda_graph=True)
+    assert isinstance(eng._draft_pool, BatchedGraphedDraftPool)
+    assert make_engine(model, tok, draft_model=draft, lookahead_k=2)._draft_pool is None
+
+
+def test_batched_draft_survives_preemption(model, draft, tok):
+    """A preempted sequence gives its draft slot back and re-feeds its draft
+    when it runs again; the output still equals plain decoding."""
+    prompts = ["first prompt that runs long", "second prompt, also long", "third"]
+    plain = make_engine(model, tok, num_blocks=256, max_model_len=128).generate(
+        prompts, greedy(24, stop_on_eos=False))
+    eng = make_engine(model, tok, block_size=4, num_blocks=22, max_num_seqs=3, max_model_len=128,
+                      draft_model=draft, lookahead_k=3, draft_cuda_graph="batched")
+    res = eng.generate(prompts, greedy(24, stop_on_eos=False))
+    assert [r["token_ids"] for r in res] == [p["token_ids"] for p in plain]
+    assert eng.total_preemptions > 0
+    assert len(eng._draft_pool._free) == 3
+
+
+def test_draft_pool_api(draft, device):
+    """acquire / release / prefill / rollback_to on the pool directly, and
+    proposals from two rows at different positions against the eager draft."""
+    from memforge_amd.runtime.batched_speculative import (BatchedGraphedDraftPool, DraftState,
+                                                           propose_draft_tokens)
+
+    pool = BatchedGraphedDraftPool(draft, max_len=64, num_slots=3, device="cuda:0")
+    a, b = pool.acquire(), pool.acquire()
+    assert (a.slot, b.slot) == (0, 1)
+    ta = [5, 9, 14, 22, 31, 40, 41]
+    tb = [7, 8]
+    pool.prefill(a, ta[:3])
+    assert a.position == 3
+    out = pool.propose([a, b], [ta, tb], 3, 0.0)
+    assert a.position == len(ta) + 3 and b.position == len(tb) + 3
+    for (cand, probs), toks in zip(out, [ta, tb]):
+        ref_cand, ref_probs = propose_draft_tokens(draft, DraftState(), toks, 3, 0.0, "cuda:0")
+        assert cand == ref_cand
+        assert len(probs) == 3 and all(int(p.argmax()) == c for p, c in zip(probs, cand))
+    a.rollback_to(len(ta) + 1)
+    with pytest.raises(ValueError):
+        a.rollback_to(a.position + 1)
+    with pytest.raises(ValueError):
+        a.rollback_to(-1)
+    # after a rollback the next round continues from the confirmed tokens
+    ta2 = ta + [out[0][0][0], 17]
+    out2 = pool.propose([a], [ta2], 2, 0.0)
+    ref_cand, _ = propose_draft_tokens(draft, DraftState(), ta2, 2, 0.0, "cuda:0")
+    assert out2[0][0] == ref_cand
+    pool.release(a)
+    pool.release(b)
+    with pytest.raises(ValueError):
+        pool.release(b)
+    assert sorted(pool._free) == [0, 1, 2]
+    with pytest.raises(ValueError):
+        pool.propose([pool.acquire()], [list(range(2, 64))], 4, 0.0)
+
+
+def test_graphed_decode_with_a_batch_limit_that_is_not_a_power_of_two(model, tok):
+    """Buckets are powers of two capped at max_num_seqs, so three running
+    sequences with max_num_seqs=3 replay a 3-row graph."""
+    eng = make_engine(model, tok, num_blocks=128, max_num_seqs=3, paged_cuda_graph=True)
+    res = eng.generate(PROMPTS[:3], greedy(10, stop_on_eos=False))
+    for r, exp in zip(res, expected(model, tok, PROMPTS[:3], 10, stop_on_eos=False)):
+        assert r["token_ids"] == exp
+    assert 3 in eng._paged_graph._buckets and eng.telemetry()["graph_replays"] > 0
