@@ -65,7 +65,7 @@ def parse_args():
     ap.add_argument("--e2e-eager", action="store_true",
                     help="run decode steps eagerly instead of replaying the captured decode graph")
     ap.add_argument("--no-mixed", action="store_true", help="skip the C2 mixed-step and C3 verify measurements")
-    ap.add_argument("--only", choices=["c2", "c3", "kv-write"],
+    ap.add_argument("--only", choices=["c2", "c3", "kv-write", "draft"],
                     help="run only one section (C2 mixed step, C3 verify, large KV write) and print its JSON")
     return ap.parse_args()
 
@@ -505,6 +505,76 @@ def run_e2e(args, dev):
     }
 
 
+# --------------------------------------------------- draft proposals (C3 shape)
+
+DRAFT_MODEL = dict(vocab_size=49152, hidden_size=576, intermediate_size=1536, num_hidden_layers=30,
+                   num_attention_heads=9, num_key_value_heads=3, head_dim=64)
+
+
+def run_draft(dev, rounds=8, warm=2, batch=16, k=4):
+    """One speculative round's draft proposals for the C3 batch (16 sequences,
+    contexts U[128, 2048], lookahead 4, greedy) with a SmolLM2-135M-shaped
+    draft, bf16, random init. Three forms: the eager per-sequence draft
+    (DynamicCache, one forward per token, a host read per candidate), the
+    batched graphed pool (K+1 replays for the whole batch, argmax fed back on
+    the device) and its unrolled form (one replay per round). Each timed round
+    is the engine's steady state: one new confirmed token per sequence."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from memforge_amd.runtime.batched_speculative import (BatchedGraphedDraftPool, DraftState,
+                                                           propose_draft_tokens)
+
+    cfg = LlamaConfig(**DRAFT_MODEL, max_position_embeddings=4096, tie_word_embeddings=True,
+                      bos_token_id=1, eos_token_id=2, pad_token_id=0)
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = LlamaForCausalLM(cfg)
+    model = model.to(torch.bfloat16).eval()
+    gen = torch.Generator().manual_seed(3)
+    lens = torch.randint(128, 2049, (batch,), generator=gen).tolist()
+    base = [torch.randint(2, DRAFT_MODEL["vocab_size"], (n,), generator=gen).tolist() for n in lens]
+    max_len = max(lens) + (warm + rounds) * 1 + k + 8
+
+    def drive(propose, states):
+        toks = [list(t) for t in base]
+        times, cands = [], []
+        for r in range(warm + rounds):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = propose(states, toks)
+            torch.cuda.synchronize()
+            if r >= warm:
+                times.append(time.perf_counter() - t0)
+            cands.append([c for c, _ in out])
+            for st, t, (c, _) in zip(states, toks, out):
+                st.rollback_to(len(t))
+                t.append(c[0])
+        return float(np.mean(times)) * 1e3, cands
+
+    res = {"workload": f"C3 draft side: {batch} sequences, ctx U[128,2048], lookahead {k}, greedy, "
+                       "SmolLM2-135M-shaped draft (30 layers, 9q/3kv, D 64, vocab 49152) bf16 random init; "
+                       "one new confirmed token per sequence per round"}
+    eager_states = [DraftState() for _ in range(batch)]
+    ms, eager_c = drive(lambda sts, toks: [propose_draft_tokens(model, st, t, k, 0.0, dev)
+                                            for st, t in zip(sts, toks)], eager_states)
+    res["eager_ms_per_round"] = round(ms, 3)
+    del eager_states
+    torch.cuda.empty_cache()
+    for name, unroll in (("batched", False), ("unrolled", True)):
+        pool = BatchedGraphedDraftPool(model, max_len=max_len, num_slots=batch, device=str(dev), unroll=unroll)
+        states = [pool.acquire() for _ in range(batch)]
+        ms, c = drive(lambda sts, toks: pool.propose(sts, toks, k, 0.0), states)
+        res[f"{name}_ms_per_round"] = round(ms, 3)
+        res[f"{name}_replays_per_round"] = pool.replays / (warm + rounds)
+        res[f"{name}_same_candidates_as_eager"] = sum(a == b for x, y in zip(c, eager_c) for a, b in zip(x, y))
+        del pool, states
+        torch.cuda.empty_cache()
+    res["candidate_lists"] = batch * (warm + rounds)
+    res["speedup_batched"] = round(res["eager_ms_per_round"] / res["batched_ms_per_round"], 2)
+    res["speedup_unrolled"] = round(res["eager_ms_per_round"] / res["unrolled_ms_per_round"], 2)
+    return res
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -530,7 +600,7 @@ def main():
         print(json.dumps({"e2e": run_e2e(args, dev)}))
         return
     if args.only:
-        section = {"c2": run_c2, "c3": run_c3, "kv-write": run_kv_write_large}[args.only]
+        section = {"c2": run_c2, "c3": run_c3, "kv-write": run_kv_write_large, "draft": run_draft}[args.only]
         print(json.dumps({args.only: section(dev)}))
         return
     ctx, tables, kpool, vpool, q = make_workload(args.sigma, dev)
@@ -664,6 +734,8 @@ def main():
         result["c2"] = run_c2(dev)
         result["c2"]["kv_write_c4_prefill"] = run_kv_write_large(dev)
         result["c3"] = run_c3(dev)
+        torch.cuda.empty_cache()
+        result["c3"]["draft"] = run_draft(dev)
         torch.cuda.empty_cache()
     if not args.no_e2e:
         kpool = vpool = partials = None
