@@ -65,7 +65,7 @@ def parse_args():
     ap.add_argument("--e2e-eager", action="store_true",
                     help="run decode steps eagerly instead of replaying the captured decode graph")
     ap.add_argument("--no-mixed", action="store_true", help="skip the C2 mixed-step and C3 verify measurements")
-    ap.add_argument("--only", choices=["c2", "c3", "kv-write", "draft"],
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "kv-write", "draft"],
                     help="run only one section (C2 mixed step, C3 verify, large KV write) and print its JSON")
     return ap.parse_args()
 
@@ -162,6 +162,96 @@ def _tables_for(kv_lens, gen):
 
 def _event_us(pairs):
     return float(np.mean([a.elapsed_time(b) for a, b in pairs])) * 1e3
+
+
+def run_c1(dev, reps=50):
+    """Config 1: one decode step at the SmolLM2 attention shape in fp32 -- 8
+    sequences, contexts U[17, 512], a 1024 x 16 pool with random block
+    placement, 15q/5kv heads, D 64, scale 1/8. Timed two ways: the standalone
+    operator (PagedKVCache + PagedAttention, one call per sequence, KV heads
+    repeated to 15 as that API needs) and one varlen launch for the batch
+    (GQA in the kernel). The error is against a torch fp32 gather + softmax
+    on the GPU."""
+    from memforge_amd import _native as nat
+    from memforge_amd.models.paged_attention import PagedAttention, PagedKVCache
+
+    gen = torch.Generator().manual_seed(0)
+    ctx = torch.randint(17, 513, (8,), generator=gen).tolist()
+    nblk = [(c + BS - 1) // BS for c in ctx]
+    perm = torch.randperm(1024, generator=gen).tolist()
+    tables, k = [], 0
+    for nb in nblk:
+        tables.append(perm[k:k + nb])
+        k += nb
+    gdev = torch.Generator(device=dev).manual_seed(1)
+    kp = torch.randn((1024, BS, SM_HKV, SM_D), generator=gdev, device=dev)
+    vp = torch.randn_like(kp)
+    q = torch.randn((8, SM_HQ, SM_D), generator=gdev, device=dev)
+    scale = 1.0 / math.sqrt(SM_D)
+    G = SM_HQ // SM_HKV
+
+    # torch fp32 reference: gather each context, repeat KV heads, softmax
+    ref = torch.empty_like(q)
+    for i, (c, t) in enumerate(zip(ctx, tables)):
+        idx = torch.tensor([t[p // BS] * BS + p % BS for p in range(c)], device=dev)
+        kk = kp.view(-1, SM_HKV, SM_D)[idx].repeat_interleave(G, dim=1).transpose(0, 1)  # (Hq, c, D)
+        vv = vp.view(-1, SM_HKV, SM_D)[idx].repeat_interleave(G, dim=1).transpose(0, 1)
+        w = torch.softmax(torch.matmul(q[i][:, None, :], kk.transpose(1, 2).contiguous()) * scale, dim=-1)
+        ref[i] = torch.matmul(w, vv)[:, 0]
+
+    # one varlen launch
+    out = torch.empty_like(q)
+    view = nat.PoolView.from_bshd(kp, vp)
+    bt = torch.zeros((8, max(nblk)), dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    bt = bt.to(dev)
+    cu_t = torch.arange(9, dtype=torch.int32, device=dev)
+    kv_t = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    pos_t = torch.tensor([c - 1 for c in ctx], dtype=torch.int64, device=dev)
+    plan = nat.plan_attention(list(range(9)), ctx, SM_HQ, SM_HKV, SM_D, torch.float32, dev)
+    partials = torch.empty(max(plan.partials_floats, 1), dtype=torch.float32, device=dev)
+
+    def varlen():
+        nat.paged_attention(q, out, view, bt, cu_t, kv_t, pos_t, plan, scale, SM_HKV, partials=partials)
+
+    # the standalone operator over a (blocks, heads, slots, dim) cache with
+    # the KV heads repeated
+    cache = PagedKVCache(1024, BS, SM_HQ, SM_D, dtype=torch.float32, device=str(dev))
+    cache.key_cache.copy_(kp.repeat_interleave(G, dim=2).permute(0, 2, 1, 3))
+    cache.value_cache.copy_(vp.repeat_interleave(G, dim=2).permute(0, 2, 1, 3))
+    op = PagedAttention(scale)
+    qs = [q[i].view(1, SM_HQ, 1, SM_D) for i in range(8)]
+
+    def operator():
+        return [op(qs[i], cache, tables[i], ctx[i]) for i in range(8)]
+
+    varlen()
+    op_out = torch.stack([o.view(SM_HQ, SM_D) for o in operator()])
+    torch.cuda.synchronize()
+    err_varlen = float((out - ref).abs().max())
+    err_op = float((op_out - ref).abs().max())
+    times = {}
+    for name, fn in (("varlen", varlen), ("operator", operator)):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in ev:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        times[name] = _event_us(ev)
+    kv_bytes = sum(ctx) * SM_HKV * SM_D * 4 * 2
+    return {
+        "workload": "C1: SmolLM2 decode, fp32, 8 sequences, ctx U[17,512], 15q/5kv, D 64, pool 1024x16 "
+                    "random placement, scale 1/8",
+        "varlen_launch_us": round(times["varlen"], 2),
+        "operator_8_calls_us": round(times["operator"], 2),
+        "max_abs_err_varlen": err_varlen,
+        "max_abs_err_operator": err_op,
+        "tolerance": 1e-5,
+        "kv_bytes": kv_bytes,
+        "context_tokens": sum(ctx),
+    }
 
 
 def run_c2(dev, layers=SM_LAYERS, reps=3):
@@ -600,7 +690,7 @@ def main():
         print(json.dumps({"e2e": run_e2e(args, dev)}))
         return
     if args.only:
-        section = {"c2": run_c2, "c3": run_c3, "kv-write": run_kv_write_large, "draft": run_draft}[args.only]
+        section = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "kv-write": run_kv_write_large, "draft": run_draft}[args.only]
         print(json.dumps({args.only: section(dev)}))
         return
     ctx, tables, kpool, vpool, q = make_workload(args.sigma, dev)
@@ -731,6 +821,7 @@ def main():
     if not args.no_mixed:
         del kpool, vpool, partials
         torch.cuda.empty_cache()
+        result["c1"] = run_c1(dev)
         result["c2"] = run_c2(dev)
         result["c2"]["kv_write_c4_prefill"] = run_kv_write_large(dev)
         result["c3"] = run_c3(dev)

@@ -13,7 +13,7 @@ from __future__ import annotations
 import ctypes
 from dataclasses import dataclass
 from pathlib import Path
-from typing import Optional, Sequence, Tuple
+from typing import List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -227,6 +227,55 @@ def kv_copy_blocks(key_pool: torch.Tensor, value_pool: torch.Tensor,
     ), "mf_kv_copy_blocks")
 
 
+# ------------------------------------------------------------------ uploads
+
+def _layout(parts: Sequence[np.ndarray]) -> Tuple[List[np.ndarray], List[int], int]:
+    """Contiguous copies of the parts, each part's int32-word offset (even, so
+    int64 parts land on 8-byte boundaries) and the total word count."""
+    arrs, offs, n = [], [], 0
+    for p in parts:
+        a = np.ascontiguousarray(p)
+        if a.dtype not in (np.int32, np.int64):
+            raise TypeError(f"upload takes int32/int64 arrays, got {a.dtype}")
+        n = (n + 1) & ~1
+        offs.append(n)
+        n += a.size * a.itemsize // 4
+        arrs.append(a)
+    return arrs, offs, max(n, 2)
+
+
+def _views(buf: torch.Tensor, arrs: Sequence[np.ndarray], offs: Sequence[int]) -> List[torch.Tensor]:
+    out = []
+    for a, o in zip(arrs, offs):
+        t = buf[o:o + a.size * a.itemsize // 4]
+        if a.dtype == np.int64:
+            t = t.view(torch.int64)
+        out.append(t.view(a.shape))
+    return out
+
+
+def upload(parts: Sequence[np.ndarray], device) -> List[torch.Tensor]:
+    """Move int32 / int64 host arrays to ``device`` with ONE host-to-device
+    copy: they are packed into a pinned buffer (each part on an 8-byte
+    boundary), copied asynchronously into a fresh device buffer on the current
+    stream, and handed back as views with their own dtype and shape. The
+    pinned buffer comes from torch's caching host allocator, which does not
+    hand it out again before the copy has completed, so the host never waits
+    for the GPU here."""
+    arrs, offs, n = _layout(parts)
+    dev = torch.device(device)
+    pinned = dev.type == "cuda"
+    host = torch.empty(n, dtype=torch.int32, pin_memory=pinned)
+    h = host.numpy()
+    for a, o in zip(arrs, offs):
+        h[o:o + a.size * a.itemsize // 4] = a.reshape(-1).view(np.int32)
+    if not pinned:
+        return _views(host.to(dev), arrs, offs)
+    buf = torch.empty(n, dtype=torch.int32, device=dev)
+    buf.copy_(host, non_blocking=True)
+    return _views(buf, arrs, offs)
+
+
 # ---------------------------------------------------------------- attention
 
 @dataclass
@@ -269,17 +318,25 @@ def plan_attention_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q
     return items[:n_items], merges[:n_merges], counts
 
 
+def plan_upload_parts(items: np.ndarray, merges: np.ndarray) -> List[np.ndarray]:
+    """The two arrays a plan puts on the device (at least one row each)."""
+    return [items if items.shape[0] else np.zeros((1, PLAN_ITEM_INTS), np.int32),
+            merges if merges.shape[0] else np.zeros((1, PLAN_MERGE_INTS), np.int32)]
+
+
+def plan_from_parts(items: np.ndarray, merges: np.ndarray, counts: np.ndarray,
+                    dev_items: torch.Tensor, dev_merges: torch.Tensor) -> AttentionPlan:
+    return AttentionPlan(dev_items, dev_merges, int(counts[0]), int(counts[1]), int(counts[2]),
+                         int(counts[3]), items, merges)
+
+
 def plan_attention(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int,
                    num_kv_heads: int, head_dim: int, dtype: torch.dtype, device,
                    partition_tiles: int = 0) -> AttentionPlan:
     items, merges, counts = plan_attention_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim,
                                                 dtype, partition_tiles)
-    dev_items = torch.from_numpy(np.ascontiguousarray(items if items.shape[0] else
-                                                      np.zeros((1, PLAN_ITEM_INTS), np.int32))).to(device)
-    dev_merges = torch.from_numpy(np.ascontiguousarray(merges if merges.shape[0] else
-                                                       np.zeros((1, PLAN_MERGE_INTS), np.int32))).to(device)
-    return AttentionPlan(dev_items, dev_merges, int(counts[0]), int(counts[1]), int(counts[2]),
-                         int(counts[3]), items, merges)
+    dev_items, dev_merges = upload(plan_upload_parts(items, merges), device)
+    return plan_from_parts(items, merges, counts, dev_items, dev_merges)
 
 
 class CountedPlan:

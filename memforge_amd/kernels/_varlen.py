@@ -20,13 +20,18 @@ def as_table_list(table) -> List[int]:
     return [int(x) for x in table]
 
 
-def padded_tables(tables: Sequence[Sequence[int]], device) -> torch.Tensor:
+def padded_tables_host(tables: Sequence[Sequence[int]]) -> np.ndarray:
+    """Block tables as one zero-padded int32 (B, max_blocks) array."""
     width = max(1, max((len(t) for t in tables), default=1))
     out = np.zeros((max(1, len(tables)), width), dtype=np.int32)
     for i, t in enumerate(tables):
         if len(t):
             out[i, : len(t)] = np.asarray(t, dtype=np.int64).astype(np.int32)
-    return torch.from_numpy(out).to(device)
+    return out
+
+
+def padded_tables(tables: Sequence[Sequence[int]], device) -> torch.Tensor:
+    return nat.upload([padded_tables_host(tables)], device)[0]
 
 
 def run_varlen(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: nat.PoolView,
@@ -60,16 +65,23 @@ def run_varlen(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: nat.PoolView,
         cu.append(len(row_map))
         kvl.append(kv_lens[s] if kv_lens is not None else max(positions[r] for r in rows) + 1)
     identity = row_map == list(range(T))
-    bt = padded_tables([tables[s] for s in order], dev)
-    plan = nat.plan_attention(cu, kvl, hq, num_kv_heads, d, q_rows.dtype, dev)
-    meta = torch.tensor(cu + kvl, dtype=torch.int32).to(dev)
-    pl = None
+    items, merges, counts = nat.plan_attention_host(cu, kvl, hq, num_kv_heads, d, q_rows.dtype)
+    # tables, plan, cu/kv lengths, positions, row map and pool lengths cross
+    # to the device in one copy
+    parts = [padded_tables_host([tables[s] for s in order]), *nat.plan_upload_parts(items, merges),
+             np.asarray(cu + kvl, dtype=np.int32), np.asarray(list(positions), dtype=np.int64)]
+    if not identity:
+        parts.append(np.asarray(row_map, dtype=np.int32))
     if pool_lens is not None:
-        pl = torch.tensor([pool_lens[s] for s in order], dtype=torch.int32).to(dev)
+        parts.append(np.asarray([pool_lens[s] for s in order], dtype=np.int32))
+    dev_parts = nat.upload(parts, dev)
+    bt, d_items, d_merges, meta, pos = dev_parts[:5]
+    rest = dev_parts[5:]
+    rmap = None if identity else rest.pop(0)
+    pl = rest.pop(0) if pool_lens is not None else None
+    plan = nat.plan_from_parts(items, merges, counts, d_items, d_merges)
     nat.paged_attention(
-        q_rows, out_rows, pool, bt, meta[: len(cu)], meta[len(cu):],
-        torch.tensor(list(positions), dtype=torch.int64).to(dev), plan,
+        q_rows, out_rows, pool, bt, meta[: len(cu)], meta[len(cu):], pos, plan,
         scale if scale is not None else 1.0 / math.sqrt(d), num_kv_heads,
-        row_map=None if identity else torch.tensor(row_map, dtype=torch.int32).to(dev),
-        pool_lens=pl, new_k_rows=new_k_rows, new_v_rows=new_v_rows,
+        row_map=rmap, pool_lens=pl, new_k_rows=new_k_rows, new_v_rows=new_v_rows,
     )

@@ -28,10 +28,11 @@ import threading
 from contextlib import contextmanager
 from typing import Any, List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from memforge_amd import _native as nat
-from memforge_amd.kernels._varlen import as_table_list, padded_tables, run_varlen
+from memforge_amd.kernels._varlen import as_table_list, padded_tables_host, run_varlen
 from memforge_amd.kernels.block_attention import paged_attention_blockwise
 
 BACKEND_NAME = "memforge_paged"
@@ -68,7 +69,9 @@ class _VarlenBinding:
     row order, cu_seqlens, kv_lens, positions, padded block tables and the
     attention work plan -- is built once and shared by every layer.
     ``pool_lens`` turns the pass into a verify pass: keys at or above
-    pool_lens[s] are the layer's in-flight key/value rows, not pool slots.
+    pool_lens[s] are the layer's in-flight key/value rows, not pool slots. A
+    host sequence is uploaded with the rest of the metadata; a device tensor
+    must already be in the grouped sequence order.
     """
 
     __slots__ = ("pool", "block_tables", "seq_ids", "positions", "block_wise", "used", "_meta",
@@ -123,16 +126,27 @@ class _VarlenBinding:
                     f"sequence {s} reads up to position {kvl[-1] - 1}, needing {needed} blocks, "
                     f"but its block table has {len(tables[s])} entries"
                 )
-        plan = nat.plan_attention(cu, kvl, num_q_heads, self.pool.spec.num_kv_heads, head_dim, dtype, device)
-        ints = torch.tensor(cu + kvl, dtype=torch.int32).to(device)
+        items, merges, counts = nat.plan_attention_host(cu, kvl, num_q_heads, self.pool.spec.num_kv_heads,
+                                                        head_dim, dtype)
         identity = row_map == list(range(len(row_map)))
+        # everything the launch reads crosses to the device in one copy
+        parts = [padded_tables_host([tables[s] for s in order]), *nat.plan_upload_parts(items, merges),
+                 np.asarray(cu + kvl, dtype=np.int32), np.asarray(list(self.positions), dtype=np.int64)]
+        if not identity:
+            parts.append(np.asarray(row_map, dtype=np.int32))
+        host_pool_lens = self.pool_lens is not None and not isinstance(self.pool_lens, torch.Tensor)
+        if host_pool_lens:
+            parts.append(np.asarray([int(self.pool_lens[s]) for s in order], dtype=np.int32))
+        dev = nat.upload(parts, device)
+        if host_pool_lens:
+            self.pool_lens = dev[-1]
         self._meta = {
-            "block_tables": padded_tables([tables[s] for s in order], device),
-            "cu_seqlens": ints[: len(cu)],
-            "kv_lens": ints[len(cu):],
-            "positions": torch.tensor(self.positions, dtype=torch.int64).to(device),
-            "row_map": None if identity else torch.tensor(row_map, dtype=torch.int32).to(device),
-            "plan": plan,
+            "block_tables": dev[0],
+            "cu_seqlens": dev[3][: len(cu)],
+            "kv_lens": dev[3][len(cu):],
+            "positions": dev[4],
+            "row_map": None if identity else dev[5],
+            "plan": nat.plan_from_parts(items, merges, counts, dev[1], dev[2]),
         }
         return self._meta
 

@@ -16,6 +16,7 @@ from __future__ import annotations
 import math
 from typing import List, Optional, Tuple
 
+import numpy as np
 import torch
 import torch.nn as nn
 
@@ -52,9 +53,10 @@ class PagedKVCache:
         return nat.PoolView.from_bhsd(self.key_cache, self.value_cache)
 
     def _slots(self, block_table: List[int], start: int, count: int) -> torch.Tensor:
-        pos = torch.arange(start, start + count)
-        table = torch.as_tensor(list(block_table), dtype=torch.long)
-        return (table[pos // self.block_size] * self.block_size + pos % self.block_size).to(self.device)
+        pos = np.arange(start, start + count, dtype=np.int64)
+        table = np.asarray(list(block_table), dtype=np.int64)
+        slots = table[pos // self.block_size] * self.block_size + pos % self.block_size
+        return nat.upload([slots], self.device)[0]
 
     def write_kv(self, key_states: torch.Tensor, value_states: torch.Tensor,
                  block_table: List[int], start_pos: int) -> None:

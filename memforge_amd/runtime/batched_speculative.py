@@ -29,6 +29,7 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 from transformers.cache_utils import DynamicCache
 
@@ -36,7 +37,7 @@ from memforge_amd import _native as nat
 from memforge_amd.kernels import attention_backend
 from memforge_amd.runtime.graphed_paged_decode import GraphedPagedDecoder, _Bucket
 from memforge_amd.runtime.kv_pool import ModelKVSpec, PagedKVPool
-from memforge_amd.runtime.packed_pass import Staging, packed_forward
+from memforge_amd.runtime.packed_pass import packed_forward
 from memforge_amd.runtime.varlen_cache import VarlenPackedCache
 from memforge_amd.speculative.rejection_sampler import RejectionSampler
 
@@ -186,7 +187,6 @@ class BatchedGraphedDraftPool:
         self._tables = [list(range(i * nb, (i + 1) * nb)) for i in range(self.num_slots)]
         self._decoder = GraphedPagedDecoder(model, self.kv, max_batch=self.num_slots,
                                             max_model_len=self.max_len)
-        self._staging = Staging(device)
         self._free = list(range(self.num_slots))
         self._ugraph: Dict[Tuple[int, int], torch.cuda.CUDAGraph] = {}
         self._uout: Dict[Tuple[int, int], torch.Tensor] = {}
@@ -224,7 +224,7 @@ class BatchedGraphedDraftPool:
         for st, toks in runs:
             if st.position + len(toks) > self.max_len:
                 raise ValueError(f"draft context {st.position + len(toks)} exceeds {self.max_len}")
-        packed_forward(self.model, self.kv, self._staging, [toks for _, toks in runs],
+        packed_forward(self.model, self.kv, [toks for _, toks in runs],
                        [st.position for st, _ in runs], [self._tables[st.slot] for st, _ in runs],
                        keep_rows=[0])
         for st, toks in runs:
@@ -366,11 +366,11 @@ def verify_candidates_batched(target_model, pool, buffers, block_tables: Sequenc
     total = len(seq_ids)
     num_layers = pool.spec.num_layers
     cache = VarlenPackedCache.verify(pool, num_layers, total)
-    binding = attention_backend._VarlenBinding(
-        pool, block_tables, seq_ids, positions,
-        pool_lens=torch.tensor([int(c) for c in context_lengths], dtype=torch.int32).to(device))
-    input_ids = torch.tensor([[t for q in query_tokens for t in q]], dtype=torch.long, device=device)
-    position_ids = torch.tensor([positions], dtype=torch.long, device=device)
+    binding = attention_backend._VarlenBinding(pool, block_tables, seq_ids, positions,
+                                               pool_lens=[int(c) for c in context_lengths])
+    input_ids, position_ids = nat.upload(
+        [np.asarray([[t for q in query_tokens for t in q]], dtype=np.int64),
+         np.asarray([positions], dtype=np.int64)], device)
     with attention_backend.backend_enabled_on(target_model) as routed:
         if not routed:
             raise RuntimeError("verification needs the attention registry, which is unavailable")

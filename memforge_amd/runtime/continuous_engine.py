@@ -54,7 +54,7 @@ from memforge_amd.runtime.batched_speculative import (
 )
 from memforge_amd.runtime.graphed_paged_decode import GraphedPagedDecoder
 from memforge_amd.runtime.kv_pool import ModelKVSpec, PagedKVPool
-from memforge_amd.runtime.packed_pass import Staging, packed_forward
+from memforge_amd.runtime.packed_pass import packed_forward
 from memforge_amd.runtime.prefix_sharing import block_owners, copy_block, sharing_telemetry
 from memforge_amd.runtime.sampling import SamplingParams, sample_logits
 
@@ -201,7 +201,6 @@ class ContinuousBatchingEngine:
                                               self.max_prefill_tokens_per_step, lookahead_slots)
         if not attention_backend.register():
             raise RuntimeError("the transformers attention registry is required")
-        self._staging = Staging(self.device)
         # Pure-decode steps replay a captured HIP graph of the packed pass
         # (False | True | "auto", as the reference's paged_cuda_graph; "auto"
         # is on whenever the model's head grouping allows it).
@@ -486,7 +485,7 @@ class ContinuousBatchingEngine:
         # only rows that produce a token go through the LM head
         emit = [i for i, e in enumerate(plan) if e["kind"] == "decode" or e["is_final"]]
         try:
-            res = packed_forward(self.model, self.pool, self._staging, [e["tokens"] for e in plan],
+            res = packed_forward(self.model, self.pool, [e["tokens"] for e in plan],
                                  [e["start"] for e in plan], [e["table"] for e in plan],
                                  [int(cu[i + 1]) - 1 for i in emit])
         except IndexError as exc:

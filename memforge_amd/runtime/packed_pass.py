@@ -2,8 +2,8 @@
 
 Every contributing sequence adds a run of query tokens at consecutive
 positions ``start .. start + len - 1`` whose K/V are written through its block
-table. The descriptors, tables and token ids are staged in pinned memory and
-cross PCIe in one copy; the ragged-pack kernel builds token ids, positions,
+table. The descriptors, tables, token ids and attention plan are staged in
+pinned memory and cross PCIe in one copy; the ragged-pack kernel builds token ids, positions,
 slot_mapping, cu_seqlens and padded tables on the device; each layer's cache
 update is the KV-write kernel and its attention the varlen kernel reading the
 pool in place. This is the reference's fused varlen step
@@ -24,32 +24,6 @@ from memforge_amd.kernels import attention_backend
 from memforge_amd.runtime.varlen_cache import VarlenPackedCache
 
 
-class Staging:
-    """Grow-only pinned host buffer and its device twin for the per-pass
-    descriptors, so a pass's metadata crosses PCIe in one copy."""
-
-    def __init__(self, device):
-        self.device = device
-        self.host = torch.empty(0, dtype=torch.int32).pin_memory()
-        self.dev = torch.empty(0, dtype=torch.int32, device=device)
-        self.copied = None  # event recorded after the last copy out of ``host``
-
-    def upload(self, arr: np.ndarray) -> torch.Tensor:
-        n = arr.size
-        if self.copied is not None:
-            # the previous copy must have left the pinned buffer before it is rewritten
-            self.copied.synchronize()
-        if self.host.numel() < n:
-            cap = max(n, 2 * self.host.numel(), 1 << 16)
-            self.host = torch.empty(cap, dtype=torch.int32).pin_memory()
-            self.dev = torch.empty(cap, dtype=torch.int32, device=self.device)
-        self.host[:n].numpy()[:] = arr
-        self.dev[:n].copy_(self.host[:n], non_blocking=True)
-        self.copied = torch.cuda.Event()
-        self.copied.record()
-        return self.dev[:n]
-
-
 @dataclass
 class PackedPassResult:
     logits: torch.Tensor      # (len(keep_rows), vocab), rows in keep_rows order
@@ -60,9 +34,8 @@ class PackedPassResult:
 
 
 @torch.no_grad()
-def packed_forward(model, pool, staging: Staging, tokens: Sequence[Sequence[int]],
-                   starts: Sequence[int], tables: Sequence[Sequence[int]],
-                   keep_rows: Sequence[int]) -> PackedPassResult:
+def packed_forward(model, pool, tokens: Sequence[Sequence[int]], starts: Sequence[int],
+                   tables: Sequence[Sequence[int]], keep_rows: Sequence[int]) -> PackedPassResult:
     """Run ``model`` once over every sequence's ``tokens`` (written at
     ``starts[i]`` onward through ``tables[i]``) and return the logits of the
     packed rows ``keep_rows``. Raises IndexError when a run does not fit its
@@ -80,7 +53,6 @@ def packed_forward(model, pool, staging: Staging, tokens: Sequence[Sequence[int]
     cu = np.zeros(B + 1, dtype=np.int64)
     np.cumsum(q_lens, out=cu[1:])
 
-    # descriptors | tables | tokens in one int32 upload
     ent = np.empty((B, nat.ENTRY_INTS), dtype=np.int32)
     t_off = np.zeros(B, dtype=np.int64)
     t_off[1:] = np.cumsum([len(t) for t in tables])[:-1]
@@ -92,19 +64,20 @@ def packed_forward(model, pool, staging: Staging, tokens: Sequence[Sequence[int]
     ent[:, 5] = cu[:-1]
     flat_tables = np.fromiter((b for t in tables for b in t), dtype=np.int32)
     flat_tokens = np.fromiter((tok for run in tokens for tok in run), dtype=np.int32)
-    buf = np.concatenate([ent.reshape(-1), flat_tables, flat_tokens])
-    dev = staging.upload(buf)
-    ne, nt = ent.size, flat_tables.size
-    packed = nat.ragged_pack(dev[:ne].view(B, nat.ENTRY_INTS), dev[ne:ne + nt], dev[ne + nt:],
-                             T, bs, max_blocks)
-    attn_plan = nat.plan_attention(cu.tolist(), kv_lens, model.config.num_attention_heads,
-                                   spec.num_kv_heads, spec.head_dim, pool.key_pool.dtype, spec.device)
+    items, merges, counts = nat.plan_attention_host(cu.tolist(), kv_lens, model.config.num_attention_heads,
+                                                    spec.num_kv_heads, spec.head_dim, pool.key_pool.dtype)
+    keep_np = np.asarray(list(keep_rows), dtype=np.int64)
+    # descriptors, tables, tokens, the attention plan and the kept rows cross
+    # to the device in one copy
+    d_ent, d_tables, d_tokens, d_items, d_merges, keep = nat.upload(
+        [ent, flat_tables, flat_tokens, *nat.plan_upload_parts(items, merges), keep_np], spec.device)
+    packed = nat.ragged_pack(d_ent, d_tables, d_tokens, T, bs, max_blocks)
+    attn_plan = nat.plan_from_parts(items, merges, counts, d_items, d_merges)
     meta = {"block_tables": packed.block_tables, "cu_seqlens": packed.cu_seqlens,
             "kv_lens": packed.kv_lens, "positions": packed.positions, "row_map": None,
             "plan": attn_plan}
     binding = attention_backend._VarlenBinding.from_packed(pool, meta, T)
     cache = VarlenPackedCache.from_slot_mapping(pool, spec.num_layers, packed.slot_mapping)
-    keep = torch.tensor(list(keep_rows), dtype=torch.long).to(spec.device)
     with attention_backend.backend_enabled_on(model) as routed:
         if not routed:
             raise RuntimeError("the packed pass needs the attention registry")

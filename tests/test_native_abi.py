@@ -194,3 +194,23 @@ def test_block_copy_rejects_a_bad_geometry():
     assert L.mf_kv_copy_blocks(1 << 20, 1 << 20, 2, 3, 1024, 1024, 1024, 8, flat.ctypes.data, 1, None) == -1
     # unknown dtype
     assert L.mf_kv_copy_blocks(1 << 20, 1 << 20, 7, 3, 8 * 1024, 1024, 1024, 8, flat.ctypes.data, 1, None) == -1
+
+
+def test_upload_packs_parts_with_their_dtypes_and_shapes():
+    """nat.upload's packing (shared by the pinned GPU path): int64 parts land
+    on 8-byte boundaries and every part comes back intact."""
+    rng = np.random.default_rng(0)
+    parts = [rng.integers(-2**31, 2**31, 5, dtype=np.int64).astype(np.int32),
+             rng.integers(-2**62, 2**62, (3, 2), dtype=np.int64),
+             np.zeros((0, 12), np.int32),
+             rng.integers(0, 100, (2, 3), dtype=np.int64).astype(np.int32),
+             np.array([7], np.int64)]
+    out = nat.upload(parts, "cpu")
+    for p, t in zip(parts, out):
+        assert t.dtype == (torch.int64 if p.dtype == np.int64 else torch.int32)
+        assert tuple(t.shape) == p.shape
+        assert np.array_equal(t.numpy(), p)
+    _, offs, n = nat._layout(parts)
+    assert all(o % 2 == 0 for o in offs) and n >= offs[-1] + 2
+    with pytest.raises(TypeError):
+        nat.upload([np.zeros(3, np.float32)], "cpu")
