@@ -675,11 +675,12 @@ void attn_kernel(AttnArgs a) {
     // quarter per wave, 16 bytes per lane) and staged in LDS, and each wave
     // reads its MFMA fragments from LDS. That takes the four-fold re-reads of
     // each tile off the texture path, which is what limits the per-wave loop
-    // on prefill. Loads run one tile ahead in registers; LDS holds two tiles
-    // (written after the barrier that retires the previous reads of that
-    // buffer). Each K row's 16-byte chunks are stored xor-swizzled by key, so
-    // the fragment reads (16 keys x one chunk) hit distinct banks; V rows are
-    // read 16 lanes to a row, conflict-free. One barrier per tile.
+    // on prefill. Tiles move in stages of TPS: loads run one stage ahead in
+    // registers; LDS holds two stages (a stage is written after the barrier
+    // that retires the previous reads of its buffer). Each K row's 16-byte
+    // chunks are stored xor-swizzled by key, so the fragment reads (16 keys x
+    // one chunk) hit distinct banks; V rows are read 16 lanes to a row,
+    // conflict-free. One barrier per stage.
     bool wg_shared = false;
     if constexpr (FAST && DT != MF_F32 && NT > 1) {
         if ((int)(blockIdx.x + 1) * kWaves <= num_items) {
@@ -698,7 +699,14 @@ void attn_kernel(AttnArgs a) {
             constexpr int NCH = RB / 16;            // 16-byte chunks per row
             constexpr int STAGE = 32 * RB;          // K tile, then V tile
             constexpr int NI = (STAGE + kWaves * 1024 - 1) / (kWaves * 1024);  // 16-byte loads per lane per tile
-            __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+            // Tiles per LDS stage: each barrier and each refill covers TPS
+            // tiles, so a refill has TPS tiles of compute to arrive in.
+            // Measured on the C2 prefill items (bf16, D 64): 1 tile 42.0 us,
+            // 2 tiles 40.3 us, 4 tiles 39.2 us. Four would take the D 32
+            // kernel past 128 registers (three waves per SIMD), so other row
+            // sizes use two.
+            constexpr int TPS = RB == 128 ? 4 : 2;
+            __shared__ __attribute__((aligned(16))) char smem[2 * TPS * STAGE];
             __shared__ int s_end[kWaves];
             if (lane == 0) s_end[wave] = fast_end;
             __syncthreads();
@@ -709,7 +717,7 @@ void attn_kernel(AttnArgs a) {
             // piece (i*4 + wave) mod STAGE, and the matching pool offset inside
             // the block (vector types rather than arrays keep them in registers)
             typedef uint32_t offs_t __attribute__((ext_vector_type(NI)));
-            typedef uint32_t regs_t __attribute__((ext_vector_type(4 * NI)));
+            typedef uint32_t regs_t __attribute__((ext_vector_type(4 * NI * TPS)));
             offs_t src_off;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
@@ -721,28 +729,37 @@ void attn_kernel(AttnArgs a) {
                 src_off[i] = (uint32_t)key * v_row_bytes + (uint32_t)q * 16;
             }
             // Loads are unconditional (a wave without a piece of a small tile
-            // re-reads another wave's piece and does not store it): a
-            // conditional load would make every later wait drain all loads.
-            auto fetch = [&](int t, regs_t& r) __attribute__((always_inline)) {
-                const int phys = tbl_at(t - kt0);
-                const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
+            // re-reads another wave's piece and does not store it; tiles past
+            // the range re-read the last one): a conditional load would make
+            // every later wait drain all loads.
+            auto fetch = [&](int t0, regs_t& r) __attribute__((always_inline)) {
 #pragma unroll
-                for (int i = 0; i < NI; ++i) {
-                    const int base = ((i * kWaves + wave) * 1024) % STAGE;
-                    const uint4 v = *(const uint4*)((base >= 16 * RB ? a.v_pool : a.k_pool) + boff + src_off[i]);
-                    r[4 * i] = v.x;
-                    r[4 * i + 1] = v.y;
-                    r[4 * i + 2] = v.z;
-                    r[4 * i + 3] = v.w;
+                for (int u = 0; u < TPS; ++u) {
+                    const int phys = tbl_at(min(t0 + u, wg_end - 1) - kt0);
+                    const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
+#pragma unroll
+                    for (int i = 0; i < NI; ++i) {
+                        const int base = ((i * kWaves + wave) * 1024) % STAGE;
+                        const uint4 v = *(const uint4*)((base >= 16 * RB ? a.v_pool : a.k_pool) + boff + src_off[i]);
+                        const int w = 4 * (u * NI + i);
+                        r[w] = v.x;
+                        r[w + 1] = v.y;
+                        r[w + 2] = v.z;
+                        r[w + 3] = v.w;
+                    }
                 }
             };
             auto stash = [&](const regs_t& r, int buf) __attribute__((always_inline)) {
 #pragma unroll
-                for (int i = 0; i < NI; ++i) {
-                    const int base = (i * kWaves + wave) * 1024;
-                    if (base < STAGE)
-                        *(uint4*)(smem + buf * STAGE + base + lane * 16) =
-                            make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
+                for (int u = 0; u < TPS; ++u) {
+#pragma unroll
+                    for (int i = 0; i < NI; ++i) {
+                        const int base = (i * kWaves + wave) * 1024;
+                        const int w = 4 * (u * NI + i);
+                        if (base < STAGE)
+                            *(uint4*)(smem + (buf * TPS + u) * STAGE + base + lane * 16) =
+                                make_uint4(r[w], r[w + 1], r[w + 2], r[w + 3]);
+                    }
                 }
             };
             auto sync = [&]() {
@@ -752,31 +769,35 @@ void attn_kernel(AttnArgs a) {
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
             };
-            // One register set in flight: tile i+1 arrives during tile i's
-            // compute, is stored to the other LDS buffer, and the set is
-            // refilled with tile i+2 (the last ones re-read tile n-1).
+            // One register set in flight: stage u+1 (TPS tiles) arrives during
+            // stage u's compute, is stored to the other LDS buffer, and the set
+            // is refilled with stage u+2.
             if (n > 0) {
+                const int nst = (n + TPS - 1) / TPS;
                 regs_t rs;
                 fetch(kt0, rs);
                 stash(rs, 0);
-                fetch(min(kt0 + 1, wg_end - 1), rs);
+                fetch(kt0 + TPS, rs);
                 sync();
-                for (int i = 0; i < n; ++i) {
-                    const int t = kt0 + i;
-                    if (t < fast_end) {
-                        const char* stg = smem + (i & 1) * STAGE;
-                        uint4 kf[NL];
-                        uint32_t vf[4][VWD];
+                for (int u = 0; u < nst; ++u) {
 #pragma unroll
-                        for (int c = 0; c < NL; ++c)
-                            kf[c] = *(const uint4*)(stg + j * RB + (((c * 4 + g) ^ (j & (NCH - 1))) << 4));
+                    for (int v = 0; v < TPS; ++v) {
+                        const int t = kt0 + u * TPS + v;
+                        if (t < fast_end) {
+                            const char* stg = smem + ((u & 1) * TPS + v) * STAGE;
+                            uint4 kf[NL];
+                            uint32_t vf[4][VWD];
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) ld_words<VB>(stg + 16 * RB + (4 * g + r) * RB + j * VB, vf[r]);
-                        process(t, kf, vf);
+                            for (int c = 0; c < NL; ++c)
+                                kf[c] = *(const uint4*)(stg + j * RB + (((c * 4 + g) ^ (j & (NCH - 1))) << 4));
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) ld_words<VB>(stg + 16 * RB + (4 * g + r) * RB + j * VB, vf[r]);
+                            process(t, kf, vf);
+                        }
                     }
-                    if (i + 1 < n) {
-                        stash(rs, (i + 1) & 1);
-                        fetch(min(t + 2, wg_end - 1), rs);
+                    if (u + 1 < nst) {
+                        stash(rs, (u + 1) & 1);
+                        fetch(kt0 + (u + 2) * TPS, rs);
                     }
                     sync();
                 }
