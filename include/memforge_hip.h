@@ -199,7 +199,7 @@ int mf_paged_attention(const void* q, int64_t q_stride_row, int64_t q_stride_hea
  * at plan_items + capacity_narrow * MF_PLAN_ITEM_INTS), plan_merges holds
  * capacity_merges records, and device_counts (device, int32[3]) gives the
  * live numbers of narrow items, wide items and merges -- each at most its
- * capacity, the wide count a multiple of four as mf_attention_plan makes it;
+ * capacity, both item counts multiples of four as mf_attention_plan makes them;
  * workgroups past them exit at once. Split-K partitions are merged
  * by the separate merge kernel. Everything else is as in mf_paged_attention.
  */
@@ -225,7 +225,11 @@ int mf_paged_attention_counted(const void* q, int64_t q_stride_row, int64_t q_st
  * from the work: narrow and wide items separately) and writes
  * MF_PLAN_ITEM_INTS ints per work item to items (narrow items -- one
  * 16-column tile -- first, then wide ones) and MF_PLAN_MERGE_INTS ints per
- * split-K merge to merges. Wide items come in workgroups of four: a run of
+ * split-K merge to merges. Narrow items come in workgroups of four: four
+ * single-wave items (ranges of at most P tiles), or one cooperative unit
+ * (last int 1) whose four waves take consecutive quarters of a range of at
+ * most 4P tiles and combine their softmax states in LDS; only longer ranges
+ * are split into several units and merged. Wide items come in workgroups of four: a run of
  * four or more column groups over one (sequence, kv head, key range) fills
  * whole workgroups, which then share each K/V tile through LDS (the last one
  * padded with items that have no column tiles and no partial slot); shorter

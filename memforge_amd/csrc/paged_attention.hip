@@ -24,6 +24,7 @@
 #include <array>
 #include <climits>
 #include <cmath>
+#include <type_traits>
 #include <vector>
 
 #include "mf_common.h"
@@ -187,11 +188,9 @@ __device__ __forceinline__ void st_words(char* p, const uint32_t* w) {
     }
 }
 
-// Writes the lane's contiguous chunk of 4*VCH output elements (value e is
-// vals[e]) in dtype DT.
-template <int DT, int VCH>
-__device__ __forceinline__ void store_out_chunk(char* p, const float* vals) {
-    constexpr int NE = 4 * VCH;
+// Writes NE contiguous output elements (value e is vals[e]) in dtype DT.
+template <int DT, int NE>
+__device__ __forceinline__ void store_elems(char* p, const float* vals) {
     if constexpr (DT == MF_F32) {
         uint32_t w[NE];
 #pragma unroll
@@ -204,6 +203,12 @@ __device__ __forceinline__ void store_out_chunk(char* p, const float* vals) {
             w[e] = f32_to_bits<DT>(vals[2 * e]) | (f32_to_bits<DT>(vals[2 * e + 1]) << 16);
         st_words<NE * 2>(p, w);
     }
+}
+
+// Writes the lane's contiguous chunk of 4*VCH output elements.
+template <int DT, int VCH>
+__device__ __forceinline__ void store_out_chunk(char* p, const float* vals) {
+    store_elems<DT, 4 * VCH>(p, vals);
 }
 
 // ------------------------------------------------------------- split-K merge
@@ -309,6 +314,19 @@ constexpr int attn_waves_per_eu() {
     return (row_bytes <= 128 || (row_bytes <= 256 && NT == 1)) ? 2 : 1;
 }
 
+// Register buffers of the single-column-tile key pipeline: the tile being
+// processed plus the two in flight. Measured on MI355X for 128-byte rows
+// (bf16 D 64): four and six buffers were no faster than three, and eight
+// slower (they cost waves per SIMD); a 256-byte row's buffer is 32 registers,
+// and three fit the two-waves-per-SIMD budget.
+#ifndef MF_NARROW_DEPTH
+#define MF_NARROW_DEPTH 3
+#endif
+template <int DT, int DP>
+constexpr int narrow_depth() {
+    return MF_NARROW_DEPTH;
+}
+
 template <int DT, int DP, int NT, bool FAST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<DT, DP, NT>())))
 void attn_kernel(AttnArgs a) {
@@ -356,10 +374,17 @@ void attn_kernel(AttnArgs a) {
     int tbl = 0, tbl_hi = 0;
     const int tbl_base = kt0;
     if constexpr (FAST) {
+        // Every lane loads (a clamped entry past the item's tiles, entry 0 of
+        // the row for an item without tiles; only entries of the item's own
+        // tiles are ever read back), so no branch skips a load and nothing
+        // consumes the values before the other setup loads are issued: the
+        // count of loads in flight is the same on every path and later waits
+        // stay exact.
         const int idx = kt0 + lane;
-        tbl = idx < tbl_end ? a.block_tables[(int64_t)s * a.bt_stride + idx] : 0;
-        if constexpr (kMaxItemTiles > 64)
-            tbl_hi = idx + 64 < tbl_end ? a.block_tables[(int64_t)s * a.bt_stride + idx + 64] : 0;
+        const int32_t* row = a.block_tables + (int64_t)s * a.bt_stride;
+        const bool any = tbl_end > kt0;
+        tbl = row[any ? min(idx, tbl_end - 1) : 0];
+        if constexpr (kMaxItemTiles > 64) tbl_hi = row[any ? min(idx + 64, tbl_end - 1) : 0];
     }
     // physical block of the item's tile i (wave-uniform i)
     auto tbl_at = [&](int i) -> int {
@@ -373,19 +398,21 @@ void attn_kernel(AttnArgs a) {
     bool qvalid[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
+        // padding columns read row0's position and query (unconditional
+        // loads, results discarded)
         const int cidx = (c0 + nt) * 16 + j;
         const bool valid = nt < nct && cidx < ncols;
-        int r = 0, gq = 0, pr = row0, pos = -1;
-        if (valid) {
-            r = cidx / a.G;
-            gq = cidx - r * a.G;
-            pr = row0 + r;
-            if (a.row_map) pr = a.row_map[pr];
-            pos = (int)a.positions[pr];
-        }
+        const int r = valid ? cidx / a.G : 0;
+        const int gq = valid ? cidx - r * a.G : 0;
+        int pr = row0 + r;
+        if (a.row_map) pr = a.row_map[pr];
+        // the low word of the little-endian int64 position (what the int
+        // conversion keeps): a 64-bit load's unused high register would be
+        // reused as a temporary, and that write waits for the load
+        const int pos = reinterpret_cast<const int32_t*>(a.positions)[2 * (int64_t)pr];
         prow[nt] = pr;
         qhead[nt] = h * a.G + gq;
-        qpos[nt] = pos;
+        qpos[nt] = valid ? pos : -1;
         qvalid[nt] = valid;
     }
 
@@ -397,8 +424,10 @@ void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int c = 0; c < NL; ++c) {
             const int d0 = (c * 4 + g) * EPL;
+            // A padding column holds row0's query (its scores are computed
+            // and never stored; every column has its own softmax state).
             uint4 v = make_uint4(0, 0, 0, 0);
-            if (qvalid[nt] && d0 < D)
+            if (FAST || d0 < D)  // the fast path has head_dim == DP: every chunk exists
                 v = *(const uint4*)(a.q + ((int64_t)prow[nt] * a.q_sr + (int64_t)qhead[nt] * a.q_sh + d0) * ES);
             qf[nt][c] = make_uint4(v.x ^ a.q_sign, v.y ^ a.q_sign, v.z ^ a.q_sign, v.w ^ a.q_sign);
         }
@@ -458,46 +487,58 @@ void attn_kernel(AttnArgs a) {
             }
         }
     };
-    auto load_tile = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD], bool dummy = false) {
+    // Lane byte offsets of the V rows 4g..4g+3 inside a block, computed once.
+    uint32_t v_off[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v_off[r] = v_lane_off + (uint32_t)r * v_row_bytes;
+    // A dummy load (a prefetch slot past the item's last tile) keeps the
+    // chunk offsets but drops the lane offsets: the wave reads the block's
+    // first few lines instead of the whole tile again. `none` (wave-uniform):
+    // the item has no pool tile at all, and the dummy reads the start of Q,
+    // which every call has.
+    auto load_tile = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD], bool dummy = false, bool none = false) {
         if constexpr (FAST) {
             // block base is wave-uniform (scalar registers); the lane's byte
-            // offsets inside a block never change, so they are computed once
+            // offsets inside a block never change
             const int phys = tbl_at(kt - tbl_base);
             const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
-            const char* kb = a.k_pool + boff;
-            const char* vb = a.v_pool + boff;
+            const char* kb = none ? a.q : a.k_pool + boff;
+            const char* vb = none ? a.q : a.v_pool + boff;
+            const uint32_t sel = (dummy || none) ? 0u : 0xffffffffu;
+            const uint32_t ko = k_lane_off & sel;
             if constexpr (NT == 1 && DP * ES >= 256) {
                 // non-temporal only for rows of 256 bytes or more: measured
-                // faster there (bf16 D 128) and slower for 128-byte rows. A
-                // dummy (clamped) prefetch reads one line with every lane.
-                const uint32_t ko = dummy ? 0u : k_lane_off;
-                const uint32_t vo = dummy ? 0u : v_lane_off;
-                const uint32_t vr = dummy ? 0u : v_row_bytes;
+                // faster there (bf16 D 128) and slower for 128-byte rows
 #pragma unroll
-                for (int c = 0; c < NL; ++c) kf[c] = ld_nt16(kb + ko + (dummy ? 0 : c * 4 * 16));
+                for (int c = 0; c < NL; ++c) kf[c] = ld_nt16(kb + ko + c * 4 * 16);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) ld_words_nt<VB>(vb + vo + r * vr, vf[r]);
+                for (int r = 0; r < 4; ++r) ld_words_nt<VB>(vb + (v_off[r] & sel), vf[r]);
             } else {
 #pragma unroll
-                for (int c = 0; c < NL; ++c) kf[c] = *(const uint4*)(kb + k_lane_off + c * 4 * 16);
+                for (int c = 0; c < NL; ++c) kf[c] = *(const uint4*)(kb + ko + c * 4 * 16);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) ld_words<VB>(vb + v_lane_off + r * v_row_bytes, vf[r]);
+                for (int r = 0; r < 4; ++r) ld_words<VB>(vb + (v_off[r] & sel), vf[r]);
             }
         } else {
             load_general(kt, kf, vf);
         }
     };
 
-    // The first two tiles of a single-column-tile (decode) item go out with
+    // The first NB-1 tiles of a single-column-tile (decode) item go out with
     // the setup loads: positions only trim the item's key range, and these
-    // tiles lie in it whenever the item has any.
-    uint4 kA[NL], kB[NL];
-    uint32_t vA[4][VWD], vB[4][VWD];
+    // tiles lie in it whenever the item has any. Slots past the item's tiles
+    // take a one-line dummy load.
+    // The loads are unconditional -- an item without pool tiles issues dummy
+    // ones -- so the count of loads in flight is the same on every path and
+    // the first use of Q waits for Q alone, not for these tiles too.
+    constexpr int NB = NT == 1 ? narrow_depth<DT, DP>() : 2;
+    uint4 kR[NB][NL];
+    uint32_t vR[NB][4][VWD];
     if constexpr (FAST && NT == 1) {
-        if (kt0 < pool_end) {
-            load_tile(kt0, kA, vA);
-            load_tile(min(kt0 + 1, pool_end - 1), kB, vB);
-        }
+        const bool none = kt0 >= pool_end;
+#pragma unroll
+        for (int i = 0; i < NB - 1; ++i)
+            load_tile(max(kt0, min(kt0 + i, pool_end - 1)), kR[i], vR[i], kt0 + i > pool_end - 1, none);
     }
 
     int maxpos = -1;
@@ -813,34 +854,56 @@ void attn_kernel(AttnArgs a) {
         if (fast_end < kt_end) load_general(fast_end, kT, vT);
     }
     if (kt0 < fast_end && !wg_shared) {
+        // Ring of NB register buffers: each step issues the tile NB-1 ahead
+        // into the slot freed last and processes the oldest. The loop runs
+        // whole rounds of NB steps and the last n % NB tiles (already in
+        // slots 0..) follow after it: an exit from inside a round would give
+        // the loop a latch that some paths reach with a slot's loads still
+        // in flight, and the compiler then drains every load at the top of
+        // each round. Prefetches past the last tile still issue (a
+        // conditional load would drain the pipeline as well), but as a
+        // single line: for 256-byte rows these loads bypass L2, so a full
+        // re-read would cost HBM.
         const int last = fast_end - 1;
         int kt = kt0;
-        if constexpr (FAST && NT == 1) {
-            // kA, kB hold tiles kt0 and kt0+1 (issued with the setup loads).
-            // Prefetches past the last tile still issue (a conditional load
-            // would make the compiler drain the pipeline), but as a single
-            // line: these loads bypass L2, so a full re-read would cost HBM.
-            uint4 kC[NL];
-            uint32_t vC[4][VWD];
-            for (;;) {
-                load_tile(min(kt + 2, last), kC, vC, kt + 2 > last);
-                process(kt, kA, vA);
-                if (++kt > last) break;
-                load_tile(min(kt + 2, last), kA, vA, kt + 2 > last);
-                process(kt, kB, vB);
-                if (++kt > last) break;
-                load_tile(min(kt + 2, last), kB, vB, kt + 2 > last);
-                process(kt, kC, vC);
-                if (++kt > last) break;
+        if constexpr (NT == 1) {
+            if constexpr (!FAST) {
+                // (fast items issued these with the setup loads)
+#pragma unroll
+                for (int i = 0; i < NB - 1; ++i) load_tile(min(kt0 + i, last), kR[i], vR[i]);
             }
+            for (int r = (fast_end - kt0) / NB; r > 0; --r) {
+#pragma unroll
+                for (int u = 0; u < NB; ++u) {
+                    const int nx = kt + NB - 1;
+                    load_tile(min(nx, last), kR[(u + NB - 1) % NB], vR[(u + NB - 1) % NB], nx > last);
+                    process(kt, kR[u], vR[u]);
+                    ++kt;
+                }
+            }
+            // The last (n mod NB) tiles, as nested tests: the flat form (one
+            // test per slot) keeps every slot live through the tail and
+            // spills at 256-byte rows.
+            auto tail = [&](auto self, auto U) {
+                constexpr int u = decltype(U)::value;
+                if constexpr (u < NB - 1) {
+                    if (kt + u <= last) {
+                        process(kt + u, kR[u], vR[u]);
+                        self(self, std::integral_constant<int, u + 1>{});
+                    }
+                }
+            };
+            tail(tail, std::integral_constant<int, 0>{});
         } else {
-            load_tile(kt, kA, vA);
+            // wide items without LDS sharing (a few pooled workgroups): two
+            // buffers, which keeps the D 64 kernel at four waves per SIMD
+            load_tile(kt, kR[0], vR[0]);
             for (;;) {
-                load_tile(min(kt + 1, last), kB, vB);
-                process(kt, kA, vA);
+                load_tile(min(kt + 1, last), kR[1], vR[1]);
+                process(kt, kR[0], vR[0]);
                 if (++kt > last) break;
-                load_tile(min(kt + 1, last), kA, vA);
-                process(kt, kB, vB);
+                load_tile(min(kt + 1, last), kR[0], vR[0]);
+                process(kt, kR[1], vR[1]);
                 if (++kt > last) break;
             }
         }
@@ -852,8 +915,84 @@ void attn_kernel(AttnArgs a) {
             if (kt < kt_end) process(kt++, kT, vT);
         }
         for (; kt < kt_end; ++kt) {
-            load_general(kt, kA, vA);
-            process(kt, kA, vA);
+            load_general(kt, kR[0], vR[0]);
+            process(kt, kR[0], vR[0]);
+        }
+    }
+
+    // ---- cooperative items: the workgroup's four waves took consecutive key
+    // ranges of one (sequence, kv head, column tile) and combine their
+    // softmax states through LDS. Every lane (g, j) of every wave holds the
+    // same column j and head_dim elements (4g + r)*VCH + c; wave w combines
+    // the elements with r == w across the four waves and stores them -- the
+    // normalised output, or one partial of a longer split.
+    if constexpr (NT == 1) {
+        if (it[11] != 0) {  // the planner flags all four items of a cooperative workgroup
+            __shared__ float s_acc[kWaves][4 * VCH][64];
+            __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+            const float lt = group_sum4(l[0]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < VCH; ++c) s_acc[wave][r * VCH + c][lane] = acc[0][c][r];
+            if (g == 0) {
+                s_m[wave][j] = m[0];
+                s_l[wave][j] = lt;
+            }
+            __syncthreads();
+            float mw[kWaves], M = kMinM;
+#pragma unroll
+            for (int u = 0; u < kWaves; ++u) {
+                mw[u] = s_m[u][j];
+                M = fmaxf(M, mw[u]);
+            }
+            float L = 0.f, o[VCH];
+#pragma unroll
+            for (int c = 0; c < VCH; ++c) o[c] = 0.f;
+#pragma unroll
+            for (int u = 0; u < kWaves; ++u) {
+                const float w = __builtin_amdgcn_exp2f(mw[u] - M);
+                L += s_l[u][j] * w;
+#pragma unroll
+                for (int c = 0; c < VCH; ++c) o[c] += w * s_acc[u][wave * VCH + c][lane];
+            }
+            const int d0 = (4 * g + wave) * VCH;
+            if (nct > 0 && qpos[0] >= 0) {
+                if (pslot < 0) {
+                    if (d0 < D) {
+                        const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+                        for (int c = 0; c < VCH; ++c) o[c] *= inv;
+                        store_elems<DT, VCH>(a.out + ((int64_t)prow[0] * a.o_sr + (int64_t)qhead[0] * a.o_sh + d0) * ES, o);
+                    }
+                } else {
+                    float* ps = a.partials + (int64_t)pslot * (16 * (a.part_dstride + 2));
+                    store_elems<MF_F32, VCH>((char*)(ps + j * a.part_dstride + d0), o);
+                    if (g == 0 && wave == 0) {
+                        ps[16 * a.part_dstride + j] = M;
+                        ps[16 * a.part_dstride + 16 + j] = L;
+                    }
+                }
+            }
+            // fused split-K merge: every wave releases its part of the
+            // partial, then wave 0 counts the workgroup's arrival
+            if (pslot >= 0 && a.counters != nullptr) {
+                __threadfence();
+                __syncthreads();
+                if (wave == 0) {
+                    const int m0 = it[7];
+                    int prev = 0;
+                    if (lane == 0) prev = atomicAdd(a.counters + m0, 1);
+                    prev = __shfl(prev, 0, 64);
+                    const int32_t* mg0 = a.merges + (int64_t)m0 * MF_PLAN_MERGE_INTS;
+                    if (prev == mg0[3] - 1) {
+                        __threadfence();
+                        if (lane == 0) a.counters[m0] = 0;
+                        merge_tile<DT, DP>(a, mg0, g, j);
+                    }
+                }
+            }
+            return;
         }
     }
 
@@ -1044,6 +1183,52 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     // come as many column groups, and each split of one costs a 16-column fp32
     // partial per tile written and merged again, so they are split only as far
     // as it takes to reach kWideItems items.
+    // Narrow partition: the candidate (a power of two from 4 to
+    // kMaxItemTiles tiles per wave) with the least estimated time, where a
+    // launch takes the longer of its bandwidth time and its longest wave's
+    // chain of tiles, plus the merge launch if any range is split. A range of
+    // T > q tiles runs as ceil(T / 4q) units of four waves. Ties go to the
+    // longer partition. The constants are fitted to partition sweeps on
+    // MI355X (bf16, D 64): a lone wave's chain costs about 0.45 us per 16-key
+    // tile, decode items stream near 5 TB/s, and a split costs about 10 us of
+    // merge launch. On a 64-sequence decode step of 96-1152 keys this picks
+    // merge-free 32-tile partitions (19.1 us against 21.1 us at 4 tiles), on
+    // C3's verify and C2's decodes 32 as well, and 128 on C5.
+    auto narrow_partition = [&](int fallback) {
+        constexpr double kChainUs = 0.45, kMergeUs = 10.0, kBytesPerUs = 5.0e6;
+        const double tile_us = 16.0 * DP * mf::dtype_size(dtype) * 2 / kBytesPerUs;
+        int64_t tiles_all = 0;
+        for (int s = 0; s < num_seqs; ++s) {
+            const int nct = col_tiles(s);
+            if (nct && (nct == 1 || WT == 1)) tiles_all += (int64_t)Hkv * nct * ((kv_lens[s] + 15) / 16);
+        }
+        if (!tiles_all) return fallback;
+        int best_q = fallback;
+        double best = 1e300;
+        for (int q = 4; q <= mf::kMaxItemTiles; q *= 2) {
+            int longest = 0;
+            bool split = false;
+            for (int s = 0; s < num_seqs; ++s) {
+                const int nct = col_tiles(s);
+                if (!nct || !(nct == 1 || WT == 1)) continue;
+                const int T = (kv_lens[s] + 15) / 16;
+                if (T <= q) {
+                    longest = std::max(longest, T);
+                    continue;
+                }
+                const int units = (T + 4 * q - 1) / (4 * q);
+                const int unit = (T + units - 1) / units;
+                longest = std::max(longest, (unit + 3) / 4);
+                split = split || units > 1;
+            }
+            const double est = std::max(tiles_all * tile_us, longest * kChainUs) + (split ? kMergeUs : 0.0);
+            if (est <= best) {
+                best = est;
+                best_q = q;
+            }
+        }
+        return best_q;
+    };
     int64_t work = 0, wide_units = 0;
     int wide_max_tiles = 0;
     for (int s = 0; s < num_seqs; ++s) {
@@ -1063,11 +1248,12 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     if (P <= 0) {
         const int64_t target_items = MF_NARROW_ITEMS;
         int64_t want = (work + target_items - 1) / target_items;
-        P = 4;
-        while (P < want && P < mf::kMaxItemTiles) P *= 2;
-        // wide: the smallest partition (a power of two, at least P) whose
+        int PA = 4;
+        while (PA < want && PA < mf::kMaxItemTiles) PA *= 2;
+        P = narrow_partition(PA);
+        // wide: the smallest partition (a power of two, at least PA) whose
         // item count stays within the target
-        PW = P;
+        PW = PA;
         if (wide_units > 0) {
             auto wide_items = [&](int q) {
                 int64_t n = 0;
@@ -1082,6 +1268,14 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
         }
     }
 
+    // Narrow items (one 16-column tile): a (sequence, kv head, column tile)
+    // of at most P key tiles is one single-wave item, packed four to a
+    // workgroup with other single items. A longer one is cut into balanced
+    // units of at most 4P tiles; a unit is a cooperative workgroup whose four
+    // waves take consecutive quarters of its tiles and combine their softmax
+    // states through LDS, so only ranges of more than 4P tiles leave split-K
+    // partials for the merge kernel.
+    //
     // Wide items are launched in workgroups of kWaves (one item per wave).
     // A (sequence, kv head, partition) run of at least kWaves column groups
     // fills whole workgroups of its own -- consecutive column groups, the last
@@ -1090,26 +1284,43 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     // a workgroup, each wave on its own keys.
     const int U = mf::kWaves;
     auto round_up = [&](int64_t n) { return (n + U - 1) / U * U; };
+    // key partitions of sequence s: count, and the start of partition p
+    // (narrow cooperative ranges are balanced; the rest are Q-tile strides)
+    auto partitions = [&](int s, bool narrow, int& Q, bool& coop) {
+        const int tiles = (kv_lens[s] + 15) / 16;
+        coop = narrow && tiles > P;
+        Q = narrow ? (coop ? U * P : P) : PW;
+        return (tiles + Q - 1) / Q;
+    };
+    auto part_begin = [&](int tiles, int nparts, int Q, bool coop, int p) {
+        return coop ? (int)((int64_t)p * tiles / nparts) : std::min(tiles, p * Q);
+    };
 
     // First walk: sizes only.
-    int64_t n_narrow = 0, n_wide = 0, n_loose = 0, n_merges = 0, n_slots = 0;
+    int64_t n_single = 0, n_coop = 0, n_wide = 0, n_loose = 0, n_merges = 0, n_slots = 0;
     for (int s = 0; s < num_seqs; ++s) {
         const int nct = col_tiles(s);
         if (!nct) continue;
         const bool narrow = nct == 1 || WT == 1;
-        const int tiles = (kv_lens[s] + 15) / 16;
-        const int Q = narrow ? P : PW;
-        const int nparts = (tiles + Q - 1) / Q;
+        int Q;
+        bool coop;
+        const int nparts = partitions(s, narrow, Q, coop);
         const int width = narrow ? 1 : WT;
         const int ngroups = (nct + width - 1) / width;
-        if (narrow) n_narrow += (int64_t)nparts * Hkv * ngroups;
-        else if (ngroups >= U) n_wide += (int64_t)nparts * Hkv * round_up(ngroups);
-        else n_loose += (int64_t)nparts * Hkv * ngroups;
+        if (narrow) {
+            if (coop) n_coop += (int64_t)U * nparts * Hkv * ngroups;
+            else n_single += (int64_t)nparts * Hkv * ngroups;
+        } else if (ngroups >= U) {
+            n_wide += (int64_t)nparts * Hkv * round_up(ngroups);
+        } else {
+            n_loose += (int64_t)nparts * Hkv * ngroups;
+        }
         if (nparts > 1) {
             n_slots += (int64_t)Hkv * nparts * nct;
             n_merges += (int64_t)Hkv * nct;
         }
     }
+    const int64_t n_narrow = round_up(n_single) + n_coop;
     n_wide += round_up(n_loose);
     const int64_t pstride = 16 * (int64_t)(mf::part_dstride_for(head_dim) + 2);
     counts[0] = n_narrow;
@@ -1120,24 +1331,25 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     if ((n_narrow + n_wide) > 0 && !items) return MF_ERR_ARG;
     if (n_merges > 0 && !merges) return MF_ERR_ARG;
 
-    // Second walk: write narrow items in place and stage wide ones, and write
-    // the merges. Column group gi of a sequence owns partial slots from
-    // slot0 + gi*Hkv*nparts*width (head-major, then partition, then its w
-    // tiles) and merge records from merge0 + gi*Hkv*width.
+    // Second walk: stage the items and write the merges. Column group gi of
+    // a sequence owns partial slots from slot0 + gi*Hkv*nparts*width
+    // (head-major, then partition, then its w tiles) and merge records from
+    // merge0 + gi*Hkv*width.
     typedef std::array<int32_t, MF_PLAN_ITEM_INTS> Item;
-    std::vector<Item> shared_items, loose_items;
-    int64_t wi_narrow = 0, wm = 0, slots = 0;
+    std::vector<Item> singles, coop_items, shared_items, loose_items;
+    int64_t wm = 0, slots = 0;
     for (int s = 0; s < num_seqs; ++s) {
         const int nct = col_tiles(s);
         if (!nct) continue;
         const bool narrow = nct == 1 || WT == 1;
         const int tiles = (kv_lens[s] + 15) / 16;
-        const int Q = narrow ? P : PW;
-        const int nparts = (tiles + Q - 1) / Q;
+        int Q;
+        bool coop;
+        const int nparts = partitions(s, narrow, Q, coop);
         const int width = narrow ? 1 : WT;
         const int ngroups = (nct + width - 1) / width;
         const int64_t slot0 = slots, merge0 = wm;
-        auto make = [&](int gi, int p, int h) {
+        auto make = [&](int gi, int p, int h, int k0, int k1) {
             const int cg0 = gi * width;
             const int w = std::min(width, nct - cg0);
             Item o;
@@ -1145,8 +1357,8 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
             o[1] = h;
             o[2] = cg0;
             o[3] = w;
-            o[4] = p * Q;
-            o[5] = std::min(tiles, (p + 1) * Q);
+            o[4] = k0;
+            o[5] = k1;
             o[6] = nparts > 1 ? (int32_t)(slot0 + (int64_t)gi * Hkv * nparts * width + ((int64_t)h * nparts + p) * w)
                               : -1;
             o[7] = nparts > 1 ? (int32_t)(merge0 + (int64_t)gi * Hkv * width + (int64_t)h * w) : -1;
@@ -1156,31 +1368,38 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
             o[11] = 0;
             return o;
         };
-        if (narrow) {
-            for (int gi = 0; gi < ngroups; ++gi)
-                for (int p = 0; p < nparts; ++p)
-                    for (int h = 0; h < Hkv; ++h) {
-                        const Item o = make(gi, p, h);
-                        std::copy(o.begin(), o.end(), items + wi_narrow * MF_PLAN_ITEM_INTS);
-                        ++wi_narrow;
-                    }
-        } else {
-            for (int p = 0; p < nparts; ++p)
-                for (int h = 0; h < Hkv; ++h) {
-                    if (ngroups >= U) {
-                        for (int gi = 0; gi < round_up(ngroups); ++gi) {
-                            Item o = make(std::min(gi, ngroups - 1), p, h);
-                            if (gi >= ngroups) {  // padding: same keys, no columns, no partial slot
-                                o[3] = 0;
-                                o[6] = -1;
-                                o[7] = -1;
-                            }
-                            shared_items.push_back(o);
+        for (int p = 0; p < nparts; ++p) {
+            const int k0 = part_begin(tiles, nparts, Q, coop, p);
+            const int k1 = part_begin(tiles, nparts, Q, coop, p + 1);
+            for (int h = 0; h < Hkv; ++h) {
+                if (narrow) {
+                    for (int gi = 0; gi < ngroups; ++gi) {
+                        if (!coop) {
+                            singles.push_back(make(gi, p, h, k0, k1));
+                            continue;
                         }
-                    } else {
-                        for (int gi = 0; gi < ngroups; ++gi) loose_items.push_back(make(gi, p, h));
+                        // four waves on consecutive quarters of [k0, k1)
+                        const int n = k1 - k0;
+                        for (int w = 0; w < U; ++w) {
+                            Item o = make(gi, p, h, k0 + (int)((int64_t)w * n / U), k0 + (int)((int64_t)(w + 1) * n / U));
+                            o[11] = 1;
+                            coop_items.push_back(o);
+                        }
                     }
+                } else if (ngroups >= U) {
+                    for (int gi = 0; gi < round_up(ngroups); ++gi) {
+                        Item o = make(std::min(gi, ngroups - 1), p, h, k0, k1);
+                        if (gi >= ngroups) {  // padding: same keys, no columns, no partial slot
+                            o[3] = 0;
+                            o[6] = -1;
+                            o[7] = -1;
+                        }
+                        shared_items.push_back(o);
+                    }
+                } else {
+                    for (int gi = 0; gi < ngroups; ++gi) loose_items.push_back(make(gi, p, h, k0, k1));
                 }
+            }
         }
         if (nparts > 1) {
             for (int gi = 0; gi < ngroups; ++gi) {
@@ -1207,40 +1426,41 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     }
     // Longest first: the hardware hands out workgroups in order as slots free
     // up, so the last round of the grid is made of the short remainder
-    // partitions instead of a few long ones. Stable, so equal lengths keep
-    // their heads-adjacent order.
+    // partitions instead of a few long ones. Items that run alone are sorted
+    // and then cut into workgroups (the last padded with empty items); all
+    // workgroups are ordered by their longest item. Stable, so equal lengths
+    // keep their heads-adjacent order.
     auto len = [](const Item& o) { return o[5] - o[4]; };
     auto longer = [&](const Item& x, const Item& y) { return len(x) > len(y); };
-    {
-        std::vector<Item> nar((size_t)n_narrow);
-        for (int64_t i = 0; i < n_narrow; ++i)
-            std::copy(items + i * MF_PLAN_ITEM_INTS, items + (i + 1) * MF_PLAN_ITEM_INTS, nar[i].begin());
-        std::stable_sort(nar.begin(), nar.end(), longer);
-        for (int64_t i = 0; i < n_narrow; ++i)
-            std::copy(nar[i].begin(), nar[i].end(), items + i * MF_PLAN_ITEM_INTS);
-    }
-    // wide: loose items sorted, then cut into workgroups (the last padded
-    // with empty items); all workgroups ordered by their longest item
-    std::stable_sort(loose_items.begin(), loose_items.end(), longer);
-    while (loose_items.size() % U) {
-        Item o{};
-        o[6] = -1;
-        o[7] = -1;
-        loose_items.push_back(o);
-    }
-    std::vector<const Item*> units;
-    for (size_t i = 0; i < shared_items.size(); i += U) units.push_back(&shared_items[i]);
-    for (size_t i = 0; i < loose_items.size(); i += U) units.push_back(&loose_items[i]);
+    auto pad_to_workgroups = [&](std::vector<Item>& v) {
+        std::stable_sort(v.begin(), v.end(), longer);
+        while (v.size() % U) {
+            Item o{};
+            o[6] = -1;
+            o[7] = -1;
+            v.push_back(o);
+        }
+    };
     auto unit_len = [&](const Item* u) {
         int l = 0;
         for (int w = 0; w < U; ++w) l = std::max(l, len(u[w]));
         return l;
     };
-    std::stable_sort(units.begin(), units.end(),
-                     [&](const Item* x, const Item* y) { return unit_len(x) > unit_len(y); });
-    int64_t wi = n_narrow;
-    for (const Item* u : units)
-        for (int w = 0; w < U; ++w, ++wi) std::copy(u[w].begin(), u[w].end(), items + wi * MF_PLAN_ITEM_INTS);
+    auto emit = [&](std::vector<const Item*>& units, int64_t wi) {
+        std::stable_sort(units.begin(), units.end(),
+                         [&](const Item* x, const Item* y) { return unit_len(x) > unit_len(y); });
+        for (const Item* u : units)
+            for (int w = 0; w < U; ++w, ++wi) std::copy(u[w].begin(), u[w].end(), items + wi * MF_PLAN_ITEM_INTS);
+    };
+    pad_to_workgroups(singles);
+    pad_to_workgroups(loose_items);
+    std::vector<const Item*> nunits, wunits;
+    for (size_t i = 0; i < coop_items.size(); i += U) nunits.push_back(&coop_items[i]);
+    for (size_t i = 0; i < singles.size(); i += U) nunits.push_back(&singles[i]);
+    for (size_t i = 0; i < shared_items.size(); i += U) wunits.push_back(&shared_items[i]);
+    for (size_t i = 0; i < loose_items.size(); i += U) wunits.push_back(&loose_items[i]);
+    emit(nunits, 0);
+    emit(wunits, n_narrow);
     return MF_OK;
 }
 

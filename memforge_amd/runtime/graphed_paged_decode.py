@@ -52,7 +52,10 @@ class _Bucket:
         self.host = torch.zeros(self.inputs.numel(), dtype=torch.int32).pin_memory()
         self.packed = nat.PackedStep.allocate(b, b, mb, dev)
         hkv = owner.pool.spec.num_kv_heads
-        cap_items = b * hkv * math.ceil(mb / _MIN_PARTITION_TILES)
+        # a (sequence, kv head) of T tiles is one item when T <= P, else four
+        # per unit of at most 4P tiles (P >= _MIN_PARTITION_TILES), and the
+        # single items are padded to whole workgroups
+        cap_items = b * hkv * (math.ceil(mb / _MIN_PARTITION_TILES) + 4) + 4
         floats = cap_items * 16 * (max(owner.pool.spec.head_dim, 32) + 2)
         self.plan = nat.CountedPlan(cap_items, 0, b * hkv, floats, dev)
         self.keep = torch.arange(b, dtype=torch.long, device=dev)

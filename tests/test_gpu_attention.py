@@ -328,3 +328,33 @@ def test_scale_sign_and_zero(device, dtype, scale):
     want = oatt.varlen_attention(to_np64(q), to_np64(kp), to_np64(vp), tables, seq_ids, positions, bs,
                                  scale=scale)
     _check(to_np64(got), want, dt)
+
+
+@pytest.mark.parametrize("dtype,d", [("fp32", 16), ("fp32", 128), ("bf16", 32), ("bf16", 64),
+                                     ("bf16", 128), ("bf16", 256), ("fp16", 64)])
+@pytest.mark.parametrize("partition_tiles,fused", [(1, False), (2, True), (8, False), (0, False)])
+def test_cooperative_units(device, dtype, d, partition_tiles, fused):
+    """Decode ranges longer than P tiles run as cooperative workgroups: four
+    waves on consecutive quarters of the range, combined through LDS. The
+    contexts give single items, units with fewer tiles than waves (empty
+    quarters), units that finish the output and units that leave split-K
+    partials (merged by the merge kernel or, fused, by the last arrival)."""
+    from memforge_amd import _native as nat
+
+    dt = DT[dtype]
+    gen = torch.Generator().manual_seed(41 + d + partition_tiles)
+    bs, hq, hkv = 16, 12, 4
+    ctx = [1, 16, 17, 33, 50, 64, 65, 130, 300, 517, 1000, 2100]
+    B = len(ctx)
+    items, _, counts = nat.plan_attention_host(list(range(B + 1)), ctx, hq, hkv, d, dt, partition_tiles)
+    coop = items[: int(counts[0])][items[: int(counts[0]), 11] == 1]
+    assert len(coop) > 0 and (coop[:, 6] >= 0).any() and (coop[:, 6] < 0).any()
+    if partition_tiles == 1:
+        assert (coop[:, 5] == coop[:, 4]).any(), "want a unit with an empty quarter"
+    tables = random_tables(gen, sum((c + bs - 1) // bs for c in ctx) + 3, ctx, bs)
+    kp, vp = _pool(gen, max(max(t) for t in tables) + 1, bs, hkv, d, dt, device)
+    q = torch.randn((hq, B, d), generator=gen).to(dt).to(device)
+    positions = [c - 1 for c in ctx]
+    got = gpu_varlen(q, kp, vp, tables, list(range(B)), positions, partition_tiles=partition_tiles, fused=fused)
+    want = oatt.varlen_attention(to_np64(q), to_np64(kp), to_np64(vp), tables, list(range(B)), positions, bs)
+    _check(to_np64(got), want, dt)

@@ -71,13 +71,29 @@ def test_plan_covers_every_tile_exactly_once_and_merges_line_up(dtype, d, pt):
         if len({(it[0], it[1], it[4], it[5]) for it in unit}) == 1:
             real = [it[2] for it in unit if it[3] > 0]
             assert len(real) == len(set(real)), "shared workgroup repeats a column group"
-    for it in items:
+    # narrow items come in workgroups of four too: four single items, or one
+    # cooperative unit (flag in the last int) whose waves take consecutive
+    # key ranges of one (sequence, head, column tile) and share its slot
+    assert p.n_narrow % 4 == 0
+    for u in range(0, p.n_narrow, 4):
+        unit = items[u:u + 4]
+        flags = {int(it[11]) for it in unit}
+        assert len(flags) == 1, "a workgroup mixes cooperative and single items"
+        if flags == {1}:
+            assert len({(int(it[0]), int(it[1]), int(it[2]), int(it[6]), int(it[7])) for it in unit}) == 1
+            assert all(int(unit[w][5]) == int(unit[w + 1][4]) for w in range(3)), "quarters not consecutive"
+            assert int(unit[0][3]) == 1
+    for i in range(p.n_narrow, p.n_narrow + p.n_wide):
+        assert int(items[i][11]) == 0
+    for i, it in enumerate(items):
         s, h, c0, nct, kt0, kt1, slot, merge, row0, nrows, kvl = (int(x) for x in it[:11])
+        coop = int(it[11]) == 1
         if nct == 0:
             assert slot == -1 and merge == -1, "padding item owns a partial slot"
             continue
         assert (row0, nrows, kvl) == (cu[s], q_lens[s], kv[s]), "item carries its sequence's bounds"
-        assert kt1 > kt0 and kt1 - kt0 <= 128
+        assert kt1 >= kt0 and kt1 - kt0 <= 128
+        assert kt1 > kt0 or coop, "an empty key range outside a cooperative unit"
         for c in range(c0, c0 + nct):
             for kt in range(kt0, kt1):
                 key = (s, h, c, kt)
@@ -85,6 +101,9 @@ def test_plan_covers_every_tile_exactly_once_and_merges_line_up(dtype, d, pt):
                 cover[key] = True
             if slot >= 0:
                 sl = slot + (c - c0)
+                if coop and i % 4:
+                    assert slots[sl] == (s, h, c)  # the unit's first wave claimed it
+                    continue
                 assert sl not in slots
                 slots[sl] = (s, h, c)
     for s, (q, n) in enumerate(zip(q_lens, kv)):
@@ -129,8 +148,32 @@ def test_plan_capacity_and_argument_errors():
 def test_plan_orders_longest_items_first():
     p = _plan([0, 1, 2, 3], [40, 4000, 900], pt=64)
     narrow = p.items_host[: p.n_narrow]
-    lengths = narrow[:, 5] - narrow[:, 4]
-    assert list(lengths) == sorted(lengths, reverse=True)
+    # workgroups ordered by their longest wave
+    lengths = [int((narrow[u:u + 4, 5] - narrow[u:u + 4, 4]).max()) for u in range(0, p.n_narrow, 4)]
+    assert lengths == sorted(lengths, reverse=True)
+
+
+def test_plan_cooperative_units_replace_split_k_up_to_four_partitions():
+    """A narrow range of more than P tiles runs as one cooperative workgroup
+    (four waves on consecutive quarters, combined in LDS) up to 4P tiles; only
+    longer ranges leave split-K partials for the merge kernel."""
+    P = 8
+    # one decode row each: 8 tiles (single), 9 and 32 tiles (one unit), 33 tiles (two units)
+    kv = [8 * 16, 9 * 16, 32 * 16, 33 * 16]
+    p = _plan([0, 1, 2, 3, 4], kv, hq=8, hkv=2, pt=P)
+    items = p.items_host[: p.n_narrow]
+    per_seq = {}
+    for it in items:
+        if int(it[3]) == 0:
+            continue
+        per_seq.setdefault(int(it[0]), []).append(it)
+    assert all(int(it[11]) == 0 for it in per_seq[0]) and len(per_seq[0]) == 2  # one per head
+    for s in (1, 2):
+        assert len(per_seq[s]) == 8 and all(int(it[11]) == 1 and int(it[6]) == -1 for it in per_seq[s])
+        assert max(int(it[5] - it[4]) for it in per_seq[s]) == -(-kv[s] // 16 // 4)
+    assert len(per_seq[3]) == 16 and all(int(it[6]) >= 0 for it in per_seq[3])
+    assert p.n_merges == 2  # sequence 3, both heads
+    assert all(int(m[3]) == 2 for m in p.merges_host)
 
 
 def test_verify_workspace_size_grows_with_the_batch():
