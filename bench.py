@@ -40,7 +40,7 @@ B, HQ, HKV, D, BS, LAYERS = 256, 40, 8, 128, 16, 48
 # rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch). Each is
 # scaled by what the same counter reads for a plain copy of exactly 1 GiB on
 # the MI355X: FETCH_SIZE reports half the bytes (x2.0), WRITE_SIZE all (x1.0).
-PMC_DEFAULT = {"fetch_kib": 1619788.4, "write_kib": 9273.4, "fetch_scale": 2.0, "write_scale": 1.0}
+PMC_DEFAULT = {"fetch_kib": 1619051.2, "write_kib": 3210.7, "fetch_scale": 2.0, "write_scale": 1.0}
 
 
 def parse_args():
