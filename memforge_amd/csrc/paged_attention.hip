@@ -821,18 +821,22 @@ void attn_kernel(AttnArgs a) {
                 fetch(kt0 + TPS, rs);
                 sync();
                 for (int u = 0; u < nst; ++u) {
+                    // fragments of staged tile v (K rows swizzled, V rows plain)
+                    auto frags = [&](int v, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
+                        const char* stg = smem + ((u & 1) * TPS + v) * STAGE;
+#pragma unroll
+                        for (int c = 0; c < NL; ++c)
+                            kf[c] = *(const uint4*)(stg + j * RB + (((c * 4 + g) ^ (j & (NCH - 1))) << 4));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) ld_words<VB>(stg + 16 * RB + (4 * g + r) * RB + j * VB, vf[r]);
+                    };
 #pragma unroll
                     for (int v = 0; v < TPS; ++v) {
                         const int t = kt0 + u * TPS + v;
                         if (t < fast_end) {
-                            const char* stg = smem + ((u & 1) * TPS + v) * STAGE;
                             uint4 kf[NL];
                             uint32_t vf[4][VWD];
-#pragma unroll
-                            for (int c = 0; c < NL; ++c)
-                                kf[c] = *(const uint4*)(stg + j * RB + (((c * 4 + g) ^ (j & (NCH - 1))) << 4));
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) ld_words<VB>(stg + 16 * RB + (4 * g + r) * RB + j * VB, vf[r]);
+                            frags(v, kf, vf);
                             process(t, kf, vf);
                         }
                     }
