@@ -98,8 +98,14 @@ def _check(status: int, what: str) -> None:
         raise MemforgeHipError(f"{what}: {msg} (status {status}, hip error {L.mf_last_hip_error()})")
 
 
-def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+def _stream(device: Optional[torch.device] = None) -> int:
+    """Raw handle of the current HIP stream of ``device`` (default: the current
+    device) -- the stream torch's own kernels are queued on, also under
+    ``torch.cuda.stream`` and graph capture. The raw query costs about 0.1 us
+    against 3 us for building a ``torch.cuda.Stream`` object."""
+    if device is None or device.index is None:
+        return torch._C._cuda_getCurrentRawStream(torch.cuda.current_device())
+    return torch._C._cuda_getCurrentRawStream(device.index)
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -186,7 +192,7 @@ def kv_write(k_rows: torch.Tensor, v_rows: torch.Tensor, slots: torch.Tensor, po
     _check(lib().mf_kv_write(
         _ptr(k_rows), _ptr(v_rows), dtype_code(k_rows.dtype), k_rows.stride(0), k_rows.stride(1),
         _ptr(slots), T, _ptr(pool.k), _ptr(pool.v), dtype_code(pool.k.dtype),
-        pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size, H, D, _stream(),
+        pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size, H, D, _stream(k_rows.device),
     ), "mf_kv_write")
 
 
@@ -203,7 +209,7 @@ def kv_gather(pool: PoolView, slots: torch.Tensor, k_rows: torch.Tensor, v_rows:
     _check(lib().mf_kv_gather(
         _ptr(pool.k), _ptr(pool.v), dtype_code(pool.k.dtype), pool.stride_block, pool.stride_slot,
         pool.stride_head, pool.block_size, _ptr(slots), T, _ptr(k_rows), _ptr(v_rows),
-        dtype_code(k_rows.dtype), k_rows.stride(0), k_rows.stride(1), H, D, _stream(),
+        dtype_code(k_rows.dtype), k_rows.stride(0), k_rows.stride(1), H, D, _stream(k_rows.device),
     ), "mf_kv_gather")
 
 
@@ -223,7 +229,7 @@ def kv_copy_blocks(key_pool: torch.Tensor, value_pool: torch.Tensor,
     flat = np.ascontiguousarray(np.asarray(list(pairs), dtype=np.int64).reshape(-1, 2))
     _check(lib().mf_kv_copy_blocks(
         _ptr(key_pool), _ptr(value_pool), dtype_code(key_pool.dtype), L, key_pool.stride(0),
-        key_pool.stride(1), bs * H * D, N, flat.ctypes.data, flat.shape[0], _stream(),
+        key_pool.stride(1), bs * H * D, N, flat.ctypes.data, flat.shape[0], _stream(key_pool.device),
     ), "mf_kv_copy_blocks")
 
 
@@ -254,6 +260,26 @@ def _views(buf: torch.Tensor, arrs: Sequence[np.ndarray], offs: Sequence[int]) -
     return out
 
 
+def _pack_host(parts: Sequence[np.ndarray], pinned: bool) -> Tuple[torch.Tensor, List[np.ndarray], List[int]]:
+    """The parts packed into one int32 host tensor (pinned if asked), each on
+    an 8-byte boundary: (tensor, contiguous parts, word offsets)."""
+    arrs, offs, n = _layout(parts)
+    host = torch.empty(n, dtype=torch.int32, pin_memory=pinned)
+    h = host.numpy()
+    for a, o in zip(arrs, offs):
+        h[o:o + a.size * a.itemsize // 4] = a.reshape(-1).view(np.int32)
+    return host, arrs, offs
+
+
+def upload_packed(parts: Sequence[np.ndarray], device) -> Tuple[torch.Tensor, List[int]]:
+    """``upload`` without the per-part views: the device int32 buffer and each
+    part's word offset in it (for callers that pass addresses to the C ABI)."""
+    host, _, offs = _pack_host(parts, True)
+    buf = torch.empty(host.numel(), dtype=torch.int32, device=device)
+    buf.copy_(host, non_blocking=True)
+    return buf, offs
+
+
 def upload(parts: Sequence[np.ndarray], device) -> List[torch.Tensor]:
     """Move int32 / int64 host arrays to ``device`` with ONE host-to-device
     copy: they are packed into a pinned buffer (each part on an 8-byte
@@ -262,16 +288,12 @@ def upload(parts: Sequence[np.ndarray], device) -> List[torch.Tensor]:
     pinned buffer comes from torch's caching host allocator, which does not
     hand it out again before the copy has completed, so the host never waits
     for the GPU here."""
-    arrs, offs, n = _layout(parts)
     dev = torch.device(device)
     pinned = dev.type == "cuda"
-    host = torch.empty(n, dtype=torch.int32, pin_memory=pinned)
-    h = host.numpy()
-    for a, o in zip(arrs, offs):
-        h[o:o + a.size * a.itemsize // 4] = a.reshape(-1).view(np.int32)
+    host, arrs, offs = _pack_host(parts, pinned)
     if not pinned:
         return _views(host.to(dev), arrs, offs)
-    buf = torch.empty(n, dtype=torch.int32, device=dev)
+    buf = torch.empty(host.numel(), dtype=torch.int32, device=dev)
     buf.copy_(host, non_blocking=True)
     return _views(buf, arrs, offs)
 
@@ -306,16 +328,30 @@ def plan_attention_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q
     L = lib()
     args = (B, cu.ctypes.data, kv.ctypes.data, num_q_heads, num_kv_heads, head_dim,
             dtype_code(dtype), partition_tiles)
-    st = L.mf_attention_plan(*args, None, 0, None, 0, counts.ctypes.data)
-    if st not in (0, -3):
-        _check(st, "mf_attention_plan")
+    # One planner call when the plan fits the largest one seen so far (the
+    # planner fills every row it reports); otherwise it reports the sizes and
+    # a second call fills arrays of exactly that size.
+    cap_items, cap_merges = _PLAN_CAPACITY
+    items = np.empty((cap_items, PLAN_ITEM_INTS), dtype=np.int32)
+    merges = np.empty((cap_merges, PLAN_MERGE_INTS), dtype=np.int32)
+    st = L.mf_attention_plan(*args, items.ctypes.data, cap_items, merges.ctypes.data, cap_merges,
+                             counts.ctypes.data)
+    if st == -3:  # MF_ERR_WORKSPACE: counts holds the sizes
+        n_items, n_merges = int(counts[0] + counts[1]), int(counts[2])
+        _PLAN_CAPACITY[0] = max(cap_items, min(n_items, 1 << 16))
+        _PLAN_CAPACITY[1] = max(cap_merges, min(n_merges, 1 << 14))
+        items = np.empty((max(n_items, 1), PLAN_ITEM_INTS), dtype=np.int32)
+        merges = np.empty((max(n_merges, 1), PLAN_MERGE_INTS), dtype=np.int32)
+        st = L.mf_attention_plan(*args, items.ctypes.data, n_items, merges.ctypes.data, n_merges,
+                                 counts.ctypes.data)
+    _check(st, "mf_attention_plan")
     n_items = int(counts[0] + counts[1])
     n_merges = int(counts[2])
-    items = np.zeros((max(n_items, 1), PLAN_ITEM_INTS), dtype=np.int32)
-    merges = np.zeros((max(n_merges, 1), PLAN_MERGE_INTS), dtype=np.int32)
-    _check(L.mf_attention_plan(*args, items.ctypes.data, n_items, merges.ctypes.data, n_merges,
-                               counts.ctypes.data), "mf_attention_plan")
     return items[:n_items], merges[:n_merges], counts
+
+
+# host array sizes for a one-call plan, grown to the largest plan seen
+_PLAN_CAPACITY = [256, 64]
 
 
 def plan_upload_parts(items: np.ndarray, merges: np.ndarray) -> List[np.ndarray]:
@@ -395,7 +431,8 @@ class Workspace:
     def partials(self, floats: int, device) -> Optional[torch.Tensor]:
         if floats <= 0:
             return None
-        key = (str(device), _stream())
+        dev = torch.device(device)
+        key = (dev.index, _stream(dev))
         buf = self._partials.get(key)
         if buf is None or buf.numel() < floats:
             buf = torch.empty(max(floats, 1 << 16), dtype=torch.float32, device=device)
@@ -405,7 +442,8 @@ class Workspace:
     def counters(self, n: int, device) -> Optional[torch.Tensor]:
         if n <= 0:
             return None
-        key = (str(device), _stream())
+        dev = torch.device(device)
+        key = (dev.index, _stream(dev))
         buf = self._counters.get(key)
         if buf is None or buf.numel() < n:
             buf = torch.zeros(max(n, 1 << 12), dtype=torch.int32, device=device)
@@ -470,7 +508,54 @@ def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView
         nk.stride(0) if nk is not None else 0, nk.stride(1) if nk is not None else 0,
         Hq, num_kv_heads, D, float(scale),
         _ptr(plan.items), plan.n_narrow, plan.n_wide, _ptr(plan.merges), plan.n_merges,
-        _ptr(partials), partials.numel() if partials is not None else 0, _ptr(counters), _stream(),
+        _ptr(partials), partials.numel() if partials is not None else 0, _ptr(counters), _stream(q_rows.device),
+    ), "mf_paged_attention")
+
+
+def paged_attention_packed(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView, buf: torch.Tensor,
+                           offsets: Sequence[int], num_seqs: int, bt_stride: int, counts: np.ndarray,
+                           scale: float, num_kv_heads: int, has_row_map: bool, has_pool_lens: bool,
+                           new_k_rows: Optional[torch.Tensor] = None,
+                           new_v_rows: Optional[torch.Tensor] = None) -> None:
+    """mf_paged_attention on index arrays that one ``upload`` placed in the
+    device buffer ``buf`` at ``offsets`` (int32 words, as ``_layout`` gives
+    them): the padded block tables, the plan's items, its merges, cu_seqlens
+    followed by kv_lens (``num_seqs`` + 1 and ``num_seqs`` int32), the int64
+    positions, then the row map and the pool lengths when present. The caller
+    built all of them, so only the tensors it did not build (query, output,
+    pool, in-flight rows) are checked, and the launch takes addresses inside
+    ``buf`` instead of building a tensor view per array."""
+    _rows_ok(q_rows, "q_rows")
+    _rows_ok(out_rows, "out_rows")
+    require_device(q_rows, out_rows, pool.k, buf)
+    if q_rows.dtype != pool.k.dtype or out_rows.dtype != pool.k.dtype:
+        raise TypeError("query, output and pool must share a dtype")
+    if buf.dtype != torch.int32 or not buf.is_contiguous():
+        raise TypeError("buf must be a contiguous int32 tensor")
+    nk, nv = new_k_rows, new_v_rows
+    if has_pool_lens:
+        if nk is None or nv is None:
+            raise ValueError("pool_lens needs the in-flight new_k_rows/new_v_rows")
+        require_device(nk, nv)
+        if nk.stride() != nv.stride():
+            raise ValueError("in-flight K and V rows must share strides")
+    dev = q_rows.device
+    n_narrow, n_wide, n_merges, floats = (int(x) for x in counts)
+    partials = _WORKSPACE.partials(floats, dev)
+    addr = [buf.data_ptr() + 4 * o for o in offsets]
+    row_map = addr[5] if has_row_map else None
+    pool_lens = addr[5 + int(has_row_map)] if has_pool_lens else None
+    _check(lib().mf_paged_attention(
+        _ptr(q_rows), q_rows.stride(0), q_rows.stride(1),
+        _ptr(out_rows), out_rows.stride(0), out_rows.stride(1),
+        dtype_code(q_rows.dtype), _ptr(pool.k), _ptr(pool.v),
+        pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size,
+        addr[0], bt_stride, addr[3], addr[3] + 4 * (num_seqs + 1), addr[4],
+        row_map, pool_lens, _ptr(nk), _ptr(nv),
+        nk.stride(0) if nk is not None else 0, nk.stride(1) if nk is not None else 0,
+        q_rows.shape[1], num_kv_heads, q_rows.shape[2], float(scale),
+        addr[1], n_narrow, n_wide, addr[2], n_merges,
+        _ptr(partials), partials.numel() if partials is not None else 0, None, _stream(dev),
     ), "mf_paged_attention")
 
 
@@ -492,7 +577,7 @@ def _paged_attention_counted(q_rows, out_rows, pool, block_tables, cu_seqlens, k
         nk.stride(0) if nk is not None else 0, nk.stride(1) if nk is not None else 0,
         Hq, num_kv_heads, D, float(scale),
         _ptr(plan.items), plan.cap_narrow, plan.cap_wide, _ptr(plan.merges), plan.cap_merges,
-        _ptr(plan.counts), _ptr(plan.partials), plan.partials.numel(), _stream(),
+        _ptr(plan.counts), _ptr(plan.partials), plan.partials.numel(), _stream(q_rows.device),
     ), "mf_paged_attention_counted")
 
 

@@ -67,21 +67,19 @@ def run_varlen(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: nat.PoolView,
     identity = row_map == list(range(T))
     items, merges, counts = nat.plan_attention_host(cu, kvl, hq, num_kv_heads, d, q_rows.dtype)
     # tables, plan, cu/kv lengths, positions, row map and pool lengths cross
-    # to the device in one copy
-    parts = [padded_tables_host([tables[s] for s in order]), *nat.plan_upload_parts(items, merges),
+    # to the device in one copy, and the launch addresses them inside that
+    # one buffer
+    tables_host = padded_tables_host([tables[s] for s in order])
+    parts = [tables_host, *nat.plan_upload_parts(items, merges),
              np.asarray(cu + kvl, dtype=np.int32), np.asarray(list(positions), dtype=np.int64)]
     if not identity:
         parts.append(np.asarray(row_map, dtype=np.int32))
     if pool_lens is not None:
         parts.append(np.asarray([pool_lens[s] for s in order], dtype=np.int32))
-    dev_parts = nat.upload(parts, dev)
-    bt, d_items, d_merges, meta, pos = dev_parts[:5]
-    rest = dev_parts[5:]
-    rmap = None if identity else rest.pop(0)
-    pl = rest.pop(0) if pool_lens is not None else None
-    plan = nat.plan_from_parts(items, merges, counts, d_items, d_merges)
-    nat.paged_attention(
-        q_rows, out_rows, pool, bt, meta[: len(cu)], meta[len(cu):], pos, plan,
+    buf, offsets = nat.upload_packed(parts, dev)
+    nat.paged_attention_packed(
+        q_rows, out_rows, pool, buf, offsets, len(order), tables_host.shape[1], counts,
         scale if scale is not None else 1.0 / math.sqrt(d), num_kv_heads,
-        row_map=rmap, pool_lens=pl, new_k_rows=new_k_rows, new_v_rows=new_v_rows,
+        has_row_map=not identity, has_pool_lens=pool_lens is not None,
+        new_k_rows=new_k_rows, new_v_rows=new_v_rows,
     )

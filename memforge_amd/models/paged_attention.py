@@ -50,7 +50,13 @@ class PagedKVCache:
         self.value_cache = torch.zeros(shape, dtype=dtype, device=device)
 
     def _view(self) -> nat.PoolView:
-        return nat.PoolView.from_bhsd(self.key_cache, self.value_cache)
+        # built once per (key_cache, value_cache) pair: the strides checks and
+        # the view are the same on every call
+        pv = getattr(self, "_pool_view", None)
+        if pv is None or pv.k is not self.key_cache or pv.v is not self.value_cache:
+            pv = nat.PoolView.from_bhsd(self.key_cache, self.value_cache)
+            self._pool_view = pv
+        return pv
 
     def _slots(self, block_table: List[int], start: int, count: int) -> torch.Tensor:
         pos = np.arange(start, start + count, dtype=np.int64)
