@@ -322,10 +322,6 @@ constexpr int attn_waves_per_eu() {
 #ifndef MF_NARROW_DEPTH
 #define MF_NARROW_DEPTH 3
 #endif
-template <int DT, int DP>
-constexpr int narrow_depth() {
-    return MF_NARROW_DEPTH;
-}
 
 template <int DT, int DP, int NT, bool FAST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<DT, DP, NT>())))
@@ -531,7 +527,7 @@ void attn_kernel(AttnArgs a) {
     // The loads are unconditional -- an item without pool tiles issues dummy
     // ones -- so the count of loads in flight is the same on every path and
     // the first use of Q waits for Q alone, not for these tiles too.
-    constexpr int NB = NT == 1 ? narrow_depth<DT, DP>() : 2;
+    constexpr int NB = NT == 1 ? MF_NARROW_DEPTH : 2;
     uint4 kR[NB][NL];
     uint32_t vR[NB][4][VWD];
     if constexpr (FAST && NT == 1) {
@@ -703,11 +699,12 @@ void attn_kernel(AttnArgs a) {
         }
     };
 
-    // ---- key loop, software-pipelined. Single-tile fast items (decode) keep
-    // two tiles in flight ahead of the one being processed (three register
-    // buffers; that kernel is at two waves per SIMD either way), the rest one. The
-    // prefetch is unconditional -- the last iterations re-read the final tile,
-    // an L2 hit -- because a conditional load makes the compiler drain every
+    // ---- key loops. Single-column-tile items (decode, verify) stream their
+    // own tiles through the NB-buffer register ring below; wide items either
+    // share each tile through LDS (next) or, pooled four to a workgroup with
+    // unrelated items, stream their own tiles through two buffers. Every
+    // prefetch is unconditional (past the end it is a dummy or a clamped
+    // re-read) because a conditional load makes the compiler drain every
     // outstanding load at the join and serialises the pipeline.
     // ---- workgroup-shared key loop (16-bit wide items on the fast path).
     // When the workgroup's four items cover one (sequence, kv head, key

@@ -5,15 +5,20 @@
 // chunks, one 256-thread workgroup per (row, chunk), every element loaded once
 // into registers with 16-byte vector loads; the workgroup writes its chunk's
 // max, sum of exp(x - max) and first argmax of the raw logits.
-// Launches 2-4 (one workgroup per (row, 4096-element chunk)): the first
-// combines the chunk statistics of the row's K+1 target positions and runs the
-// sequential accept loop over the K candidates in one lane, in double
-// precision, exactly the reference's arithmetic; then the vocabulary passes of
-// the final draw -- the residual max(p - q, 0) and its sum, the weights and
-// their sum (the second normalisation the reference's sample_from_probs
-// applies), and argmax(w / E) with first-index ties, which is
-// torch.multinomial(w, 1) given the same Exp(1) draws E. Launch 5 combines the
-// chunk winners.
+// Launch 2 (one workgroup per (row, 4096-element chunk)): combines the chunk
+// statistics of the row's K+1 target positions, runs the sequential accept
+// loop over the K candidates in one lane, in double precision, exactly the
+// reference's arithmetic, and takes one pass over its chunk of the stopping
+// position for the final draw. The reference draws with
+// torch.multinomial(w, 1), which for one sample is argmax(w / E) with Exp(1)
+// draws E, where w is the residual max(p - q, 0) normalised twice (by its sum,
+// then again in sample_from_probs) when the round rejected and the residual
+// has mass, else the target row p normalised, or uniform when p has no mass.
+// Each normalisation divides every candidate by the same positive number, which
+// leaves the argmax where it is, so the pass keeps the three first-index
+// argmaxes -- of max(p - q, 0) / E, of max(p, 0) / E and of 1 / E -- and
+// whether any residual or target value is positive. Launch 3 picks the family
+// the reference's branches would take and combines the chunk winners.
 // (memforge_ml/speculative/rejection_sampler.py:12-83,
 //  memforge_ml/runtime/batched_speculative.py:112-124, 731-777)
 #include <cfloat>
@@ -54,27 +59,14 @@ struct VerifyArgs {
     float* st_max;        // [rows][nchunk]
     float* st_sum;
     int32_t* st_arg;
-    float* pos_max;       // [rows] combined statistics of each target position
-    float* pos_sum;
-    int32_t* pos_arg;
     int32_t* row_stop;    // [B] stop position and whether it rejected
     int32_t* row_reject;
     int npass;            // draw-pass chunks per row
-    float* part_diff;     // [B][npass]
-    float* part_w;
-    float* part_best;
+    float* part_best;     // [3][B][npass]: residual, target, uniform candidates
     int32_t* part_best_i;
+    int32_t* part_any;    // [B][npass]: bit 0 some residual > 0, bit 1 some target p > 0
     int vec_logits, vec_q, vec_e;  // rows are aligned for vector loads
 };
-
-// Target probability of token v at target row `row` (= b * (K + 1) + i)
-// whose raw logit (or probability) is `raw`.
-__device__ __forceinline__ float target_prob(const VerifyArgs& a, int row, float raw, int v) {
-    if (a.target_is_probs) return raw;
-    if (a.temperature <= 0.f) return v == a.pos_arg[row] ? 1.f : 0.f;
-    const float x = a.temperature == 1.f ? raw : raw / a.temperature;
-    return expf(x - a.pos_max[row]) / a.pos_sum[row];
-}
 
 __device__ __forceinline__ const char* logit_row(const VerifyArgs& a, int b, int i) {
     const int es = a.ldt == MF_F32 ? 4 : 2;
@@ -263,7 +255,7 @@ __global__ __launch_bounds__(kStatThreads) void row_stats_kernel(VerifyArgs a) {
 // each, into shared memory), then the sequential accept loop (lane 0, double
 // precision). Every workgroup of the row runs this -- it reads (K+1) x chunks
 // statistics and K probabilities -- and the chunk-0 workgroup publishes the
-// result.
+// accepted tokens and the stopping position.
 __device__ void accept_row(const VerifyArgs& a, int b, float* s_max, float* s_sum, int* s_arg, int* s_stop,
                            int* s_reject, bool publish) {
     const int K = a.K;
@@ -291,11 +283,6 @@ __device__ void accept_row(const VerifyArgs& a, int b, float* s_max, float* s_su
         s_max[lane] = gm;
         s_sum[lane] = tot;
         s_arg[lane] = arg;
-        if (publish) {
-            a.pos_max[row] = gm;
-            a.pos_sum[row] = tot;
-            a.pos_arg[row] = arg;
-        }
     }
     // lane i < K fetches candidate i's token, draft and target probabilities
     // and uniform in parallel; lane 0 then walks them in order
@@ -341,76 +328,53 @@ __device__ void accept_row(const VerifyArgs& a, int b, float* s_max, float* s_su
     __syncthreads();
 }
 
-// The draw's vocabulary passes, one (chunk, row) per workgroup:
-//   PASS 0: partial sum of the residual max(p - q, 0) (rows that rejected)
-//   PASS 1: partial sum of the weights w_v (residual / its sum, or p)
-//   PASS 2: partial argmax of (w_v / sum w) / E_v
-// Sums of partials are taken in chunk order, so results do not depend on
-// scheduling.
-template <int PASS, int DT>
-__global__ __launch_bounds__(kPassThreads) void draw_pass_kernel(VerifyArgs a) {
-    __shared__ float shs[kPassThreads / 64];
+// The draw's pass over one (chunk, row): first-index argmaxes of the three
+// candidate families at the stopping position (residual only when the round
+// rejected), and the chunk's "has mass" bits.
+template <int DT>
+__global__ __launch_bounds__(kPassThreads) void draw_kernel(VerifyArgs a) {
+    __shared__ float shv[kPassThreads / 64];
     __shared__ int shi[kPassThreads / 64];
     __shared__ float s_max[kMaxPositions], s_sum[kMaxPositions];
     __shared__ int s_arg[kMaxPositions];
     __shared__ int s_stop, s_reject;
     const int c = blockIdx.x, b = blockIdx.y;
-    const int K = a.K;
-    int i;
-    bool reject;
-    if (PASS == 0) {
-        accept_row(a, b, s_max, s_sum, s_arg, &s_stop, &s_reject, c == 0);
-        i = s_stop;
-        reject = s_reject != 0;
-    } else {
-        i = a.row_stop[b];
-        reject = a.row_reject[b] != 0;
-    }
-    const int prow = b * (K + 1) + i;
-    // pass 0 reads the stop position's statistics from shared memory (the
-    // published copy is not visible until the kernel ends)
+    accept_row(a, b, s_max, s_sum, s_arg, &s_stop, &s_reject, c == 0);
+    const int i = s_stop;
+    const bool reject = s_reject != 0;
+    // the stopping position's softmax statistics, as accept_row combined them
+    // (the draw's candidates only need their order, so the softmax divides
+    // by its sum through one reciprocal; the accept test above used the
+    // reference's exact division)
+    const float inv_sum = 1.f / s_sum[i];
     auto tprob = [&](float raw, int v) -> float {
-        if (PASS != 0) return target_prob(a, prow, raw, v);
         if (a.target_is_probs) return raw;
         if (a.temperature <= 0.f) return v == s_arg[i] ? 1.f : 0.f;
         const float x = a.temperature == 1.f ? raw : raw / a.temperature;
-        return expf(x - s_max[i]) / s_sum[i];
+        return expf(x - s_max[i]) * inv_sum;
     };
     const char* lrow = logit_row(a, b, i);
     const float* q = a.draft_probs + (int64_t)b * a.dp_sr + (int64_t)i * a.dp_sp;
-    const int64_t po = (int64_t)b * a.npass;
-    if (PASS == 0 && !reject) {
-        if (threadIdx.x == 0) a.part_diff[po + c] = 0.f;
-        return;
-    }
-    float diff_sum = 0.f, wsum = 0.f;
-    if (PASS >= 1 && reject)
-        for (int k = 0; k < a.npass; ++k) diff_sum += a.part_diff[po + k];
-    const bool use_diff = reject && diff_sum > 0.f;
-    if (PASS == 2)
-        for (int k = 0; k < a.npass; ++k) wsum += a.part_w[po + k];
-
-    const int base = c * kPassChunk + threadIdx.x * 4;
     const float* Erow = a.noise + (int64_t)b * a.noise_sr;
-    const bool need_q = PASS == 0 || use_diff;
+    const int base = c * kPassChunk + threadIdx.x * 4;
     float x[kPassVec][4], qq[kPassVec][4], en[kPassVec][4];
-    if ((c + 1) * kPassChunk <= a.V && a.vec_logits && (a.vec_q || !need_q) && (a.vec_e || PASS != 2)) {
+    if ((c + 1) * kPassChunk <= a.V && a.vec_logits && (a.vec_q || !reject) && a.vec_e) {
         vload_logits<DT, kPassVec>(lrow, base, kPassThreads * 4, x);
-        if (need_q) vload_floats<kPassVec>(q, base, kPassThreads * 4, qq);
-        if (PASS == 2) vload_floats<kPassVec>(Erow, base, kPassThreads * 4, en);
+        if (reject) vload_floats<kPassVec>(q, base, kPassThreads * 4, qq);
+        vload_floats<kPassVec>(Erow, base, kPassThreads * 4, en);
     } else {
 #pragma unroll
         for (int u = 0; u < kPassVec; ++u) {
             const int e = base + u * kPassThreads * 4;
             logits4(a, lrow, e, x[u]);
-            if (need_q) floats4(q, e, a.V, a.vec_q, qq[u]);
-            if (PASS == 2) floats4(Erow, e, a.V, a.vec_e, en[u]);
+            if (reject) floats4(q, e, a.V, a.vec_q, qq[u]);
+            floats4(Erow, e, a.V, a.vec_e, en[u]);
         }
     }
-    float part = 0.f;
-    float best = -__builtin_huge_valf();
-    int best_i = INT_MAX;
-    const float uniform = 1.f / (float)a.V;
+    const float kNegInf = -__builtin_huge_valf();
+    float best[3] = {kNegInf, kNegInf, kNegInf};
+    int best_i[3] = {INT_MAX, INT_MAX, INT_MAX};
+    int any = 0;
 #pragma unroll
     for (int u = 0; u < kPassVec; ++u)
 #pragma unroll
@@ -418,41 +382,58 @@ __global__ __launch_bounds__(kPassThreads) void draw_pass_kernel(VerifyArgs a) {
             const int e = base + u * kPassThreads * 4 + k;
             if (e >= a.V) continue;
             const float p = tprob(x[u][k], e);
-            if (PASS == 0) {
-                part += fmaxf(p - qq[u][k], 0.f);
-            } else {
-                const float w = use_diff ? fmaxf(p - qq[u][k], 0.f) / diff_sum : fmaxf(p, 0.f);
-                if (PASS == 1) {
-                    part += w;
-                } else {
-                    const float pv = wsum == 0.f ? uniform : w / wsum;
-                    argmax_merge(best, best_i, pv / en[u][k], e);
-                }
+            const float r = 1.f / en[u][k];
+            if (reject) {
+                const float d = fmaxf(p - qq[u][k], 0.f);
+                any |= d > 0.f ? 1 : 0;
+                argmax_merge(best[0], best_i[0], d * r, e);
             }
+            const float w = fmaxf(p, 0.f);
+            any |= w > 0.f ? 2 : 0;
+            argmax_merge(best[1], best_i[1], w * r, e);
+            argmax_merge(best[2], best_i[2], r, e);
         }
-    if (PASS < 2) {
-        const float tot = block_sum<kPassThreads / 64>(part, shs);
-        if (threadIdx.x == 0) (PASS == 0 ? a.part_diff : a.part_w)[po + c] = tot;
-    } else {
-        block_argmax<kPassThreads / 64>(best, best_i, shs, shi);
+    const int64_t po = (int64_t)b * a.npass + c;
+    const int64_t fam = (int64_t)a.B * a.npass;
+#pragma unroll
+    for (int f = 0; f < 3; ++f) {
+        block_argmax<kPassThreads / 64>(best[f], best_i[f], shv, shi);
         if (threadIdx.x == 0) {
-            a.part_best[po + c] = best;
-            a.part_best_i[po + c] = best_i;
+            a.part_best[f * fam + po] = best[f];
+            a.part_best_i[f * fam + po] = best_i[f];
         }
+    }
+    // OR of the lanes' bits, through the argmax scratch
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) any |= __shfl_xor(any, off, 64);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) shi[threadIdx.x >> 6] = any;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int t = 0;
+#pragma unroll
+        for (int w = 0; w < kPassThreads / 64; ++w) t |= shi[w];
+        a.part_any[po] = t;
     }
 }
 
 // Combine each row's chunk winners (a kernel boundary, not a per-workgroup
 // release fence: on this multi-XCD part a device-scope fence writes back L2).
+// The family is the reference's branch: the residual when the round rejected
+// and the residual has mass, else the target row, else uniform.
 __global__ __launch_bounds__(64) void finish_kernel(VerifyArgs a) {
     const int b = blockIdx.x * 64 + threadIdx.x;
     if (b >= a.B) return;
     const int K = a.K;
     const int i = a.row_stop[b];
     const int64_t po = (int64_t)b * a.npass;
+    int any = 0;
+    for (int k = 0; k < a.npass; ++k) any |= a.part_any[po + k];
+    const int f = (a.row_reject[b] && (any & 1)) ? 0 : ((any & 2) ? 1 : 2);
+    const int64_t fo = (int64_t)f * a.B * a.npass + po;
     float best = -__builtin_huge_valf();
     int best_i = INT_MAX;
-    for (int k = 0; k < a.npass; ++k) argmax_merge(best, best_i, a.part_best[po + k], a.part_best_i[po + k]);
+    for (int k = 0; k < a.npass; ++k) argmax_merge(best, best_i, a.part_best[fo + k], a.part_best_i[fo + k]);
     a.out_tokens[(int64_t)b * (K + 1) + i] = best_i;
     a.out_is_draft[(int64_t)b * (K + 1) + i] = 0;
     a.out_count[b] = i + 1;
@@ -469,7 +450,7 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 namespace {
 struct Layout {
-    int64_t st, pos, rows, pass;  // float/int slots of each section
+    int64_t st, rows, pass;  // float/int slots of each section
     int64_t total_bytes;
 };
 inline Layout layout_for(int64_t num_rows, int num_draft) {
@@ -477,10 +458,9 @@ inline Layout layout_for(int64_t num_rows, int num_draft) {
     const int64_t rows = num_rows * (num_draft + 1);
     Layout l;
     l.st = rows * mf::chunks_for(1 << 20);
-    l.pos = rows;
     l.rows = num_rows;
     l.pass = num_rows * mf::pass_chunks_for(1 << 20);
-    l.total_bytes = (3 * l.st + 3 * l.pos + 2 * l.rows + 4 * l.pass) * 4 + 256;
+    l.total_bytes = (3 * l.st + 2 * l.rows + 7 * l.pass) * 4 + 256;
     return l;
 }
 }  // namespace
@@ -525,20 +505,16 @@ extern "C" int mf_spec_verify(int num_rows, int num_draft, int vocab, const int3
     float* st_max = take(l.st);
     float* st_sum = take(l.st);
     int32_t* st_arg = (int32_t*)take(l.st);
-    float* pos_max = take(l.pos);
-    float* pos_sum = take(l.pos);
-    int32_t* pos_arg = (int32_t*)take(l.pos);
     int32_t* row_stop = (int32_t*)take(l.rows);
     int32_t* row_reject = (int32_t*)take(l.rows);
-    float* part_diff = take(l.pass);
-    float* part_w = take(l.pass);
-    float* part_best = take(l.pass);
-    int32_t* part_best_i = (int32_t*)take(l.pass);
+    float* part_best = take(3 * l.pass);
+    int32_t* part_best_i = (int32_t*)take(3 * l.pass);
+    int32_t* part_any = (int32_t*)take(l.pass);
     VerifyArgs a{num_rows, num_draft, vocab, draft_tokens, draft_probs, dp_stride_row, dp_stride_pos,
                  (const char*)target_logits, target_dtype, tl_stride_row, tl_stride_pos, temperature,
                  target_is_probs, u_accept, exp_noise, noise_stride_row, out_tokens, out_is_draft, out_count,
-                 out_num_accepted, nchunk, st_max, st_sum, st_arg, pos_max, pos_sum, pos_arg, row_stop,
-                 row_reject, npass, part_diff, part_w, part_best, part_best_i,
+                 out_num_accepted, nchunk, st_max, st_sum, st_arg, row_stop,
+                 row_reject, npass, part_best, part_best_i, part_any,
                  vec_logits ? 1 : 0, vec_q ? 1 : 0, vec_e ? 1 : 0};
     hipStream_t st = (hipStream_t)stream;
     auto run = [&](auto dt_tag) -> int {
@@ -549,11 +525,7 @@ extern "C" int mf_spec_verify(int num_rows, int num_draft, int vocab, const int3
             if (int e = check_launch()) return e;
         }
         const dim3 grid((unsigned)npass, (unsigned)num_rows);
-        hipLaunchKernelGGL((draw_pass_kernel<0, DT>), grid, dim3(kPassThreads), 0, st, a);
-        if (int e = check_launch()) return e;
-        hipLaunchKernelGGL((draw_pass_kernel<1, DT>), grid, dim3(kPassThreads), 0, st, a);
-        if (int e = check_launch()) return e;
-        hipLaunchKernelGGL((draw_pass_kernel<2, DT>), grid, dim3(kPassThreads), 0, st, a);
+        hipLaunchKernelGGL((draw_kernel<DT>), grid, dim3(kPassThreads), 0, st, a);
         if (int e = check_launch()) return e;
         hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((num_rows + 63) / 64)), dim3(64), 0, st, a);
         return check_launch();

@@ -93,3 +93,39 @@ def test_greedy_known_answers(device):
     noise = torch.empty((B, V)).exponential_(1.0, generator=gen)
     count, nacc = _run_both(device, draft, target, tokens, u, noise, 0.0)
     assert nacc.tolist() == [4, 2, 0] and count.tolist() == [5, 3, 1]
+
+
+def test_draw_families_residual_target_uniform(device):
+    """The three branches of the final draw, on target probabilities given as
+    such: a rejection whose residual max(p - q, 0) has mass draws from it; a
+    rejection where the target equals the draft (no residual mass) draws from
+    the target; a bonus position with no target mass draws uniformly (the
+    smallest Exp(1) draw wins). Checked against the oracle's restatement."""
+    B, K, V = 3, 2, 4000
+    gen = torch.Generator().manual_seed(5)
+    draft = torch.softmax(torch.randn((B, K, V), generator=gen) * 2.0, dim=-1)
+    target = torch.softmax(torch.randn((B, K + 1, V), generator=gen) * 2.0, dim=-1)
+    tokens = torch.stack([torch.multinomial(draft[b], 1, generator=gen).view(-1) for b in range(B)]).to(torch.int32)
+    u = torch.rand((B, K), generator=gen)
+    # row 0: reject at once (u = 1 > any ratio below 1), residual has mass
+    u[0, 0] = 1.0
+    target[0, 0, int(tokens[0, 0])] = 0.5 * float(draft[0, 0, int(tokens[0, 0])])
+    # row 1: target equals the draft at position 0, rejected by u = 1 since
+    # p / (q + 1e-9) < 1: the residual is zero everywhere
+    target[1, 0] = draft[1, 0]
+    u[1, 0] = 1.0
+    # row 2: both candidates accepted (u = 0), bonus position has no mass
+    u[2] = 0.0
+    target[2, K] = 0.0
+    noise = torch.empty((B, V)).exponential_(1.0, generator=gen)
+    res = nat.spec_verify(tokens.to(device), draft.to(device), target.to(device), 1.0, u.to(device),
+                          noise.to(device), target_is_probs=True)
+    tok = res.tokens.cpu().numpy()
+    cnt = res.count.cpu().numpy()
+    for b in range(B):
+        want, flags, nacc = orj.verify_tokens(tokens[b].tolist(), [draft[b, i].numpy() for i in range(K)],
+                                              [target[b, i].numpy() for i in range(K + 1)], u[b].tolist(),
+                                              noise[b].numpy())
+        assert tok[b, :cnt[b]].tolist() == want, f"row {b}"
+    assert cnt.tolist() == [1, 1, 3]
+    assert int(tok[2, 2]) == int(torch.argmin(noise[2]))
