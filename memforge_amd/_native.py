@@ -25,6 +25,9 @@ DTYPE_CODES = {torch.float32: MF_F32, torch.float16: MF_F16, torch.bfloat16: MF_
 
 PLAN_ITEM_INTS = 12
 PLAN_MERGE_INTS = 8
+# 16-key tiles one wave of a plan may cover (MF_MAX_ITEM_TILES in
+# paged_attention.hip); a cooperative unit of four waves covers four times that
+MAX_ITEM_TILES = 128
 ENTRY_INTS = 6
 
 PACK_TABLE_OVERFLOW = 1

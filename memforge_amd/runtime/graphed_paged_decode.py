@@ -11,11 +11,14 @@ kernel reading the pool in place -- so nothing is gathered or padded by
 context length.
 
 What makes the attention capturable is mf_paged_attention_counted: its grids
-are sized by a capacity fixed at capture time (every sequence at the longest
-reachable context, split into the smallest partitions the planner uses), and
-the live item and merge counts are read from device memory, so each step's
-plan -- made on the host from that step's context lengths -- is swapped in
-by a copy before the replay.
+are sized by a capacity fixed at capture time, and the live item and merge
+counts are read from device memory, so each step's plan -- made on the host
+from that step's context lengths -- is swapped in by a copy before the
+replay. When the longest reachable context fits one cooperative unit (four
+waves of 128 key tiles), every step's plan is made merge-free -- at most four
+items per (sequence, kv head), no split-K partials -- and the graph holds no
+merge launch at all; otherwise the capacity is every sequence at the longest
+context split into the smallest partitions the planner uses.
 
 Batches are bucketed to powers of two. Padding rows are empty entries (no
 keys, slot -1): they write nothing and attend to nothing, and their logits
@@ -52,12 +55,17 @@ class _Bucket:
         self.host = torch.zeros(self.inputs.numel(), dtype=torch.int32).pin_memory()
         self.packed = nat.PackedStep.allocate(b, b, mb, dev)
         hkv = owner.pool.spec.num_kv_heads
-        # a (sequence, kv head) of T tiles is one item when T <= P, else four
-        # per unit of at most 4P tiles (P >= _MIN_PARTITION_TILES), and the
-        # single items are padded to whole workgroups
-        cap_items = b * hkv * (math.ceil(mb / _MIN_PARTITION_TILES) + 4) + 4
-        floats = cap_items * 16 * (max(owner.pool.spec.head_dim, 32) + 2)
-        self.plan = nat.CountedPlan(cap_items, 0, b * hkv, floats, dev)
+        if owner.merge_free:
+            # one single item or one four-wave unit per (sequence, kv head),
+            # the single items padded to whole workgroups; nothing to merge
+            self.plan = nat.CountedPlan(4 * b * hkv + 4, 0, 0, 0, dev)
+        else:
+            # a (sequence, kv head) of T tiles is one item when T <= P, else
+            # four per unit of at most 4P tiles (P >= _MIN_PARTITION_TILES),
+            # and the single items are padded to whole workgroups
+            cap_items = b * hkv * (math.ceil(mb / _MIN_PARTITION_TILES) + 4) + 4
+            floats = cap_items * 16 * (max(owner.pool.spec.head_dim, 32) + 2)
+            self.plan = nat.CountedPlan(cap_items, 0, b * hkv, floats, dev)
         self.keep = torch.arange(b, dtype=torch.long, device=dev)
         meta = {"block_tables": self.packed.block_tables, "cu_seqlens": self.packed.cu_seqlens,
                 "kv_lens": self.packed.kv_lens, "positions": self.packed.positions, "row_map": None,
@@ -92,6 +100,9 @@ class GraphedPagedDecoder:
         self.max_batch = max(1, int(max_batch))
         # room for the longest context plus a speculative lookahead block
         self.max_blocks = (max_model_len + self.bs - 1) // self.bs + 1
+        # every reachable context (in 16-key tiles) fits one cooperative unit:
+        # plans can always be merge-free, and the graph needs no merge launch
+        self.merge_free = (self.max_blocks * self.bs + 15) // 16 <= 4 * nat.MAX_ITEM_TILES
         self.num_q_heads = hq
         self._mem_pool = torch.cuda.graph_pool_handle()
         self._buckets: Dict[int, _Bucket] = {}
@@ -163,9 +174,17 @@ class GraphedPagedDecoder:
         bk.copied = torch.cuda.Event()
         bk.copied.record()
         kv = [int(c) + 1 for c in ctx_lens] + [0] * (b - n)
-        items, merges, counts = nat.plan_attention_host(list(range(b + 1)), kv, self.num_q_heads,
-                                                        self.pool.spec.num_kv_heads, self.pool.spec.head_dim,
-                                                        self.pool.key_pool.dtype)
+        plan_args = (list(range(b + 1)), kv, self.num_q_heads, self.pool.spec.num_kv_heads,
+                     self.pool.spec.head_dim, self.pool.key_pool.dtype)
+        items, merges, counts = nat.plan_attention_host(*plan_args)
+        if self.merge_free and counts[2] > 0:
+            # the planner's pick splits a range: take the smallest partition
+            # whose units hold the longest context whole instead
+            longest = (max(kv) + 15) // 16
+            part = _MIN_PARTITION_TILES
+            while 4 * part < longest:
+                part *= 2
+            items, merges, counts = nat.plan_attention_host(*plan_args, partition_tiles=part)
         bk.plan.update(items, merges, counts)
 
     def bucket(self, n: int) -> _Bucket:

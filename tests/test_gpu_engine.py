@@ -310,6 +310,50 @@ def test_graphed_decoder_step_equals_the_eager_packed_pass(model, device):
     assert dec.captures == 2 and dec.replays == 6
 
 
+@pytest.mark.parametrize("max_model_len", [6600, 9000])
+def test_graphed_decoder_long_context(model, device, max_model_len):
+    """A 6,400-token context next to short ones. Up to 8,192 reachable tokens
+    the decoder plans merge-free steps (here the planner's own pick would
+    split the long range, so the step is replanned with 128-tile waves) and
+    captures no merge launch; beyond that the graph keeps the merge launch and
+    the step runs split-K. Both against the eager varlen pass."""
+    from memforge_amd import _native as nat
+    from memforge_amd.kernels import attention_backend
+    from memforge_amd.runtime.graphed_paged_decode import GraphedPagedDecoder
+    from memforge_amd.runtime.kv_pool import ModelKVSpec, PagedKVPool
+    from memforge_amd.runtime.varlen_cache import VarlenPackedCache
+
+    spec = ModelKVSpec.from_config(model.config, torch.float32, "cuda:0")
+    pool = PagedKVPool(spec, num_blocks=440, block_size=16)
+    gen = torch.Generator().manual_seed(9)
+    pool.key_pool.copy_(torch.randn(pool.key_pool.shape, generator=gen).to(device))
+    pool.value_pool.copy_(torch.randn(pool.value_pool.shape, generator=gen).to(device))
+    dec = GraphedPagedDecoder(model, pool, max_batch=4, max_model_len=max_model_len)
+    assert dec.merge_free == (max_model_len <= 8176)
+    perm = torch.randperm(440, generator=gen).tolist()
+    tables = [perm[:402], perm[402:412], perm[412:420]]
+    ctx = [6400, 150, 99]
+    toks = [5, 17, 33]
+    hkv, d = spec.num_kv_heads, spec.head_dim
+    kv = [c + 1 for c in ctx] + [0]
+    auto_merges = int(nat.plan_attention_host(list(range(5)), kv, model.config.num_attention_heads, hkv, d,
+                                              torch.float32)[2][2])
+    assert auto_merges > 0, "want a step whose own plan splits the long range"
+    want_k, want_v = pool.key_pool.clone(), pool.value_pool.clone()
+    got = dec.step(toks, ctx, tables)
+    assert (dec._buckets[4].plan.cap_merges == 0) == dec.merge_free
+    pool.key_pool.copy_(want_k)
+    pool.value_pool.copy_(want_v)
+    cache = VarlenPackedCache(pool, 2, [torch.tensor(t) for t in tables], [0, 1, 2], ctx)
+    with attention_backend.backend_enabled_on(model):
+        with attention_backend.varlen_attention_context(pool, [torch.tensor(t) for t in tables], [0, 1, 2], ctx):
+            with torch.no_grad():
+                ref = model(input_ids=torch.tensor([toks], device=device),
+                            position_ids=torch.tensor([ctx], device=device), past_key_values=cache,
+                            use_cache=True).logits[0]
+    torch.testing.assert_close(got, ref, atol=2e-5, rtol=1e-4)
+
+
 def test_graphed_engine_output_equals_eager(model, tok):
     prompts = PROMPTS + ["five", "a sixth prompt that is rather long indeed, for padding"]
     eager = make_engine(model, tok, num_blocks=128, max_num_seqs=8)
