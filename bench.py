@@ -160,6 +160,34 @@ def _tables_for(kv_lens, gen):
     return tables, sum(nblk)
 
 
+def _graph_us(fn, layers, reps=10):
+    """Per-layer GPU time of ``fn(i)`` for i < layers, captured once in a HIP
+    graph and replayed: the launches run back to back, so the figure excludes
+    the host's submission time that per-call events include at these sizes."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(layers):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(layers):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    evs = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        evs.append((a, b))
+    torch.cuda.synchronize()
+    return float(np.median([a.elapsed_time(b) for a, b in evs])) * 1e3 / layers
+
+
 def _event_us(pairs):
     return float(np.mean([a.elapsed_time(b) for a, b in pairs])) * 1e3
 
@@ -326,6 +354,7 @@ def run_c2(dev, layers=SM_LAYERS, reps=3):
     dec_us = _event_us([(e[1], e[2]) for e in evs])
     pre_us = _event_us([(e[2], e[3]) for e in evs])
     mrg_us = _event_us([(e[3], e[4]) for e in evs])
+    graph_layer_us = _graph_us(layer, layers)
     kvb = SM_HKV * SM_D * 2 * 2  # K+V bytes per token per layer
     write_bytes = T * kvb * 2 + T * 8  # read new rows, write pool rows, read slots
     dec_bytes = sum(dctx) * kvb + 28 * SM_HQ * SM_D * 2 * 2
@@ -346,6 +375,9 @@ def run_c2(dev, layers=SM_LAYERS, reps=3):
         "merge_us": round(mrg_us, 2),
         "plan": {"narrow": plan.n_narrow, "wide": plan.n_wide, "merges": plan.n_merges},
         "step_attn_us": round(dec_us + pre_us + mrg_us, 2),
+        "graph_layer_us": round(graph_layer_us, 2),
+        "graph_note": "one layer's KV write + decode items + prefill items + merge, replayed as a captured "
+                      "graph of all layers (no host submission time)",
     }
 
 
@@ -443,6 +475,7 @@ def run_c3(dev, layers=SM_LAYERS, reps=3):
             evs.append((a, b))
     torch.cuda.synchronize()
     attn_us = _event_us(evs)
+    graph_attn_us = _graph_us(layer, layers)
     kvb = SM_HKV * SM_D * 2 * 2
     attn_bytes = sum(c + K + 1 for c in ctx) * kvb + T * SM_HQ * SM_D * 2 * 2
     attn_flops = sum(4 * SM_HQ * SM_D * (c + j + 1) for c in ctx for j in range(K + 1))
@@ -469,6 +502,8 @@ def run_c3(dev, layers=SM_LAYERS, reps=3):
         "verify_attn_gbps": round(attn_bytes / attn_us / 1e3, 1),
         "verify_attn_frac": round(attn_bytes / attn_us / 1e3 / HBM_PEAK_GBPS, 4),
         "verify_attn_tflops": round(attn_flops / attn_us / 1e6, 2),
+        "graph_verify_attn_us": round(graph_attn_us, 2),
+        "graph_verify_attn_gbps": round(attn_bytes / graph_attn_us / 1e3, 1),
         "rejection_us": round(ver_us, 2),
         "rejection_gbps": round(ver_bytes / ver_us / 1e3, 1),
         "accepted_per_row": res.num_accepted.cpu().tolist(),

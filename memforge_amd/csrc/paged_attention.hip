@@ -1190,13 +1190,14 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     // chain of tiles, plus the merge launch if any range is split. A range of
     // T > q tiles runs as ceil(T / 4q) units of four waves. Ties go to the
     // longer partition. The constants are fitted to partition sweeps on
-    // MI355X (bf16, D 64): a lone wave's chain costs about 0.45 us per 16-key
-    // tile, decode items stream near 5 TB/s, and a split costs about 10 us of
-    // merge launch. On a 64-sequence decode step of 96-1152 keys this picks
-    // merge-free 32-tile partitions (19.1 us against 21.1 us at 4 tiles), on
-    // C3's verify and C2's decodes 32 as well, and 128 on C5.
+    // MI355X (bf16, D 64) timed as HIP-graph replays, i.e. without host
+    // submission time: a lone wave's chain costs about 0.53 us per 16-key
+    // tile, decode items stream near 5 TB/s, and a split costs about 9 us of
+    // merge. Picks: merge-free 32-tile waves for a 64-sequence decode step of
+    // 96-1152 keys (17.0 us against 18.5 at 4 tiles), 8 for C3's verify (16.8
+    // against 18.5 merge-free at 32), 16 for C2's decodes, 128 on C5.
     auto narrow_partition = [&](int fallback) {
-        constexpr double kChainUs = 0.45, kMergeUs = 10.0, kBytesPerUs = 5.0e6;
+        constexpr double kChainUs = 0.53, kMergeUs = 9.0, kBytesPerUs = 5.0e6;
         const double tile_us = 16.0 * DP * mf::dtype_size(dtype) * 2 / kBytesPerUs;
         int64_t tiles_all = 0;
         for (int s = 0; s < num_seqs; ++s) {
