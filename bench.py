@@ -269,10 +269,12 @@ def run_c1(dev, reps=50):
         torch.cuda.synchronize()
         times[name] = _event_us(ev)
     kv_bytes = sum(ctx) * SM_HKV * SM_D * 4 * 2
+    graph_us = _graph_us(lambda i: varlen(), 16)
     return {
         "workload": "C1: SmolLM2 decode, fp32, 8 sequences, ctx U[17,512], 15q/5kv, D 64, pool 1024x16 "
                     "random placement, scale 1/8",
         "varlen_launch_us": round(times["varlen"], 2),
+        "graph_varlen_launch_us": round(graph_us, 2),
         "operator_8_calls_us": round(times["operator"], 2),
         "max_abs_err_varlen": err_varlen,
         "max_abs_err_operator": err_op,
