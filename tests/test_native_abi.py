@@ -257,3 +257,39 @@ def test_upload_packs_parts_with_their_dtypes_and_shapes():
     assert all(o % 2 == 0 for o in offs) and n >= offs[-1] + 2
     with pytest.raises(TypeError):
         nat.upload([np.zeros(3, np.float32)], "cpu")
+
+
+def _partition_of(items):
+    """Tiles per wave the plan used: the longest single-wave item, or a
+    cooperative unit's range / 4, rounded up to the planner's powers of two."""
+    longest = 0
+    for u in range(0, items.shape[0], 4):
+        unit = items[u:u + 4]
+        if int(unit[0][11]) == 1:
+            longest = max(longest, -(-int(unit[3][5] - unit[0][4]) // 4))
+        else:
+            longest = max(longest, int((unit[:, 5] - unit[:, 4]).max()))
+    return longest
+
+
+def test_planner_partition_picks_on_the_config_shapes():
+    """The narrow-partition estimate (bandwidth time or longest chain, plus a
+    merge when a range is split) on the configs' decode shapes: merge-free
+    on a 64-sequence decode step at C4's contexts, 8-tile waves on C3's verify
+    rows, 128-tile waves (and only the longest sequences split) on C5."""
+    import math
+
+    g = torch.Generator().manual_seed(5)
+    c4 = torch.randint(96, 1153, (64,), generator=g).tolist()
+    p = _plan(list(range(65)), c4, hq=15, hkv=5, d=64)
+    assert p.n_merges == 0 and 16 < _partition_of(p.items_host[: p.n_narrow]) <= 32
+    g = torch.Generator().manual_seed(0)
+    ctx = [c + 5 for c in torch.randint(128, 2049, (16,), generator=g).tolist()]
+    p = _plan([5 * i for i in range(17)], ctx, hq=15, hkv=5, d=64)
+    assert p.n_merges > 0 and _partition_of(p.items_host[: p.n_narrow]) <= 8
+    gen = torch.Generator().manual_seed(0)
+    z = torch.randn(256, generator=gen, dtype=torch.float64)
+    c5 = torch.clamp(torch.round(torch.exp(math.log(2048.0) + z)), 64, 32768).to(torch.int64).tolist()
+    p = _plan(list(range(257)), c5, hq=40, hkv=8, d=128)
+    long_seqs = sum(1 for c in c5 if (c + 15) // 16 > 512)
+    assert p.n_merges == 8 * long_seqs and _partition_of(p.items_host[: p.n_narrow]) == 128
