@@ -164,7 +164,10 @@ int mf_ragged_pack(const int32_t* entries, int num_entries,
  * merge_counters (device int32[num_merges], all-zero on entry and again on
  * exit) lets the attention kernel merge split-K partitions itself: the last
  * partition of a group to finish merges it. With merge_counters NULL a
- * separate merge kernel runs after the attention kernel. Passing the plan's
+ * separate merge kernel runs after the attention kernel. A plan holding both
+ * single-tile (decode) and wide (prefill) items runs them in one launch when
+ * block_size is 16 and head_dim is one of the kernel's sizes, 16-bit dtypes
+ * only. Passing the plan's
  * items with num_merges = 0, then a second call with no items and only the
  * merges, runs the unfused work in two launches (to time them apart).
  * Concurrent calls must not share partials or merge_counters.

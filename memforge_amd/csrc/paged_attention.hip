@@ -319,13 +319,20 @@ constexpr int attn_waves_per_eu() {
 // (bf16 D 64): four and six buffers were no faster than three, and eight
 // slower (they cost waves per SIMD); a 256-byte row's buffer is 32 registers,
 // and three fit the two-waves-per-SIMD budget.
+// One launch for plans holding both single-tile and wide items (see
+// attn_mixed_kernel); 0 launches them one after the other.
+#ifndef MF_MIXED_LAUNCH
+#define MF_MIXED_LAUNCH 1
+#endif
+
 #ifndef MF_NARROW_DEPTH
 #define MF_NARROW_DEPTH 3
 #endif
 
+// The body of one workgroup of the attention kernel: `block` is its index
+// among the workgroups that run items of this column-tile width.
 template <int DT, int DP, int NT, bool FAST>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<DT, DP, NT>())))
-void attn_kernel(AttnArgs a) {
+__device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     constexpr int ES = DT == MF_F32 ? 4 : 2;
     constexpr int EPL = 16 / ES;      // elements per 16-byte chunk
     constexpr int NL = DP * ES / 64;  // 16-byte K/Q chunks per lane
@@ -336,7 +343,7 @@ void attn_kernel(AttnArgs a) {
     constexpr float kNegInf = -__builtin_huge_valf();
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int item = blockIdx.x * kWaves + wave;
+    const int item = block * kWaves + wave;
     const int num_items = a.dev_count ? *a.dev_count : a.num_items;
     if (item >= num_items) return;
     const int lane = threadIdx.x & 63;
@@ -721,8 +728,8 @@ void attn_kernel(AttnArgs a) {
     // conflict-free. One barrier per stage.
     bool wg_shared = false;
     if constexpr (FAST && DT != MF_F32 && NT > 1) {
-        if ((int)(blockIdx.x + 1) * kWaves <= num_items) {
-            const int32_t* i0 = a.items + (int64_t)blockIdx.x * kWaves * MF_PLAN_ITEM_INTS;
+        if ((block + 1) * kWaves <= num_items) {
+            const int32_t* i0 = a.items + (int64_t)block * kWaves * MF_PLAN_ITEM_INTS;
             wg_shared = true;
 #pragma unroll
             for (int w = 1; w < kWaves; ++w) {
@@ -1050,6 +1057,33 @@ void attn_kernel(AttnArgs a) {
     }
 }
 
+template <int DT, int DP, int NT, bool FAST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<DT, DP, NT>())))
+void attn_kernel(AttnArgs a) {
+    attn_body<DT, DP, NT, FAST>(a, blockIdx.x);
+}
+
+// Single-tile and wide items of one plan in one launch: the first
+// workgroups run the single-tile items (decode rows: chains of dependent
+// loads, latency-bound), the last `wide_blocks` the wide ones (prefill rows:
+// MFMA and softmax work), which fill the slots the single-tile workgroups
+// leave and overlap their load latency. Two back-to-back launches would leave
+// the chip half idle for the length of the shorter one. Measured on the C2
+// step (bf16, D 64, 382 single-tile and 900 wide workgroups): 67.9 us per
+// layer as two launches, 62.7 us with the wide workgroups first, 58.6 us with
+// the single-tile ones first. Each workgroup is entirely one kind, so the
+// barriers of either body stay workgroup-uniform.
+template <int DT, int DP, int NTW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
+    attn_waves_per_eu<DT, DP, NTW>() < attn_waves_per_eu<DT, DP, 1>() ? attn_waves_per_eu<DT, DP, NTW>()
+                                                                      : attn_waves_per_eu<DT, DP, 1>())))
+void attn_mixed_kernel(AttnArgs narrow, AttnArgs wide, int wide_blocks) {
+    const int b = blockIdx.x;
+    const int narrow_blocks = (int)gridDim.x - wide_blocks;
+    if (b < narrow_blocks) attn_body<DT, DP, 1, true>(narrow, b);
+    else attn_body<DT, DP, NTW, true>(wide, b - narrow_blocks);
+}
+
 // --------------------------------------------------------------- merge kernel
 // One workgroup per merge record: wave w merges partitions w, w+4, ... and the
 // four partial results are combined through LDS by wave 0.
@@ -1108,6 +1142,26 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
     // With arrival counters the attention kernel merges its own partitions;
     // a merges-only call (no items) still runs the separate merge kernel.
     const bool fused = a.counters != nullptr && (n_narrow + n_wide) > 0;
+    constexpr int NTW = wide_tiles(DT, DP);
+#if MF_MIXED_LAUNCH
+    if constexpr (NTW > 1 && DT != MF_F32) {
+        if (fast && n_narrow > 0 && n_wide > 0) {
+            AttnArgs an = a, aw = a;
+            an.items = items;
+            an.num_items = (int)n_narrow;
+            an.dev_count = dev_counts ? dev_counts + 0 : nullptr;
+            aw.items = items + n_narrow * MF_PLAN_ITEM_INTS;
+            aw.num_items = (int)n_wide;
+            aw.dev_count = dev_counts ? dev_counts + 1 : nullptr;
+            const int64_t wide_blocks = (n_wide + kWaves - 1) / kWaves;
+            const dim3 grid((unsigned)(wide_blocks + (n_narrow + kWaves - 1) / kWaves));
+            hipLaunchKernelGGL((attn_mixed_kernel<DT, DP, NTW>), grid, dim3(256), 0, stream, an, aw,
+                               (int)wide_blocks);
+            if (int st = check_launch()) return st;
+            n_narrow = n_wide = 0;
+        }
+    }
+#endif
     if (n_narrow > 0) {
         a.items = items;
         a.num_items = (int)n_narrow;
@@ -1117,7 +1171,6 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
         else hipLaunchKernelGGL((attn_kernel<DT, DP, 1, false>), grid, dim3(256), 0, stream, a);
         if (int st = check_launch()) return st;
     }
-    constexpr int NTW = wide_tiles(DT, DP);
     if constexpr (NTW > 1) {
         if (n_wide > 0) {
             a.items = items + n_narrow * MF_PLAN_ITEM_INTS;
