@@ -5,7 +5,7 @@
 // chunks, one 256-thread workgroup per (row, chunk), every element loaded once
 // into registers with 16-byte vector loads; the workgroup writes its chunk's
 // max, sum of exp(x - max) and first argmax of the raw logits.
-// Launch 2 (one workgroup per (row, 4096-element chunk)): combines the chunk
+// Launch 2 (one workgroup per (row, 2048-element chunk)): combines the chunk
 // statistics of the row's K+1 target positions, runs the sequential accept
 // loop over the K candidates in one lane, in double precision, exactly the
 // reference's arithmetic, and takes one pass over its chunk of the stopping
@@ -19,6 +19,12 @@
 // argmaxes -- of max(p - q, 0) / E, of max(p, 0) / E and of 1 / E -- and
 // whether any residual or target value is positive. Launch 3 picks the family
 // the reference's branches would take and combines the chunk winners.
+// At this size the three launches are bound by dependent memory round trips,
+// not bytes: the accept walk takes two (tokens with statistics, then the
+// candidates' probabilities) and the draw one more. Fetching every
+// position's chunk during the walk instead was measured slower on MI355X
+// (C3: draw 13.9 us against 10.4 us; the extra rows cost more than the round
+// trip they save).
 // (memforge_ml/speculative/rejection_sampler.py:12-83,
 //  memforge_ml/runtime/batched_speculative.py:112-124, 731-777)
 #include <cfloat>
@@ -34,9 +40,10 @@ constexpr int kStatThreads = 256;
 constexpr int kStatVec = 8;                             // float4 groups per thread per chunk
 constexpr int kChunk = kStatThreads * 4 * kStatVec;    // elements per statistics workgroup
 constexpr int kPassThreads = 256;
-constexpr int kPassVec = 4;                             // float4 groups per thread per pass chunk
+constexpr int kPassVec = 2;                             // float4 groups per thread per pass chunk
 constexpr int kPassChunk = kPassThreads * 4 * kPassVec;  // elements per draw-pass workgroup
 constexpr int kMaxPositions = 64;                       // K + 1 target positions per row
+constexpr int kStatBatch = 8;                           // chunk statistics loaded per round trip
 
 struct VerifyArgs {
     int B, K, V;
@@ -77,6 +84,14 @@ __device__ __forceinline__ float logit_at(const VerifyArgs& a, const char* row, 
     if (a.ldt == MF_F32) return ((const float*)row)[v];
     const uint32_t bits = ((const uint16_t*)row)[v];
     return a.ldt == MF_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
+}
+
+template <int DT>
+__device__ __forceinline__ float logit_at_t(const VerifyArgs& a, int b, int i, int v) {
+    constexpr int ES = DT == MF_F32 ? 4 : 2;
+    const char* row = a.logits + ((int64_t)b * a.tl_sr + (int64_t)i * a.tl_sp) * ES;
+    if constexpr (DT == MF_F32) return ((const float*)row)[v];
+    else return bits_to_f32<DT>(((const uint16_t*)row)[v]);
 }
 
 // Four consecutive logits starting at e (e % 4 == 0); elements >= V read as 0
@@ -144,7 +159,9 @@ __device__ __forceinline__ void vload_floats(const float* row, int e0, int strid
 
 // Max with the first index among equal maxima; NaN never wins.
 __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
-    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+    const bool take = ov > v || (ov == v && oi < i);  // selects, not a branch
+    v = take ? ov : v;
+    i = take ? oi : i;
 }
 
 template <int NW>
@@ -247,73 +264,119 @@ __global__ __launch_bounds__(kStatThreads) void row_stats_kernel(VerifyArgs a) {
             a.st_max[(int64_t)row * a.nchunk + c] = gm;
             a.st_sum[(int64_t)row * a.nchunk + c] = tot;
         }
+    } else if (threadIdx.x == 0) {
+        // greedy: the chunk's largest raw logit, so the row's argmax combines
+        // from the statistics alone
+        a.st_max[(int64_t)row * a.nchunk + c] = am;
     }
     if (threadIdx.x == 0) a.st_arg[(int64_t)row * a.nchunk + c] = ai;
 }
 
-// Combined softmax statistics of the row's K+1 target positions (one lane
-// each, into shared memory), then the sequential accept loop (lane 0, double
-// precision). Every workgroup of the row runs this -- it reads (K+1) x chunks
-// statistics and K probabilities -- and the chunk-0 workgroup publishes the
-// accepted tokens and the stopping position.
-__device__ void accept_row(const VerifyArgs& a, int b, float* s_max, float* s_sum, int* s_arg, int* s_stop,
-                           int* s_reject, bool publish) {
+// Combined softmax statistics of the row's K+1 target positions (lane i
+// combines position i's chunks), then the sequential accept loop (lane 0,
+// double precision). Every workgroup of the row runs this -- it reads
+// (K+1) x chunks statistics and K probabilities -- and the chunk-0 workgroup
+// publishes the accepted tokens and the stopping position.
+//
+// Two round trips: the candidate tokens, uniforms and the first kStatBatch
+// chunk statistics go out together; the candidates' draft and target
+// probabilities follow once the tokens are in. Every lane issues the loads,
+// at clamped positions (a lane past the last candidate or position repeats
+// the last one; with no draft the candidate loads read stand-in buffers and
+// are ignored), so none sits behind a branch: the compiler's wait counts are
+// only exact for loads on every path.
+template <int DT>
+__device__ __forceinline__ void accept_row(const VerifyArgs& a, int b, float* s_max, float* s_sum, int* s_arg,
+                                           int* s_stop, int* s_reject, bool publish) {
     const int K = a.K;
     const float T = a.temperature;
     const float kNegInf = -__builtin_huge_valf();
     const int lane = threadIdx.x;
-    if (!a.target_is_probs && lane < K + 1) {
-        const int row = b * (K + 1) + lane;
-        const int64_t o = (int64_t)row * a.nchunk;
-        const char* lrow = logit_row(a, b, lane);
-        float gm = kNegInf, v = kNegInf;
-        int arg = INT_MAX;
-        for (int c = 0; c < a.nchunk; ++c) {
-            if (T > 0.f) gm = fmaxf(gm, a.st_max[o + c]);
-            const int ci = a.st_arg[o + c];
-            if (ci != INT_MAX) argmax_merge(v, arg, logit_at(a, lrow, ci), ci);
+    const bool cand = lane < K;
+    const bool stat = !a.target_is_probs && lane < K + 1;
+    const int lk = min(lane, max(K - 1, 0));
+    const int tok = a.draft_tokens[(int64_t)b * K + lk];
+    const float u = a.u_accept[(int64_t)b * K + lk];
+    const int64_t o = (int64_t)(b * (K + 1) + min(lane, K)) * a.nchunk;
+    float cm[kStatBatch], cs[kStatBatch];
+    int ca[kStatBatch];
+#pragma unroll
+    for (int k = 0; k < kStatBatch; ++k) {
+        const int c = min(k, a.nchunk - 1);  // clamped duplicates are masked below
+        cm[k] = a.st_max[o + c];
+        cs[k] = a.st_sum[o + c];
+        ca[k] = a.st_arg[o + c];
+    }
+    // the address only: a token outside the vocabulary reads an entry in it
+    const int tk = min(max(tok, 0), a.V - 1);
+    const float q = a.draft_probs[(int64_t)b * a.dp_sr + (int64_t)lk * a.dp_sp + tk];
+    const float raw = logit_at_t<DT>(a, b, lk, tk);
+    // position `lane`'s row: max and sum of exp(x / T - max) (T > 0), or the
+    // first argmax of the raw logits (T <= 0)
+    float gm = kNegInf, tot = 0.f, v = kNegInf;
+    int arg = INT_MAX;
+    // Both readings of the statistics are combined, without branches (the
+    // caller keeps the one its temperature needs): running max and sum of
+    // the scaled rows, and the first argmax of the raw rows. The clamped
+    // duplicate chunks change neither max nor argmax; only the sum masks them.
+    auto combine = [&](int n) {
+        float bm = gm;
+#pragma unroll
+        for (int k = 0; k < kStatBatch; ++k) bm = fmaxf(bm, cm[k]);
+        float t = gm == kNegInf ? 0.f : tot * expf(gm - bm);
+#pragma unroll
+        for (int k = 0; k < kStatBatch; ++k) {
+            const float e = expf(cm[k] - bm);
+            t += (k < n && cm[k] != kNegInf) ? cs[k] * e : 0.f;
         }
-        float tot = 0.f;
-        if (T > 0.f) {
-            for (int c = 0; c < a.nchunk; ++c) {
-                const float cm = a.st_max[o + c];
-                if (cm != kNegInf) tot += a.st_sum[o + c] * expf(cm - gm);
-            }
+        gm = bm;
+        tot = t;
+#pragma unroll
+        for (int k = 0; k < kStatBatch; ++k) argmax_merge(v, arg, cm[k], ca[k]);
+    };
+    // Every lane combines (its clamped position's) statistics, and only the
+    // statistics lanes keep the result: behind a lane condition the compiler
+    // would sink the loads into the condition, after the candidate loads.
+    combine(min(kStatBatch, a.nchunk));
+    for (int c0 = kStatBatch; c0 < a.nchunk; c0 += kStatBatch) {
+#pragma unroll
+        for (int k = 0; k < kStatBatch; ++k) {
+            const int c = min(c0 + k, a.nchunk - 1);
+            cm[k] = a.st_max[o + c];
+            cs[k] = a.st_sum[o + c];
+            ca[k] = a.st_arg[o + c];
         }
+        combine(min(kStatBatch, a.nchunk - c0));
+    }
+    if (stat) {
         s_max[lane] = gm;
         s_sum[lane] = tot;
         s_arg[lane] = arg;
     }
-    // lane i < K fetches candidate i's token, draft and target probabilities
-    // and uniform in parallel; lane 0 then walks them in order
     __shared__ int s_tok[kMaxPositions];
     __shared__ float s_q[kMaxPositions], s_p[kMaxPositions], s_u[kMaxPositions];
-    __syncthreads();
-    if (lane < K) {
-        const int tok = a.draft_tokens[(int64_t)b * K + lane];
-        const float q = a.draft_probs[(int64_t)b * a.dp_sr + (int64_t)lane * a.dp_sp + tok];
-        const float raw = logit_at(a, logit_row(a, b, lane), tok);
+    if (cand) {
         float pf;
         if (a.target_is_probs) pf = raw;
-        else if (T <= 0.f) pf = tok == s_arg[lane] ? 1.f : 0.f;
-        else pf = expf((T == 1.f ? raw : raw / T) - s_max[lane]) / s_sum[lane];
+        else if (T <= 0.f) pf = tok == arg ? 1.f : 0.f;
+        else pf = expf((T == 1.f ? raw : raw / T) - gm) / tot;
         s_tok[lane] = tok;
         s_q[lane] = q;
         s_p[lane] = pf;
-        s_u[lane] = a.u_accept[(int64_t)b * K + lane];
+        s_u[lane] = u;
     }
     __syncthreads();
     if (lane == 0) {
         int stop = K, reject = 0;
         for (int i = 0; i < K; ++i) {
-            const int tok = s_tok[i];
-            const double q = (double)s_q[i];
+            const int tk = s_tok[i];
+            const double qd = (double)s_q[i];
             const double p = (double)s_p[i];
-            const double ratio = p / (q + 1e-9);
+            const double ratio = p / (qd + 1e-9);
             const double acc = ratio < 1.0 ? ratio : 1.0;
             const double r = (double)s_u[i];
             if (publish) {
-                a.out_tokens[(int64_t)b * (K + 1) + i] = tok;
+                a.out_tokens[(int64_t)b * (K + 1) + i] = tk;
                 a.out_is_draft[(int64_t)b * (K + 1) + i] = 1;
             }
             if (!(r <= acc)) { stop = i; reject = 1; break; }
@@ -339,9 +402,9 @@ __global__ __launch_bounds__(kPassThreads) void draw_kernel(VerifyArgs a) {
     __shared__ int s_arg[kMaxPositions];
     __shared__ int s_stop, s_reject;
     const int c = blockIdx.x, b = blockIdx.y;
-    accept_row(a, b, s_max, s_sum, s_arg, &s_stop, &s_reject, c == 0);
-    const int i = s_stop;
-    const bool reject = s_reject != 0;
+    accept_row<DT>(a, b, s_max, s_sum, s_arg, &s_stop, &s_reject, c == 0);
+    const int i = __builtin_amdgcn_readfirstlane(s_stop);
+    const bool reject = __builtin_amdgcn_readfirstlane(s_reject) != 0;
     // the stopping position's softmax statistics, as accept_row combined them
     // (the draw's candidates only need their order, so the softmax divides
     // by its sum through one reciprocal; the accept test above used the
@@ -419,22 +482,42 @@ __global__ __launch_bounds__(kPassThreads) void draw_kernel(VerifyArgs a) {
 
 // Combine each row's chunk winners (a kernel boundary, not a per-workgroup
 // release fence: on this multi-XCD part a device-scope fence writes back L2).
+// One wave per row: lane k takes chunks k, k + 64, ..., with every load of a
+// chunk issued together, and the wave reduces by shuffles (the first-index
+// argmax order is total, so any combining order gives the same winner).
 // The family is the reference's branch: the residual when the round rejected
 // and the residual has mass, else the target row, else uniform.
 __global__ __launch_bounds__(64) void finish_kernel(VerifyArgs a) {
-    const int b = blockIdx.x * 64 + threadIdx.x;
-    if (b >= a.B) return;
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x;
     const int K = a.K;
     const int i = a.row_stop[b];
+    const int rejected = a.row_reject[b];
     const int64_t po = (int64_t)b * a.npass;
+    const int64_t fam = (int64_t)a.B * a.npass;
     int any = 0;
-    for (int k = 0; k < a.npass; ++k) any |= a.part_any[po + k];
-    const int f = (a.row_reject[b] && (any & 1)) ? 0 : ((any & 2) ? 1 : 2);
-    const int64_t fo = (int64_t)f * a.B * a.npass + po;
-    float best = -__builtin_huge_valf();
-    int best_i = INT_MAX;
-    for (int k = 0; k < a.npass; ++k) argmax_merge(best, best_i, a.part_best[fo + k], a.part_best_i[fo + k]);
-    a.out_tokens[(int64_t)b * (K + 1) + i] = best_i;
+    float best[3] = {-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf()};
+    int best_i[3] = {INT_MAX, INT_MAX, INT_MAX};
+    for (int k = lane; k < a.npass; k += 64) {
+        any |= a.part_any[po + k];
+#pragma unroll
+        for (int f = 0; f < 3; ++f) argmax_merge(best[f], best_i[f], a.part_best[f * fam + po + k],
+                                                 a.part_best_i[f * fam + po + k]);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        any |= __shfl_xor(any, off, 64);
+#pragma unroll
+        for (int f = 0; f < 3; ++f) {
+            const float ov = __shfl_xor(best[f], off, 64);
+            const int oi = __shfl_xor(best_i[f], off, 64);
+            argmax_merge(best[f], best_i[f], ov, oi);
+        }
+    }
+    if (lane != 0) return;
+    const int f = (rejected && (any & 1)) ? 0 : ((any & 2) ? 1 : 2);
+    const int tok = f == 0 ? best_i[0] : (f == 1 ? best_i[1] : best_i[2]);
+    a.out_tokens[(int64_t)b * (K + 1) + i] = tok;
     a.out_is_draft[(int64_t)b * (K + 1) + i] = 0;
     a.out_count[b] = i + 1;
     a.out_num_accepted[b] = i;
@@ -510,6 +593,16 @@ extern "C" int mf_spec_verify(int num_rows, int num_draft, int vocab, const int3
     float* part_best = take(3 * l.pass);
     int32_t* part_best_i = (int32_t*)take(3 * l.pass);
     int32_t* part_any = (int32_t*)take(l.pass);
+    if (num_draft == 0) {
+        // every lane of the accept walk loads a candidate unconditionally;
+        // with no draft those loads read these in-bounds stand-ins (a token
+        // from the workspace, then an entry of noise row 0, which holds at
+        // least `vocab` values) and are ignored
+        draft_tokens = row_stop;
+        u_accept = st_max;
+        draft_probs = exp_noise;
+        dp_stride_row = dp_stride_pos = 0;
+    }
     VerifyArgs a{num_rows, num_draft, vocab, draft_tokens, draft_probs, dp_stride_row, dp_stride_pos,
                  (const char*)target_logits, target_dtype, tl_stride_row, tl_stride_pos, temperature,
                  target_is_probs, u_accept, exp_noise, noise_stride_row, out_tokens, out_is_draft, out_count,
@@ -527,7 +620,7 @@ extern "C" int mf_spec_verify(int num_rows, int num_draft, int vocab, const int3
         const dim3 grid((unsigned)npass, (unsigned)num_rows);
         hipLaunchKernelGGL((draw_kernel<DT>), grid, dim3(kPassThreads), 0, st, a);
         if (int e = check_launch()) return e;
-        hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((num_rows + 63) / 64)), dim3(64), 0, st, a);
+        hipLaunchKernelGGL(finish_kernel, dim3((unsigned)num_rows), dim3(64), 0, st, a);
         return check_launch();
     };
     if (target_dtype == MF_F32) return run(std::integral_constant<int, MF_F32>{});
