@@ -1346,6 +1346,13 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
                 return n;
             };
             while (PW < mf::kMaxItemTiles && PW < wide_max_tiles && wide_items(PW) > MF_WIDE_ITEMS) PW *= 2;
+            // Beside wide items the narrow ones run in the same launch
+            // (attn_mixed_kernel), where a narrow chain as long as a wide
+            // wave's key range is hidden behind the wide waves; longer
+            // narrow partitions then only save items and merges. Measured
+            // on the C2 step (PW 32): narrow P 16 (the estimate's pick)
+            // 58.1-58.9 us per layer, P 32 56.6-56.8, P 64 60.3-60.5.
+            if (MF_MIXED_LAUNCH && WT > 1 && dtype != MF_F32 && head_dim == DP) P = std::max(P, PW);
         }
     }
 
