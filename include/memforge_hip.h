@@ -49,7 +49,9 @@ const char* mf_status_string(int status);
 
 /* ------------------------------------------------------------------ KV write
  * Scatter `num_tokens` new key/value rows into one layer of the pool through
- * slot_mapping (int64, one slot per row; a negative slot skips the row).
+ * slot_mapping (int64, one slot per row). A row whose slot is outside
+ * [0, num_slots) -- num_slots = blocks * block_size of one pool layer -- is
+ * skipped, so a malformed slot can never address memory past the pool.
  * Source row t, head h starts at src + t*src_stride_t + h*src_stride_h (the
  * same strides for k_src and v_src). Converts src_dtype -> pool_dtype with
  * round-to-nearest-even, so the result is bit-identical to torch's
@@ -63,20 +65,21 @@ int mf_kv_write(const void* k_src, const void* v_src, int src_dtype,
                 const int64_t* slot_mapping, int64_t num_tokens,
                 void* k_pool, void* v_pool, int pool_dtype,
                 int64_t pool_stride_block, int64_t pool_stride_slot,
-                int64_t pool_stride_head, int block_size, int num_heads,
-                int head_dim, mf_stream_t stream);
+                int64_t pool_stride_head, int block_size, int64_t num_slots,
+                int num_heads, int head_dim, mf_stream_t stream);
 
 /* ----------------------------------------------------------------- KV gather
  * The inverse of mf_kv_write: copy pool slots slot_mapping[0..num_tokens) of
  * one layer into dst rows (dst + t*dst_stride_t + h*dst_stride_h), converting
- * pool_dtype -> dst_dtype.
+ * pool_dtype -> dst_dtype. Rows whose slot is outside [0, num_slots) are left
+ * unwritten.
  * Replaces paged_gather.gather_kv (memforge_ml/kernels/paged_gather.py:58-89),
  * PagedKVPool.gather / gather_flat (memforge_ml/runtime/kv_pool.py:151-179)
  * and PagedKVCache.read_kv (memforge_ml/models/paged_attention.py:69-97).
  */
 int mf_kv_gather(const void* k_pool, const void* v_pool, int pool_dtype,
                  int64_t pool_stride_block, int64_t pool_stride_slot,
-                 int64_t pool_stride_head, int block_size,
+                 int64_t pool_stride_head, int block_size, int64_t num_slots,
                  const int64_t* slot_mapping, int64_t num_tokens,
                  void* k_dst, void* v_dst, int dst_dtype,
                  int64_t dst_stride_t, int64_t dst_stride_h, int num_heads,
@@ -114,18 +117,30 @@ int mf_kv_copy_blocks(void* k_pool, void* v_pool, int pool_dtype, int num_layers
  *   [3] table_off  offset of its block table in `tables`
  *   [4] table_len  entries in its block table
  *   [5] token_off  offset of its q_len token ids in `tokens`
+ * `tables` holds tables_len int32 block ids and `tokens` tokens_len int32 token
+ * ids (device). An entry is malformed (MF_PACK_BAD_ENTRY) when a field is
+ * negative, its table run [table_off, table_off + table_len) leaves `tables`,
+ * or its token run [token_off, token_off + q_len) leaves `tokens`; the rows of
+ * a malformed entry load nothing (token 0, slot -1) and its block-table row is
+ * all 0. total_tokens must equal the sum of q_len (MF_PACK_ROW_COUNT
+ * otherwise; surplus rows get seq_slot -1 and slot -1).
  * Outputs (device): token_ids[T] and positions[T] (int64, the model's
  * input_ids / position_ids), seq_slot[T] (entry index per row), slot_mapping[T]
  * (int64, table[p / bs] * bs + p % bs), cu_seqlens[B+1], kv_lens[B] and the
  * padded block_tables[B][max_blocks] (unused entries 0). T = sum of q_len.
  * status (device, int32[4], written by this call) reports malformed input:
  *   status[0] bit flags: MF_PACK_TABLE_OVERFLOW, MF_PACK_NEGATIVE_POSITION,
- *             MF_PACK_DUPLICATE_SLOT, MF_PACK_BAD_ENTRY
- *   status[1] first row needing a block past its table (or -1)
+ *             MF_PACK_DUPLICATE_SLOT, MF_PACK_BAD_ENTRY, MF_PACK_ROW_COUNT,
+ *             MF_PACK_BLOCK_OUT_OF_POOL
+ *   status[1] first row whose slot could not be formed: it needs a block past
+ *             its table, or (num_slots > 0) its block lies outside a pool of
+ *             num_slots slots (or -1)
  *   status[2] a row whose slot another row also writes (or -1)
  *   status[3] first malformed entry (or -1)
- * Duplicate detection runs when slot_bitmap is non-NULL: a device bitmap of
- * num_slots bits that must be all-zero on entry and is all-zero again on exit.
+ * With num_slots > 0, slots at or past num_slots are reported and replaced by
+ * -1. Duplicate detection runs when slot_bitmap is non-NULL: a device bitmap
+ * of num_slots bits that must be all-zero on entry and is all-zero again on
+ * exit. num_entries == 0 with total_tokens > 0 is MF_ERR_ARG.
  * Replaces the engine's per-step packing (memforge_ml/runtime/
  * continuous_engine.py:782-905, 1104-1131; batched_speculative.py:696-701) and
  * VarlenPackedCache._build_write_index (memforge_ml/runtime/varlen_cache.py:161-191).
@@ -135,8 +150,11 @@ int mf_kv_copy_blocks(void* k_pool, void* v_pool, int pool_dtype, int num_layers
 #define MF_PACK_NEGATIVE_POSITION 2
 #define MF_PACK_DUPLICATE_SLOT 4
 #define MF_PACK_BAD_ENTRY 8
+#define MF_PACK_ROW_COUNT 16
+#define MF_PACK_BLOCK_OUT_OF_POOL 32
 int mf_ragged_pack(const int32_t* entries, int num_entries,
-                   const int32_t* tables, const int32_t* tokens,
+                   const int32_t* tables, int64_t tables_len,
+                   const int32_t* tokens, int64_t tokens_len,
                    int block_size, int max_blocks, int64_t total_tokens,
                    int64_t* token_ids, int64_t* positions, int32_t* seq_slot,
                    int64_t* slot_mapping, int32_t* cu_seqlens, int32_t* kv_lens,

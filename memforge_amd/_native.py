@@ -34,6 +34,8 @@ PACK_TABLE_OVERFLOW = 1
 PACK_NEGATIVE_POSITION = 2
 PACK_DUPLICATE_SLOT = 4
 PACK_BAD_ENTRY = 8
+PACK_ROW_COUNT = 16
+PACK_BLOCK_OUT_OF_POOL = 32
 
 _c_int, _c_i64, _c_f32, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -42,13 +44,13 @@ _SIGNATURES = {
     "mf_last_hip_error": (_c_int, []),
     "mf_status_string": (ctypes.c_char_p, [_c_int]),
     "mf_kv_write": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_int,
-                             _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp]),
-    "mf_kv_gather": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _vp, _c_i64,
+                             _c_i64, _c_i64, _c_i64, _c_int, _c_i64, _c_int, _c_int, _vp]),
+    "mf_kv_gather": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_i64, _vp, _c_i64,
                               _vp, _vp, _c_int, _c_i64, _c_i64, _c_int, _c_int, _vp]),
     "mf_kv_copy_blocks": (_c_int, [_vp, _vp, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _vp,
                                    _c_int, _vp]),
-    "mf_ragged_pack": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_i64, _vp, _vp, _vp,
-                                _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),
+    "mf_ragged_pack": (_c_int, [_vp, _c_int, _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_i64, _vp,
+                                _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),
     "mf_paged_attention": (_c_int, [
         _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
         _c_int, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int,
@@ -146,6 +148,15 @@ class PoolView:
     num_heads: int
     head_dim: int
 
+    @property
+    def num_blocks(self) -> int:
+        return int(self.k.shape[0])
+
+    @property
+    def num_slots(self) -> int:
+        """Token slots of the layer; the kernels skip slots outside [0, num_slots)."""
+        return int(self.k.shape[0]) * self.block_size
+
     @staticmethod
     def from_bshd(k: torch.Tensor, v: torch.Tensor) -> "PoolView":
         """``(blocks, slots, heads, dim)`` -- one layer of PagedKVPool."""
@@ -195,7 +206,8 @@ def kv_write(k_rows: torch.Tensor, v_rows: torch.Tensor, slots: torch.Tensor, po
     _check(lib().mf_kv_write(
         _ptr(k_rows), _ptr(v_rows), dtype_code(k_rows.dtype), k_rows.stride(0), k_rows.stride(1),
         _ptr(slots), T, _ptr(pool.k), _ptr(pool.v), dtype_code(pool.k.dtype),
-        pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size, H, D, _stream(k_rows.device),
+        pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size, pool.num_slots, H, D,
+        _stream(k_rows.device),
     ), "mf_kv_write")
 
 
@@ -211,7 +223,7 @@ def kv_gather(pool: PoolView, slots: torch.Tensor, k_rows: torch.Tensor, v_rows:
     T, H, D = k_rows.shape
     _check(lib().mf_kv_gather(
         _ptr(pool.k), _ptr(pool.v), dtype_code(pool.k.dtype), pool.stride_block, pool.stride_slot,
-        pool.stride_head, pool.block_size, _ptr(slots), T, _ptr(k_rows), _ptr(v_rows),
+        pool.stride_head, pool.block_size, pool.num_slots, _ptr(slots), T, _ptr(k_rows), _ptr(v_rows),
         dtype_code(k_rows.dtype), k_rows.stride(0), k_rows.stride(1), H, D, _stream(k_rows.device),
     ), "mf_kv_gather")
 
@@ -611,14 +623,50 @@ class PackedStep:
         )
 
 
+def check_pack_entries(entries: np.ndarray, tables: np.ndarray, tokens_len: int, total_tokens: int,
+                       num_blocks: Optional[int] = None) -> None:
+    """Host check of ragged-pack descriptors before they go to the device:
+    every field non-negative, every table run inside ``tables`` and every
+    token run inside ``tokens_len``, the row count equal to the sum of q_len,
+    and (with ``num_blocks``) every block id the runs name inside the pool.
+    Raises ValueError / IndexError naming the first bad entry."""
+    ent = np.asarray(entries, dtype=np.int64).reshape(-1, ENTRY_INTS)
+    if ent.shape[0] == 0:
+        if total_tokens:
+            raise ValueError(f"{total_tokens} packed rows but no entries")
+        return
+    bad = np.flatnonzero((ent[:, [0, 2, 3, 4, 5]] < 0).any(axis=1)
+                         | (ent[:, 3] + ent[:, 4] > len(tables))
+                         | (ent[:, 5] + ent[:, 0] > tokens_len))
+    if bad.size:
+        e = int(bad[0])
+        raise ValueError(f"ragged-pack entry {e} is malformed: {ent[e].tolist()} against "
+                         f"{len(tables)} table ids and {tokens_len} tokens")
+    rows = int(ent[:, 0].sum())
+    if rows != total_tokens:
+        raise ValueError(f"entries hold {rows} rows, the step declares {total_tokens}")
+    if num_blocks is not None and len(tables):
+        t = np.asarray(tables)
+        lo, hi = int(t.min()), int(t.max())
+        if lo < 0 or hi >= num_blocks:
+            raise IndexError(f"block id {lo if lo < 0 else hi} is outside a pool of {num_blocks} blocks")
+
+
 def ragged_pack(entries: torch.Tensor, tables: torch.Tensor, tokens: torch.Tensor,
                 total_tokens: int, block_size: int, max_blocks: int,
                 slot_bitmap: Optional[torch.Tensor] = None, num_slots: int = 0,
                 out: Optional[PackedStep] = None) -> PackedStep:
     """Run mf_ragged_pack on device descriptors (int32 tensors already on the
     GPU), into ``out``'s buffers when given (they must be sized for
-    ``total_tokens`` rows, ``entries.shape[0]`` entries and ``max_blocks``)."""
+    ``total_tokens`` rows, ``entries.shape[0]`` entries and ``max_blocks``).
+    The kernel bounds every load by ``tables.numel()`` / ``tokens.numel()``
+    and, with ``num_slots``, every block id by the pool; host callers that
+    built the descriptors check them first with ``check_pack_entries``."""
     require_device(entries, tables, tokens)
+    if entries.dtype != torch.int32 or tables.dtype != torch.int32 or tokens.dtype != torch.int32:
+        raise TypeError("ragged_pack takes int32 entries, tables and tokens")
+    if not (entries.is_contiguous() and tables.is_contiguous() and tokens.is_contiguous()):
+        raise ValueError("ragged_pack takes contiguous entries, tables and tokens")
     dev = entries.device
     B = entries.shape[0]
     if out is not None:
@@ -628,7 +676,8 @@ def ragged_pack(entries: torch.Tensor, tables: torch.Tensor, tokens: torch.Tenso
     else:
         out = PackedStep.allocate(total_tokens, B, max_blocks, dev)
     _check(lib().mf_ragged_pack(
-        _ptr(entries), B, _ptr(tables), _ptr(tokens), block_size, max_blocks, total_tokens,
+        _ptr(entries), B, _ptr(tables), tables.numel(), _ptr(tokens), tokens.numel(), block_size,
+        max_blocks, total_tokens,
         _ptr(out.token_ids), _ptr(out.positions), _ptr(out.seq_slot), _ptr(out.slot_mapping),
         _ptr(out.cu_seqlens), _ptr(out.kv_lens), _ptr(out.block_tables), _ptr(slot_bitmap),
         num_slots, _ptr(out.status), _stream(),

@@ -107,6 +107,7 @@ struct CopyArgs {
     int64_t p_sb, p_ss, p_sh;  // elements
     const int64_t* slots;
     int64_t num_tokens;
+    int64_t num_slots;  // slots of one pool layer; rows outside [0, num_slots) are skipped
     int block_size, num_heads, head_dim;
 };
 
@@ -125,7 +126,7 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(CopyArgs a) {
         const int h = rem / chunks;
         const int c = rem - h * chunks;
         const int64_t slot = a.slots[t];
-        if (slot < 0) continue;
+        if (slot < 0 || slot >= a.num_slots) continue;
         const int64_t blk = slot / a.block_size;
         const int64_t off = slot - blk * a.block_size;
         const int64_t pe = blk * a.p_sb + off * a.p_ss + (int64_t)h * a.p_sh + (int64_t)c * VW;
@@ -191,7 +192,8 @@ int dispatch_copy(int rdt, int pdt, const CopyArgs& a, hipStream_t stream) {
 
 bool copy_args_ok(const CopyArgs& a, int rdt, int pdt) {
     if (!dtype_ok(rdt) || !dtype_ok(pdt)) return false;
-    if (a.num_tokens < 0 || a.block_size <= 0 || a.num_heads <= 0 || a.head_dim <= 0) return false;
+    if (a.num_tokens < 0 || a.num_slots < 0 || a.block_size <= 0 || a.num_heads <= 0 || a.head_dim <= 0)
+        return false;
     if (a.num_tokens > 0 && (!a.row_k || !a.row_v || !a.pool_k || !a.pool_v || !a.slots)) return false;
     return true;
 }
@@ -204,10 +206,11 @@ extern "C" int mf_kv_write(const void* k_src, const void* v_src, int src_dtype,
                            const int64_t* slot_mapping, int64_t num_tokens, void* k_pool,
                            void* v_pool, int pool_dtype, int64_t pool_stride_block,
                            int64_t pool_stride_slot, int64_t pool_stride_head, int block_size,
-                           int num_heads, int head_dim, mf_stream_t stream) {
+                           int64_t num_slots, int num_heads, int head_dim, mf_stream_t stream) {
     mf::CopyArgs a{(const char*)k_src, (const char*)v_src, src_stride_t, src_stride_h,
                    (char*)k_pool, (char*)v_pool, pool_stride_block, pool_stride_slot,
-                   pool_stride_head, slot_mapping, num_tokens, block_size, num_heads, head_dim};
+                   pool_stride_head, slot_mapping, num_tokens, num_slots, block_size, num_heads,
+                   head_dim};
     if (!mf::copy_args_ok(a, src_dtype, pool_dtype)) return MF_ERR_ARG;
     if (num_tokens == 0) return MF_OK;
     return mf::dispatch_copy<false>(src_dtype, pool_dtype, a, (hipStream_t)stream);
@@ -215,14 +218,15 @@ extern "C" int mf_kv_write(const void* k_src, const void* v_src, int src_dtype,
 
 extern "C" int mf_kv_gather(const void* k_pool, const void* v_pool, int pool_dtype,
                             int64_t pool_stride_block, int64_t pool_stride_slot,
-                            int64_t pool_stride_head, int block_size,
+                            int64_t pool_stride_head, int block_size, int64_t num_slots,
                             const int64_t* slot_mapping, int64_t num_tokens, void* k_dst,
                             void* v_dst, int dst_dtype, int64_t dst_stride_t,
                             int64_t dst_stride_h, int num_heads, int head_dim,
                             mf_stream_t stream) {
     mf::CopyArgs a{(const char*)k_dst, (const char*)v_dst, dst_stride_t, dst_stride_h,
                    (char*)k_pool, (char*)v_pool, pool_stride_block, pool_stride_slot,
-                   pool_stride_head, slot_mapping, num_tokens, block_size, num_heads, head_dim};
+                   pool_stride_head, slot_mapping, num_tokens, num_slots, block_size, num_heads,
+                   head_dim};
     if (!mf::copy_args_ok(a, dst_dtype, pool_dtype)) return MF_ERR_ARG;
     if (num_tokens == 0) return MF_OK;
     return mf::dispatch_copy<true>(dst_dtype, pool_dtype, a, (hipStream_t)stream);

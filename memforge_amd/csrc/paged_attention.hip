@@ -1352,6 +1352,11 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
             // narrow partitions then only save items and merges. Measured
             // on the C2 step (PW 32): narrow P 16 (the estimate's pick)
             // 58.1-58.9 us per layer, P 32 56.6-56.8, P 64 60.3-60.5.
+            // The planner does not see the pool's block size: the shared
+            // launch needs 16-key blocks, and with other block sizes the two
+            // classes run as separate launches, where the raised partition
+            // only lengthens the narrow launch's chains (no effect on
+            // results, which do not depend on the partition).
             if (MF_MIXED_LAUNCH && WT > 1 && dtype != MF_F32 && head_dim == DP) P = std::max(P, PW);
         }
     }

@@ -65,6 +65,17 @@ def run_varlen(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: nat.PoolView,
         cu.append(len(row_map))
         kvl.append(kv_lens[s] if kv_lens is not None else max(positions[r] for r in rows) + 1)
     identity = row_map == list(range(T))
+    # every block id the kernel will read must address the pool
+    bs, nblocks = pool.block_size, pool.num_blocks
+    for i, s in enumerate(order):
+        keys = kvl[i] if pool_lens is None else min(kvl[i], pool_lens[s])
+        need = (keys + bs - 1) // bs
+        if need > len(tables[s]):
+            raise IndexError(f"sequence {s} needs {need} blocks but its block table has {len(tables[s])}")
+        ids = np.asarray(tables[s][:need], dtype=np.int64)
+        if ids.size and (int(ids.min()) < 0 or int(ids.max()) >= nblocks):
+            raise IndexError(f"block table of sequence {s} names a block outside the pool of {nblocks}")
+    nat.require_device(q_rows, out_rows, pool.k)
     items, merges, counts = nat.plan_attention_host(cu, kvl, hq, num_kv_heads, d, q_rows.dtype)
     # tables, plan, cu/kv lengths, positions, row map and pool lengths cross
     # to the device in one copy, and the launch addresses them inside that

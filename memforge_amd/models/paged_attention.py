@@ -58,9 +58,21 @@ class PagedKVCache:
             self._pool_view = pv
         return pv
 
+    def _blocks(self, block_table: List[int], needed: int) -> np.ndarray:
+        """The first ``needed`` physical block ids as the reference's tensor
+        indexing reads them: a negative id counts from the end of the cache,
+        and an id outside [-num_blocks, num_blocks) raises torch's IndexError
+        (``self.key_cache[physical_block_id]``, paged_attention.py:65, 87)."""
+        ids = np.asarray(list(block_table)[:needed], dtype=np.int64)
+        bad = (ids < -self.num_blocks) | (ids >= self.num_blocks)
+        if bad.any():
+            raise IndexError(f"index {int(ids[bad][0])} is out of bounds for dimension 0 with size "
+                             f"{self.num_blocks}")
+        return np.where(ids < 0, ids + self.num_blocks, ids)
+
     def _slots(self, block_table: List[int], start: int, count: int) -> torch.Tensor:
         pos = np.arange(start, start + count, dtype=np.int64)
-        table = np.asarray(list(block_table), dtype=np.int64)
+        table = self._blocks(block_table, (start + count + self.block_size - 1) // self.block_size)
         slots = table[pos // self.block_size] * self.block_size + pos % self.block_size
         return nat.upload([slots], self.device)[0]
 
@@ -118,6 +130,7 @@ class PagedAttention(nn.Module):
             )
         q = query[0].to(paged_kv.dtype).permute(1, 0, 2)  # (q_len, H, D) view
         out = torch.empty((1, q_len, num_heads * head_dim), dtype=paged_kv.dtype, device=query.device)
-        run_varlen(q, out[0].view(q_len, num_heads, head_dim), paged_kv._view(), [list(block_table)],
+        table = paged_kv._blocks(block_table, (context_len + paged_kv.block_size - 1) // paged_kv.block_size)
+        run_varlen(q, out[0].view(q_len, num_heads, head_dim), paged_kv._view(), [table.tolist()],
                    [0] * q_len, [context_len - 1] * q_len, scale, num_heads, kv_lens=[context_len])
         return out.to(query.dtype)

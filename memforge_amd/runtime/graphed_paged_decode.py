@@ -41,6 +41,16 @@ from memforge_amd.runtime.varlen_cache import VarlenPackedCache
 _MIN_PARTITION_TILES = 4
 
 
+def split_plan_capacity(batch: int, num_kv_heads: int, max_blocks: int, block_size: int, head_dim: int):
+    """(narrow items, wide items, merges, partial floats) that hold any decode
+    plan of ``batch`` single-row sequences whose tables have at most
+    ``max_blocks`` blocks of ``block_size`` keys."""
+    tiles = math.ceil(max_blocks * block_size / 16)
+    cap_items = batch * num_kv_heads * (math.ceil(tiles / _MIN_PARTITION_TILES) + 4) + 4
+    floats = cap_items * 16 * (max(head_dim, 32) + 2)
+    return cap_items, 0, batch * num_kv_heads, floats
+
+
 class _Bucket:
     """Static buffers and the captured graph of one batch size."""
 
@@ -60,12 +70,13 @@ class _Bucket:
             # the single items padded to whole workgroups; nothing to merge
             self.plan = nat.CountedPlan(4 * b * hkv + 4, 0, 0, 0, dev)
         else:
-            # a (sequence, kv head) of T tiles is one item when T <= P, else
-            # four per unit of at most 4P tiles (P >= _MIN_PARTITION_TILES),
-            # and the single items are padded to whole workgroups
-            cap_items = b * hkv * (math.ceil(mb / _MIN_PARTITION_TILES) + 4) + 4
-            floats = cap_items * 16 * (max(owner.pool.spec.head_dim, 32) + 2)
-            self.plan = nat.CountedPlan(cap_items, 0, b * hkv, floats, dev)
+            # a (sequence, kv head) of T 16-key tiles is one item when T <= P,
+            # else four per unit of at most 4P tiles (P >= _MIN_PARTITION_TILES),
+            # i.e. at most ceil(T / P) + 4 items; the single items are padded to
+            # whole workgroups. T counts tiles, not pool blocks: a block of 32
+            # keys is two tiles.
+            self.plan = nat.CountedPlan(*split_plan_capacity(b, hkv, mb, owner.bs, owner.pool.spec.head_dim),
+                                        dev)
         self.keep = torch.arange(b, dtype=torch.long, device=dev)
         meta = {"block_tables": self.packed.block_tables, "cu_seqlens": self.packed.cu_seqlens,
                 "kv_lens": self.packed.kv_lens, "positions": self.packed.positions, "row_map": None,
@@ -117,7 +128,8 @@ class GraphedPagedDecoder:
         return min(p, self.max_batch) if b <= self.max_batch else p
 
     def _forward(self, bk: _Bucket) -> torch.Tensor:
-        nat.ragged_pack(bk.entries, bk.tables, bk.tokens, bk.b, self.bs, self.max_blocks, out=bk.packed)
+        nat.ragged_pack(bk.entries, bk.tables, bk.tokens, bk.b, self.bs, self.max_blocks, out=bk.packed,
+                        num_slots=self.pool.capacity_tokens)
         with attention_backend.backend_enabled_on(self.model) as routed:
             if not routed:
                 raise RuntimeError("graphed decode needs the attention registry")
@@ -170,6 +182,8 @@ class GraphedPagedDecoder:
             ent[i, 4] = len(t)
             tab[i, : len(t)] = t
             tok[i] = int(tokens[i])
+        if n and (tab[:n].min() < 0 or tab[:n].max() >= self.pool.num_blocks):
+            raise IndexError(f"a block table names a block outside the pool of {self.pool.num_blocks}")
         bk.inputs.copy_(bk.host, non_blocking=True)
         bk.copied = torch.cuda.Event()
         bk.copied.record()

@@ -88,7 +88,7 @@ class PagedKVPool:
 
     def slot_indices(self, block_table: torch.Tensor, start: int, end: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """(physical block, slot) tensors for token range [start, end)
-        (kv_pool.py:233-251). The bound check is integer arithmetic on the host,
+        (memforge_ml/runtime/kv_pool.py:92-110). The bound check is integer arithmetic on the host,
         so it costs no device synchronisation."""
         if end > start and (end - 1) // self.block_size >= block_table.numel():
             raise IndexError(

@@ -64,6 +64,7 @@ def packed_forward(model, pool, tokens: Sequence[Sequence[int]], starts: Sequenc
     ent[:, 5] = cu[:-1]
     flat_tables = np.fromiter((b for t in tables for b in t), dtype=np.int32)
     flat_tokens = np.fromiter((tok for run in tokens for tok in run), dtype=np.int32)
+    nat.check_pack_entries(ent, flat_tables, len(flat_tokens), T, pool.num_blocks)
     items, merges, counts = nat.plan_attention_host(cu.tolist(), kv_lens, model.config.num_attention_heads,
                                                     spec.num_kv_heads, spec.head_dim, pool.key_pool.dtype)
     keep_np = np.asarray(list(keep_rows), dtype=np.int64)
@@ -71,7 +72,7 @@ def packed_forward(model, pool, tokens: Sequence[Sequence[int]], starts: Sequenc
     # to the device in one copy
     d_ent, d_tables, d_tokens, d_items, d_merges, keep = nat.upload(
         [ent, flat_tables, flat_tokens, *nat.plan_upload_parts(items, merges), keep_np], spec.device)
-    packed = nat.ragged_pack(d_ent, d_tables, d_tokens, T, bs, max_blocks)
+    packed = nat.ragged_pack(d_ent, d_tables, d_tokens, T, bs, max_blocks, num_slots=pool.capacity_tokens)
     attn_plan = nat.plan_from_parts(items, merges, counts, d_items, d_merges)
     meta = {"block_tables": packed.block_tables, "cu_seqlens": packed.cu_seqlens,
             "kv_lens": packed.kv_lens, "positions": packed.positions, "row_map": None,

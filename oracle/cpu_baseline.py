@@ -4,10 +4,10 @@
 Per sequence and layer the reference reads its context out of the pool with
 one flat ``index_select`` and a permute (``gather_kv``,
 memforge_ml/kernels/paged_gather.py:58-89, slot mapping from
-kv_pool.py:233-271), repeats KV heads for grouped-query attention and runs a
-plain softmax attention over the materialised context
+memforge_ml/runtime/kv_pool.py:92-130), repeats KV heads for grouped-query
+attention and runs a plain softmax attention over the materialised context
 (``paged_attention_varlen_materialised``, memforge_ml/kernels/
-varlen_attention.py:577-596). That is exactly what this does, in float32.
+varlen_attention.py:291-395). That is exactly what this does, in float32.
 """
 
 from __future__ import annotations

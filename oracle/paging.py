@@ -20,7 +20,7 @@ def flat_slot_index(physical: Sequence[int], slots: Sequence[int], block_size: i
 def slot_indices(block_table: Sequence[int], start: int, end: int,
                  block_size: int) -> Tuple[np.ndarray, np.ndarray]:
     """(physical block, slot) for token range [start, end), with the reference's
-    IndexError text (memforge_ml/runtime/kv_pool.py:233-251)."""
+    IndexError text (memforge_ml/runtime/kv_pool.py:92-110)."""
     table = np.asarray(block_table, dtype=np.int64)
     positions = np.arange(start, end, dtype=np.int64)
     logical = positions // block_size
@@ -34,7 +34,8 @@ def slot_indices(block_table: Sequence[int], start: int, end: int,
 
 
 def slot_mapping(block_table: Sequence[int], start: int, end: int, block_size: int) -> np.ndarray:
-    """Flat pool slots of [start, end) (kv_pool.py:257-271 = slot_indices + flat index)."""
+    """Flat pool slots of [start, end): ``flat_indices``, i.e. slot_indices plus
+    the flat index (memforge_ml/runtime/kv_pool.py:116-130)."""
     physical, slots = slot_indices(block_table, start, end, block_size)
     return flat_slot_index(physical, slots, block_size)
 

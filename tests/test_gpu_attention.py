@@ -211,6 +211,37 @@ def test_operator_layout_bhsd(device):
     assert np.abs(to_np64(got) - want).max() <= 1e-5
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_operator_forward_through_its_own_api(device, dtype):
+    """PagedKVCache.write_kv + PagedAttention.forward at the C1 head shape
+    (15 heads, D 64, block 16, 8 sequences of U[17,512] keys, 2 query rows
+    each) against the operator oracle. In bf16 the reference rounds the fp32
+    softmax to the query dtype before the value product
+    (memforge_ml/models/paged_attention.py:133); the oracle does the same
+    (round_probs) and the bar is 2e-2 max-abs / 1e-2 mean-rel; fp32 at 1e-5."""
+    from memforge_amd.models.paged_attention import PagedAttention, PagedKVCache
+    from oracle.bf16 import round_to_bf16
+
+    dt = DT[dtype]
+    gen = torch.Generator().manual_seed(23)
+    h, d, bs = 15, 64, 16
+    cache = PagedKVCache(1024, bs, h, d, dtype=dt, device=str(device))
+    ctx = torch.randint(17, 513, (8,), generator=gen).tolist()
+    tables = random_tables(gen, 1024, ctx, bs)
+    op = PagedAttention()
+    for c, t in zip(ctx, tables):
+        k = torch.randn((1, h, c, d), generator=gen).to(dt)
+        v = torch.randn((1, h, c, d), generator=gen).to(dt)
+        cache.write_kv(k.to(device), v.to(device), t, 0)
+        q = torch.randn((1, h, 2, d), generator=gen).to(dt)
+        got = op(q.to(device), cache, t, c)
+        assert got.shape == (1, 2, h * d) and got.dtype == dt
+        want = oatt.paged_operator(q.float().numpy(), cache.key_cache.float().cpu().numpy(),
+                                   cache.value_cache.float().cpu().numpy(), t, c,
+                                   round_probs=round_to_bf16 if dtype == "bf16" else None)
+        _check(to_np64(got), want, dt)
+
+
 @pytest.mark.parametrize("fused", [True, False])
 def test_split_k_merge_fused_and_separate_agree(device, fused):
     """The in-kernel (last arrival) merge and the separate merge kernel give the

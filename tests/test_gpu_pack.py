@@ -103,3 +103,48 @@ def test_pack_verify_rows(device):
     want = paging.ragged_pack(entries, bs, max_blocks)
     for name in ("token_ids", "positions", "slot_mapping", "cu_seqlens", "kv_lens"):
         np.testing.assert_array_equal(getattr(out, name).cpu().numpy(), want[name], err_msg=name)
+
+
+def test_pack_skips_malformed_entries_and_reports_them(device):
+    """Malformed descriptors through the C ABI are reported, not followed:
+    an entry whose table run or token run leaves the arrays, or with a
+    negative field, loads nothing (token 0, slot -1, an all-zero table row),
+    a block id outside the pool gives slot -1, and well-formed entries in the
+    same step pack exactly as the oracle packs them."""
+    bs = 16
+    good = [(3, 5, 8, [2], [11, 12, 13]), (1, 40, 41, [4, 1, 6], [14])]
+    d, t, k, total = _upload(good, device)
+    want = paging.ragged_pack(good, bs, 3)
+    desc = d.cpu()
+    rows = desc.tolist()
+    # entry 2: its table run leaves `tables`; entry 3: its token run leaves
+    # `tokens`; entry 4: a negative table length
+    rows.append([2, 0, 2, t.numel() - 1, 5, 0])
+    rows.append([2, 0, 2, 0, 1, k.numel() + 100])
+    rows.append([1, 0, 1, 0, -3, 0])
+    bad = torch.tensor(rows, dtype=torch.int32, device=device)
+    out = nat.ragged_pack(bad, t, k, total + 5, bs, 3, num_slots=8 * bs)
+    st = out.status.cpu().tolist()
+    assert st[0] & nat.PACK_BAD_ENTRY and st[3] == 2, st
+    assert not st[0] & nat.PACK_ROW_COUNT
+    slots = out.slot_mapping.cpu().numpy()
+    toks = out.token_ids.cpu().numpy()
+    np.testing.assert_array_equal(slots[:total], want["slot_mapping"])
+    np.testing.assert_array_equal(toks[:total], want["token_ids"])
+    assert (slots[total:] == -1).all() and (toks[total:] == 0).all()
+    bt = out.block_tables.cpu().numpy()
+    np.testing.assert_array_equal(bt[:2], want["block_tables"])
+    assert (bt[2:] == 0).all()
+    # a block id past a pool of 5 blocks: its row gets slot -1, its table entry 0
+    out = nat.ragged_pack(d, t, k, total, bs, 3, num_slots=5 * bs)
+    st = out.status.cpu().tolist()
+    assert st[0] & nat.PACK_BLOCK_OUT_OF_POOL and st[1] == 3, st
+    assert out.slot_mapping.cpu().tolist() == want["slot_mapping"][:3].tolist() + [-1]
+    assert out.block_tables.cpu().numpy()[1].tolist() == [4, 1, 0]
+    # more rows declared than the entries hold: the surplus rows load nothing
+    out = nat.ragged_pack(d, t, k, total + 2, bs, 3)
+    st = out.status.cpu().tolist()
+    assert st[0] & nat.PACK_ROW_COUNT, st
+    assert out.slot_mapping.cpu().tolist()[total:] == [-1, -1]
+    assert out.seq_slot.cpu().tolist()[total:] == [-1, -1]
+    assert out.cu_seqlens.cpu().tolist() == [0, 3, 4]

@@ -293,3 +293,83 @@ def test_planner_partition_picks_on_the_config_shapes():
     p = _plan(list(range(257)), c5, hq=40, hkv=8, d=128)
     long_seqs = sum(1 for c in c5 if (c + 15) // 16 > 512)
     assert p.n_merges == 8 * long_seqs and _partition_of(p.items_host[: p.n_narrow]) == 128
+
+
+def test_planner_mixed_step_partitions_on_the_c2_shape():
+    """The C2 mixed step (4 chunks of 512 on priors U[0,2048] + 28 decodes of
+    U[64,4096], bf16 D 64): the wide partition is the smallest power of two
+    that keeps wide items within the target (32 tiles), and the narrow
+    partition is raised to it because both classes share one launch."""
+    g = torch.Generator().manual_seed(0)
+    prior = torch.randint(0, 2049, (4,), generator=g).tolist()
+    dctx = torch.randint(64, 4097, (28,), generator=g).tolist()
+    q_lens = [512] * 4 + [1] * 28
+    kv = [p + 512 for p in prior] + dctx
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).tolist()
+    p = _plan(cu, kv, hq=15, hkv=5, d=64)
+    wide = p.items_host[p.n_narrow:]
+    live = wide[wide[:, 3] > 0]
+    assert int((live[:, 5] - live[:, 4]).max()) == 32
+    assert _partition_of(p.items_host[: p.n_narrow]) == 32
+    # decode rows alone keep the estimate's own pick
+    alone = _plan(list(range(29)), dctx, hq=15, hkv=5, d=64)
+    assert _partition_of(alone.items_host[: alone.n_narrow]) == 16
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_graphed_split_capacity_holds_the_longest_context_plans(bs):
+    """The capacity a graphed decode bucket reserves when plans may need a
+    merge counts 16-key tiles, not pool blocks: every plan of a full bucket at
+    the longest context fits it, at the planner's own pick and at the smallest
+    partition it uses."""
+    from memforge_amd.runtime.graphed_paged_decode import _MIN_PARTITION_TILES, split_plan_capacity
+
+    max_model_len = 12000
+    mb = (max_model_len + bs - 1) // bs + 1
+    for b, hkv, hq, d in ((1, 5, 15, 64), (8, 8, 40, 128), (4, 2, 16, 64)):
+        cap_items, _, cap_merges, floats = split_plan_capacity(b, hkv, mb, bs, d)
+        kv = [mb * bs] * b
+        for pt in (0, _MIN_PARTITION_TILES, 8):
+            items, merges, counts = nat.plan_attention_host(list(range(b + 1)), kv, hq, hkv, d,
+                                                            torch.bfloat16, pt)
+            assert counts[0] <= cap_items and counts[1] == 0, (bs, b, pt, counts, cap_items)
+            assert counts[2] <= cap_merges and counts[3] <= floats, (bs, b, pt, counts)
+
+
+def test_pack_host_check_names_the_malformed_entry():
+    ent = np.array([[2, 0, 2, 0, 1, 0], [1, 5, 6, 1, 1, 2]], dtype=np.int32)
+    tables = np.array([3, 4], dtype=np.int32)
+    nat.check_pack_entries(ent, tables, 3, 3, num_blocks=8)
+    for bad, what in (((1, 3), -1), ((1, 4), 2), ((1, 5), 3), ((0, 0), 4)):
+        e = ent.copy()
+        e[bad] = what
+        with pytest.raises(ValueError, match="entry"):
+            nat.check_pack_entries(e, tables, 3, int(max(e[:, 0].sum(), 0)), num_blocks=8)
+    with pytest.raises(ValueError, match="rows"):
+        nat.check_pack_entries(ent, tables, 3, 4)
+    with pytest.raises(IndexError, match="outside a pool"):
+        nat.check_pack_entries(ent, tables, 3, 3, num_blocks=4)
+    with pytest.raises(ValueError, match="no entries"):
+        nat.check_pack_entries(np.zeros((0, 6), np.int32), tables, 3, 2)
+
+
+def test_pack_rejects_rows_without_entries_and_bad_lengths_before_any_launch():
+    """mf_ragged_pack's argument checks run before any launch (no GPU needed):
+    packed rows with no entry to take them from, negative array lengths and
+    missing arrays are MF_ERR_ARG."""
+    L = nat.lib()
+    dummy = 1 << 20  # never dereferenced
+    base = dict(entries=dummy, n=1, tables=dummy, tl=4, tokens=dummy, kl=4, bs=16, mb=1, T=2)
+
+    def call(**kw):
+        a = {**base, **kw}
+        return L.mf_ragged_pack(a["entries"], a["n"], a["tables"], a["tl"], a["tokens"], a["kl"], a["bs"],
+                                a["mb"], a["T"], dummy, dummy, dummy, dummy, dummy, dummy, dummy, None, 0,
+                                dummy, None)
+
+    assert call(n=0) == -1            # two rows, no entry
+    assert call(tl=-1) == -1
+    assert call(kl=-1) == -1
+    assert call(tables=None) == -1    # a table length without a table
+    assert call(tokens=None) == -1
+    assert call(bs=0) == -1
