@@ -240,6 +240,35 @@ int mf_paged_attention_counted(const void* q, int64_t q_stride_row, int64_t q_st
                                int64_t capacity_merges, const int32_t* device_counts,
                                float* partials, int64_t partials_floats, mf_stream_t stream);
 
+/* mf_paged_attention without a partials buffer or merge counters, so that
+ * the call allocates nothing. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops or harnesses that forbid hipMalloc). Split-K partials go to
+ * a device array the library owns: MF_NOALLOC_PARTIALS_FLOATS fp32 values
+ * (32 MiB) per GPU, held from the first call on that GPU until the process
+ * ends; partitions are merged by the separate merge kernel. partials_floats
+ * is what the plan needs (counts[3] from mf_attention_plan): a plan needing
+ * more is MF_ERR_WORKSPACE, returned before anything touches the device. The
+ * stream must belong to the current device. Every call on one GPU uses the
+ * same array, which keeps the last call's contents (no kernel here needs it
+ * cleared), so calls that overlap on one GPU race. Everything else is as in
+ * mf_paged_attention. */
+#define MF_NOALLOC_PARTIALS_FLOATS (8 * 1024 * 1024)
+int mf_paged_attention_noalloc(const void* q, int64_t q_stride_row, int64_t q_stride_head,
+                               void* out, int64_t out_stride_row, int64_t out_stride_head,
+                               int dtype, const void* k_pool, const void* v_pool,
+                               int64_t pool_stride_block, int64_t pool_stride_slot,
+                               int64_t pool_stride_head, int block_size,
+                               const int32_t* block_tables, int64_t block_table_stride,
+                               const int32_t* cu_seqlens, const int32_t* kv_lens,
+                               const int64_t* positions, const int32_t* row_map,
+                               const int32_t* pool_lens, const void* new_k, const void* new_v,
+                               int64_t new_stride_row, int64_t new_stride_head,
+                               int num_q_heads, int num_kv_heads, int head_dim, float scale,
+                               const int32_t* plan_items, int64_t num_items_narrow,
+                               int64_t num_items_wide, const int32_t* plan_merges,
+                               int64_t num_merges, int64_t partials_floats, mf_stream_t stream);
+
 /* Host-side planner for mf_paged_attention. Inputs are HOST arrays:
  * cu_seqlens[B+1] and kv_lens[B]. Splits every (sequence, kv head, column
  * tile) over key partitions of `partition_tiles` 16-key tiles (0 = chosen

@@ -59,6 +59,10 @@ _SIGNATURES = {
         _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
         _c_int, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int,
         _c_int, _c_f32, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _vp]),
+    "mf_paged_attention_noalloc": (_c_int, [
+        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
+        _c_int, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int,
+        _c_int, _c_f32, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp]),
     "mf_attention_plan": (_c_int, [_c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                    _vp, _c_i64, _vp, _c_i64, _vp]),
     "mf_spec_verify_workspace_size": (_c_i64, [_c_int, _c_int]),
@@ -525,6 +529,47 @@ def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView
         _ptr(plan.items), plan.n_narrow, plan.n_wide, _ptr(plan.merges), plan.n_merges,
         _ptr(partials), partials.numel() if partials is not None else 0, _ptr(counters), _stream(q_rows.device),
     ), "mf_paged_attention")
+
+
+# fp32 partials the no-allocation entry point holds per GPU (32 MiB)
+NOALLOC_PARTIALS_FLOATS = 8 * 1024 * 1024
+
+
+def paged_attention_noalloc(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView,
+                            block_tables: torch.Tensor, cu_seqlens: torch.Tensor, kv_lens: torch.Tensor,
+                            positions: torch.Tensor, plan: AttentionPlan, scale: float, num_kv_heads: int,
+                            row_map: Optional[torch.Tensor] = None, pool_lens: Optional[torch.Tensor] = None,
+                            new_k_rows: Optional[torch.Tensor] = None,
+                            new_v_rows: Optional[torch.Tensor] = None) -> None:
+    """``paged_attention`` through mf_paged_attention_noalloc: the split-K
+    partials live in the library's own per-GPU array, so the call allocates
+    nothing (neither here nor in the library). Plans needing more than
+    NOALLOC_PARTIALS_FLOATS partial floats are refused."""
+    _rows_ok(q_rows, "q_rows")
+    _rows_ok(out_rows, "out_rows")
+    require_device(q_rows, out_rows, pool.k, block_tables, cu_seqlens, kv_lens, positions)
+    if q_rows.dtype != pool.k.dtype or out_rows.dtype != pool.k.dtype:
+        raise TypeError("query, output and pool must share a dtype")
+    nk, nv = new_k_rows, new_v_rows
+    if pool_lens is not None:
+        if nk is None or nv is None:
+            raise ValueError("pool_lens needs the in-flight new_k_rows/new_v_rows")
+        require_device(pool_lens, nk, nv)
+        if nk.stride() != nv.stride():
+            raise ValueError("in-flight K and V rows must share strides")
+    bt_stride = block_tables.shape[1] if block_tables.dim() == 2 else 0
+    _check(lib().mf_paged_attention_noalloc(
+        _ptr(q_rows), q_rows.stride(0), q_rows.stride(1),
+        _ptr(out_rows), out_rows.stride(0), out_rows.stride(1),
+        dtype_code(q_rows.dtype), _ptr(pool.k), _ptr(pool.v),
+        pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size,
+        _ptr(block_tables), bt_stride, _ptr(cu_seqlens), _ptr(kv_lens), _ptr(positions),
+        _ptr(row_map), _ptr(pool_lens), _ptr(nk), _ptr(nv),
+        nk.stride(0) if nk is not None else 0, nk.stride(1) if nk is not None else 0,
+        q_rows.shape[1], num_kv_heads, q_rows.shape[2], float(scale),
+        _ptr(plan.items), plan.n_narrow, plan.n_wide, _ptr(plan.merges), plan.n_merges,
+        plan.partials_floats, _stream(q_rows.device),
+    ), "mf_paged_attention_noalloc")
 
 
 def paged_attention_packed(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView, buf: torch.Tensor,

@@ -22,8 +22,10 @@
 // kernel combines them with the log-sum-exp rule.
 #include <algorithm>
 #include <array>
+#include <atomic>
 #include <climits>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -1700,4 +1702,75 @@ extern "C" int mf_paged_attention_counted(
                                 num_kv_heads, head_dim, scale, plan_items, capacity_narrow, capacity_wide,
                                 plan_merges, capacity_merges, partials, partials_floats, nullptr,
                                 device_counts, stream);
+}
+
+// ------------------------------------------------------- no-allocation entry
+//
+// mf_paged_attention for callers that cannot allocate device memory: the
+// split-K partials go to `scratch`, a library-owned device array that every
+// GPU holding this code object keeps until the process ends. In host code the
+// array's name is only a stand-in for the symbol; its device address, which
+// differs per GPU, comes from hipGetSymbolAddress on the first call on each
+// device and is the only form host code ever passes to a kernel. Nothing in
+// it needs clearing between calls (every partial slot is written before the
+// merge reads it), and calls that overlap on one GPU race on it.
+static __device__ __align__(256) float scratch[MF_NOALLOC_PARTIALS_FLOATS];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::atomic<float*> g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's `scratch`, looked up once per device.
+int scratch_for_current_device(float** out) {
+    int dev = -1;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) {
+        mf::set_last_hip_error((int)err);
+        return MF_ERR_HIP;
+    }
+    if (dev < 0 || dev >= kMaxScratchDevices) return MF_ERR_UNSUPPORTED;
+    float* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            void* addr = nullptr;
+            err = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+            if (err != hipSuccess || !addr) {
+                mf::set_last_hip_error((int)err);
+                return MF_ERR_HIP;
+            }
+            p = (float*)addr;
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return MF_OK;
+}
+}  // namespace
+
+extern "C" int mf_paged_attention_noalloc(
+    const void* q, int64_t q_stride_row, int64_t q_stride_head, void* out, int64_t out_stride_row,
+    int64_t out_stride_head, int dtype, const void* k_pool, const void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head, int block_size,
+    const int32_t* block_tables, int64_t block_table_stride, const int32_t* cu_seqlens,
+    const int32_t* kv_lens, const int64_t* positions, const int32_t* row_map,
+    const int32_t* pool_lens, const void* new_k, const void* new_v, int64_t new_stride_row,
+    int64_t new_stride_head, int num_q_heads, int num_kv_heads, int head_dim, float scale,
+    const int32_t* plan_items, int64_t num_items_narrow, int64_t num_items_wide,
+    const int32_t* plan_merges, int64_t num_merges, int64_t partials_floats, mf_stream_t stream) {
+    // sizes first: a plan that needs more than the array is refused before
+    // anything touches the device
+    if (partials_floats < 0) return MF_ERR_ARG;
+    if (partials_floats > MF_NOALLOC_PARTIALS_FLOATS) return MF_ERR_WORKSPACE;
+    float* partials = nullptr;
+    if (int st = scratch_for_current_device(&partials)) return st;
+    return paged_attention_impl(q, q_stride_row, q_stride_head, out, out_stride_row, out_stride_head, dtype,
+                                k_pool, v_pool, pool_stride_block, pool_stride_slot, pool_stride_head,
+                                block_size, block_tables, block_table_stride, cu_seqlens, kv_lens, positions,
+                                row_map, pool_lens, new_k, new_v, new_stride_row, new_stride_head, num_q_heads,
+                                num_kv_heads, head_dim, scale, plan_items, num_items_narrow, num_items_wide,
+                                plan_merges, num_merges, partials, MF_NOALLOC_PARTIALS_FLOATS, nullptr,
+                                nullptr, stream);
 }

@@ -373,3 +373,20 @@ def test_pack_rejects_rows_without_entries_and_bad_lengths_before_any_launch():
     assert call(tables=None) == -1    # a table length without a table
     assert call(tokens=None) == -1
     assert call(bs=0) == -1
+
+
+def test_noalloc_attention_refuses_oversized_plans_before_touching_the_device():
+    """mf_paged_attention_noalloc checks the plan's partials against its fixed
+    array (MF_NOALLOC_PARTIALS_FLOATS) first: too large is MF_ERR_WORKSPACE,
+    negative MF_ERR_ARG, with no device call (so this runs without a GPU)."""
+    L = nat.lib()
+
+    def call(floats):
+        return L.mf_paged_attention_noalloc(None, 64, 64, None, 64, 64, 2, None, None, 16 * 64, 64, 64, 16,
+                                            None, 4, None, None, None, None, None, None, None, 0, 0,
+                                            1, 1, 64, 0.125, None, 1, 0, None, 1, floats, None)
+
+    assert call(nat.NOALLOC_PARTIALS_FLOATS + 1) == -3
+    assert call(-1) == -1
+    m = re.search(r"#define MF_NOALLOC_PARTIALS_FLOATS \((\d+) \* 1024 \* 1024\)", HEADER.read_text())
+    assert m and nat.NOALLOC_PARTIALS_FLOATS == int(m.group(1)) << 20
