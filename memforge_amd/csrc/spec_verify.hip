@@ -444,17 +444,19 @@ __global__ __launch_bounds__(kPassThreads) void draw_kernel(VerifyArgs a) {
         for (int k = 0; k < 4; ++k) {
             const int e = base + u * kPassThreads * 4 + k;
             if (e >= a.V) continue;
+            // keys are correctly rounded quotients w / E, as torch.multinomial's
+            // exponential race forms them (one rounding, not a reciprocal
+            // and a product)
             const float p = tprob(x[u][k], e);
-            const float r = 1.f / en[u][k];
             if (reject) {
                 const float d = fmaxf(p - qq[u][k], 0.f);
                 any |= d > 0.f ? 1 : 0;
-                argmax_merge(best[0], best_i[0], d * r, e);
+                argmax_merge(best[0], best_i[0], d / en[u][k], e);
             }
             const float w = fmaxf(p, 0.f);
             any |= w > 0.f ? 2 : 0;
-            argmax_merge(best[1], best_i[1], w * r, e);
-            argmax_merge(best[2], best_i[2], r, e);
+            argmax_merge(best[1], best_i[1], w / en[u][k], e);
+            argmax_merge(best[2], best_i[2], 1.f / en[u][k], e);
         }
     const int64_t po = (int64_t)b * a.npass + c;
     const int64_t fam = (int64_t)a.B * a.npass;

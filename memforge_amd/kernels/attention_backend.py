@@ -75,7 +75,7 @@ class _VarlenBinding:
     """
 
     __slots__ = ("pool", "block_tables", "seq_ids", "positions", "block_wise", "used", "_meta",
-                 "pool_lens", "num_rows")
+                 "pool_lens", "num_rows", "timer")
 
     def __init__(self, pool, block_tables, seq_ids, positions, block_wise=False, pool_lens=None):
         self.pool = pool
@@ -87,6 +87,7 @@ class _VarlenBinding:
         self._meta = None
         self.pool_lens = pool_lens
         self.num_rows = len(self.seq_ids)
+        self.timer = None  # a sampled pass's event record (engine telemetry)
 
     @classmethod
     def from_packed(cls, pool, meta: dict, num_rows: int, pool_lens: Optional[torch.Tensor] = None):
@@ -100,6 +101,7 @@ class _VarlenBinding:
         b._meta = meta
         b.pool_lens = pool_lens
         b.num_rows = num_rows
+        b.timer = None
         return b
 
     def meta(self, num_q_heads: int, head_dim: int, dtype: torch.dtype, device) -> dict:
@@ -218,12 +220,16 @@ def _varlen_forward(module, query, key, value, scaling, binding: _VarlenBinding)
     if binding.pool_lens is not None:
         nk = key[0].to(dtype).permute(1, 0, 2)
         nv = value[0].to(dtype).permute(1, 0, 2)
+    timer = binding.timer
+    began = timer.start() if timer is not None else None
     nat.paged_attention(
         q_rows, out[0], pool.layer_view(layer), meta["block_tables"], meta["cu_seqlens"],
         meta["kv_lens"], meta["positions"], meta["plan"],
         scaling if scaling is not None else 1.0 / math.sqrt(d), pool.spec.num_kv_heads,
         row_map=meta["row_map"], pool_lens=binding.pool_lens, new_k_rows=nk, new_v_rows=nv,
     )
+    if timer is not None:
+        timer.stop("attention", began)
     return out.to(query.dtype)
 
 

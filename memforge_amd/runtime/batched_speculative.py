@@ -352,6 +352,17 @@ def verify_candidates_batched(target_model, pool, buffers, block_tables: Sequenc
     ``scatter_accepted_kv``, and the widest context. ``buffers`` (the
     reference's padded-batch scratch) is unused: nothing is padded here.
     """
+    logits, new_kv = verify_pass(target_model, pool, block_tables, context_lengths, query_tokens, device)
+    batch, query_len = logits.shape[0], logits.shape[1]
+    per_sequence_logits = [[logits[b, j] for j in range(query_len)] for b in range(batch)]
+    return per_sequence_logits, new_kv, max(int(c) for c in context_lengths)
+
+
+@torch.no_grad()
+def verify_pass(target_model, pool, block_tables: Sequence, context_lengths: Sequence[int],
+                query_tokens: Sequence[Sequence[int]], device: str) -> Tuple[torch.Tensor, List[Tuple[torch.Tensor, torch.Tensor]]]:
+    """``verify_candidates_batched`` with the logits as one ``(batch,
+    query_len, vocab)`` tensor (what the batched resolve consumes)."""
     batch = len(context_lengths)
     if batch == 0:
         raise ValueError("verify_candidates_batched requires at least one sequence")
@@ -380,13 +391,12 @@ def verify_candidates_batched(target_model, pool, buffers, block_tables: Sequenc
     if binding.used != num_layers:
         raise RuntimeError(f"verify pass: {binding.used} of {num_layers} layers used the varlen kernel")
     logits = out.logits[0].view(batch, query_len, -1)
-    per_sequence_logits = [[logits[b, j] for j in range(query_len)] for b in range(batch)]
     new_kv = []
     for k, v in cache.new_kv:
         hkv, d = k.shape[1], k.shape[3]
         new_kv.append((k[0].view(hkv, batch, query_len, d).permute(1, 0, 2, 3),
                        v[0].view(hkv, batch, query_len, d).permute(1, 0, 2, 3)))
-    return per_sequence_logits, new_kv, max(int(c) for c in context_lengths)
+    return logits, new_kv
 
 
 def resolve_round(seq_id: int, candidates: List[int], draft_probs: List[torch.Tensor],
@@ -421,6 +431,121 @@ def resolve_rounds_batched(seq_ids: Sequence[int], candidates: torch.Tensor, dra
     return [SpeculativeRound(seq_id=int(s), candidates=cand[b], accepted=tokens[b][: counts[b]],
                              is_draft=[bool(x) for x in flags[b][: counts[b]]], num_accepted_draft=nacc[b])
             for b, s in enumerate(seq_ids)]
+
+
+def resolve_rounds_global_rng(seq_ids: Sequence[int], candidates: Sequence[Sequence[int]],
+                              draft_probs: torch.Tensor, target_logits: torch.Tensor,
+                              temperatures: Sequence[float]) -> List[SpeculativeRound]:
+    """Every row of a speculative step resolved by ONE mf_spec_verify launch,
+    with the same outcome, row for row, as ``resolve_round`` applied to the
+    rows in order -- including what each consumes of torch's global
+    generators (memforge_ml/runtime/continuous_engine.py:1295-1311,
+    memforge_ml/speculative/rejection_sampler.py:28-83):
+
+    1. row b's target distribution is ``_probs_from_logits`` at its own
+       temperature over the draft's vocabulary width (the same torch softmax,
+       row by row);
+    2. the acceptance test needs p and q at each candidate, which cross to the
+       host in one copy; the host then walks the CPU generator's stream as the
+       reference does -- one uniform per examined candidate, row after row,
+       stopping a row at its first rejection -- by drawing the most a round can
+       use, replaying the walk, and re-drawing from the saved state exactly the
+       count the walk used (``torch.rand(n)`` is ``n`` draws of
+       ``torch.rand(1)`` on the CPU generator);
+    3. each row's final draw takes one Exp(1) vector of the vocabulary's size
+       from the GPU generator, in row order, as ``torch.multinomial`` would;
+    4. the kernel draws every row at once, with the host's accept decisions
+       passed in as forced uniforms (0 accepts, 2 rejects).
+
+    ``draft_probs`` is (B, K, V) fp32 and ``target_logits`` (B, K+1, >= V),
+    both on the GPU.
+    """
+    B = len(candidates)
+    if B == 0:
+        return []
+    K = len(candidates[0])
+    if any(len(c) != K for c in candidates):
+        raise ValueError("every row must carry the same number of candidates")
+    dev = target_logits.device
+    V = draft_probs.shape[-1] if K else target_logits.shape[-1]
+    logits = target_logits[..., :V].float()
+    probs = torch.empty((B, K + 1, V), dtype=torch.float32, device=dev)
+    groups: Dict[float, List[int]] = {}
+    for b, t in enumerate(temperatures):
+        groups.setdefault(float(t), []).append(b)
+    for t, rows in groups.items():
+        sel = logits if len(rows) == B else logits[rows]
+        p = _probs_from_logits_rows(sel.reshape(-1, V), t).view(len(rows), K + 1, V)
+        if len(rows) == B:
+            probs.copy_(p)
+        else:
+            probs[rows] = p
+    cand = torch.tensor(list(candidates), dtype=torch.int64).view(B, K).to(dev)
+    # (2) p and q at each candidate, one copy to the host
+    if K:
+        pq = torch.stack([probs[:, :K].gather(2, cand[..., None])[..., 0],
+                          draft_probs.gather(2, cand[..., None])[..., 0]]).cpu().double().tolist()
+    saved = torch.get_rng_state()
+    draws = torch.rand(B * K).tolist() if K else []
+    forced = np.full((B, K), 2.0, dtype=np.float32)
+    used = 0
+    for b in range(B):
+        for i in range(K):
+            r = draws[used]
+            used += 1
+            if r <= min(1.0, pq[0][b][i] / (pq[1][b][i] + 1e-9)):
+                forced[b, i] = 0.0
+            else:
+                break
+    torch.set_rng_state(saved)
+    if used:
+        torch.rand(used)
+    # (3) one Exp(1) vector per row on the GPU generator, in row order, each
+    # drawn into a fresh vocabulary-sized tensor exactly as multinomial's
+    # ``empty_like(p).exponential_(1)`` draws it
+    noise = torch.stack([torch.empty(V, dtype=torch.float32, device=dev).exponential_(1.0) for _ in range(B)])
+    # (4) one launch for every row
+    u = torch.from_numpy(forced).to(dev)
+    dp = draft_probs if K else torch.zeros((B, 0, V), dtype=torch.float32, device=dev)
+    res = nat.spec_verify(cand.to(torch.int32), dp, probs, 1.0, u, noise, target_is_probs=True)
+    out = torch.cat([res.tokens, res.is_draft.to(torch.int32), res.count[:, None],
+                     res.num_accepted[:, None]], dim=1).cpu().tolist()
+    rounds = []
+    for b, s in enumerate(seq_ids):
+        row = out[b]
+        n = row[2 * (K + 1)]
+        rounds.append(SpeculativeRound(seq_id=int(s), candidates=list(candidates[b]), accepted=row[:n],
+                                       is_draft=[bool(x) for x in row[K + 1:K + 1 + n]],
+                                       num_accepted_draft=row[2 * (K + 1) + 1]))
+    return rounds
+
+
+def confirmed_slot_mapping(tables: Sequence[Sequence[int]], context_lengths: Sequence[int],
+                           confirmed: Sequence[int], width: int, block_size: int) -> np.ndarray:
+    """Pool slots for a verify pass's packed rows (``width`` per sequence):
+    row j of sequence b goes to position ctx_b + j when j < confirmed[b], and
+    nowhere (slot -1) otherwise, so one KV write per layer stores exactly every
+    sequence's confirmed prefix (batched_speculative.py:780-811 for all rows)."""
+    slots = np.full((len(tables), width), -1, dtype=np.int64)
+    for b, (table, ctx, n) in enumerate(zip(tables, context_lengths, confirmed)):
+        if n <= 0:
+            continue
+        pos = np.arange(int(ctx), int(ctx) + int(n), dtype=np.int64)
+        blocks = np.asarray(table, dtype=np.int64)[pos // block_size]
+        slots[b, :n] = blocks * block_size + pos % block_size
+    return slots.reshape(-1)
+
+
+def scatter_confirmed_rows(pool, new_kv: Sequence[Tuple[torch.Tensor, torch.Tensor]],
+                           slots: torch.Tensor) -> None:
+    """One KV write per layer for every sequence's confirmed prefix:
+    ``new_kv`` as ``verify_candidates_batched`` returns it ((B, kv_heads, width,
+    head_dim) per layer), ``slots`` from ``confirmed_slot_mapping`` on the GPU."""
+    for layer_idx, (keys, values) in enumerate(new_kv):
+        B, H, W, D = keys.shape
+        rows_k = keys.permute(0, 2, 1, 3).reshape(B * W, H, D)
+        rows_v = values.permute(0, 2, 1, 3).reshape(B * W, H, D)
+        nat.kv_write(rows_k, rows_v, slots, pool.layer_view(layer_idx))
 
 
 def scatter_accepted_kv(pool, block_table: torch.Tensor, context_length: int,

@@ -24,8 +24,15 @@ model, because the varlen HIP kernel serves prefill chunks and decodes alike:
    sampling is one device argmax and one device-to-host copy per step.
 
 Speculative decoding (draft model + lookahead) verifies all candidate runs in
-one varlen pass with the candidates attended in flight, resolves them with the
-rejection sampler, and writes only the confirmed K/V.
+one varlen pass with the candidates attended in flight, resolves every row
+with one rejection-sampling launch (consuming torch's generators exactly as
+the per-row reference does), and writes every row's confirmed K/V with one
+KV-write launch per layer.
+
+Per-request bookkeeping works on runs of tokens: a pass commits each
+request's new tokens together (one token, or a speculative round's confirmed
+run), with one clock reading per step, and detokenises incrementally over a
+short window instead of re-decoding the whole output for every token.
 """
 
 from __future__ import annotations
@@ -36,7 +43,7 @@ import time
 import warnings
 from collections import deque
 from dataclasses import dataclass, field
-from typing import Any, Deque, Dict, List, Optional
+from typing import Any, Deque, Dict, List, Optional, Sequence
 
 import numpy as np
 import torch
@@ -47,11 +54,15 @@ from memforge_amd.runtime.batched_speculative import (
     BatchedGraphedDraftPool,
     BatchedGraphedDraftState,
     DraftState,
+    confirmed_slot_mapping,
     propose_draft_tokens,
     resolve_round,
+    resolve_rounds_global_rng,
     scatter_accepted_kv,
-    verify_candidates_batched,
+    scatter_confirmed_rows,
+    verify_pass,
 )
+from memforge_amd.runtime.engine_telemetry import DataPathMeter, device_figures
 from memforge_amd.runtime.graphed_paged_decode import GraphedPagedDecoder
 from memforge_amd.runtime.kv_pool import ModelKVSpec, PagedKVPool
 from memforge_amd.runtime.packed_pass import packed_forward
@@ -125,6 +136,10 @@ class SequenceRuntime:
     draft: Optional[DraftState] = None
     num_draft_proposed: int = 0
     num_draft_accepted: int = 0
+    # incremental detokenisation window: generated[text_from:] is what the
+    # next decode looks at, generated[text_from:text_to] what was already shown
+    text_from: int = 0
+    text_to: int = 0
 
     @property
     def done(self) -> bool:
@@ -155,6 +170,62 @@ class StepReport:
     events: List[TokenEvent]
 
 
+class _AbortRequests:
+    """Sequence ids another thread asked to abandon. The stepping thread takes
+    them all at the top of a step, so an abort never lands in the middle of one
+    (a step may be writing into the sequence's blocks)."""
+
+    __slots__ = ("_lock", "_ids")
+
+    def __init__(self) -> None:
+        self._lock = threading.Lock()
+        self._ids: set = set()
+
+    def add(self, seq_id: int) -> None:
+        with self._lock:
+            self._ids.add(seq_id)
+
+    def take(self) -> List[int]:
+        with self._lock:
+            ids, self._ids = self._ids, set()
+        return sorted(ids)
+
+    def __bool__(self) -> bool:
+        with self._lock:
+            return bool(self._ids)
+
+
+class _ThroughputWindow:
+    """Tokens emitted over the last ``seconds`` of activity, kept as one
+    (time, count) mark per commit instead of one timestamp per token. The rate
+    is tokens over the span from the oldest to the newest mark in the window."""
+
+    __slots__ = ("seconds", "_marks", "_count")
+
+    def __init__(self, seconds: float):
+        self.seconds = seconds
+        self._marks: Deque = deque()
+        self._count = 0
+
+    def mark(self, when: float, count: int) -> None:
+        if count:
+            self._marks.append((when, count))
+            self._count += count
+
+    def rate(self, now: float) -> float:
+        horizon = now - self.seconds
+        while self._marks and self._marks[0][0] < horizon:
+            self._count -= self._marks.popleft()[1]
+        if self._count < 2:
+            return 0.0
+        span = self._marks[-1][0] - self._marks[0][0]
+        return round(self._count / span, 2) if span > 0 else 0.0
+
+
+def _share(part: float, whole: float, digits: int) -> float:
+    return round(part / whole, digits) if whole else 0.0
+
+
 class ContinuousBatchingEngine:
     def __init__(self, model, tokenizer, *, block_size: int = 16, num_blocks: Optional[int] = None,
                  kv_budget_mb: float = 512.0, max_num_seqs: int = 16, max_model_len: int = 2048,
@@ -163,7 +234,8 @@ class ContinuousBatchingEngine:
                  decode_view_cache: bool = False, view_cache_budget_mb: float = 512.0,
                  block_attention: bool = False, max_prefill_tokens_per_step: int = 0,
                  draft_model=None, lookahead_k: int = 0, fused_prefill: bool = False,
-                 paged_attn_kernel: str = "gather", draft_cuda_graph=False, paged_cuda_graph=False):
+                 paged_attn_kernel: str = "gather", draft_cuda_graph=False, paged_cuda_graph=False,
+                 telemetry_sample_every: int = 16):
         if not HAS_CPP_ENGINE:
             raise RuntimeError("The native memforge_c extension is required; build it with "
                                "`python -m memforge_amd._build`")
@@ -233,34 +305,36 @@ class ContinuousBatchingEngine:
             self._draft_pool = BatchedGraphedDraftPool(
                 draft_model, max_len=max_model_len, num_slots=max_num_seqs, device=self.device,
                 unroll=draft_cuda_graph == "batched-unrolled")
+        # every speculative step resolves its rows with one kernel launch; the
+        # one-row-at-a-time form stays selectable for differential tests
+        self._batched_resolve = True
 
         self.eos_token_ids = self._resolve_eos_ids()
         self.runtimes: Dict[int, SequenceRuntime] = {}
         self._next_seq_id = 1
         self._step_index = 0
-        self.total_tokens_generated = 0
-        self.total_prefill_tokens = 0
-        self.total_steps = 0
-        self.total_forward_passes = 0
-        self.total_preemptions = 0
-        self.total_cached_prefix_tokens = 0
-        self.total_cow_copies = 0
-        self.total_prefill_chunks = 0
-        self.total_fused_steps = 0
-        self.total_fused_tokens = 0
-        self.total_draft_tokens_proposed = 0
-        self.total_draft_tokens_accepted = 0
-        self.total_speculative_rounds = 0
-        self.total_speculative_sequence_rounds = 0
-        self.total_blockwise_layers = 0
-        self.total_blockwise_fallbacks = 0
-        self.total_attended_kv_tokens = 0  # sum over passes of every sequence's kv length
-        self.total_packed_rows = 0  # query rows through the model (prefill + decode + verify)
+        for name in ("total_tokens_generated", "total_prefill_tokens", "total_steps", "total_forward_passes",
+                     "total_preemptions", "total_cached_prefix_tokens", "total_cow_copies",
+                     "total_prefill_chunks", "total_fused_steps", "total_fused_tokens",
+                     "total_draft_tokens_proposed", "total_draft_tokens_accepted", "total_speculative_rounds",
+                     "total_speculative_sequence_rounds", "total_blockwise_layers", "total_blockwise_fallbacks",
+                     # sum over passes of every sequence's kv length / of packed query rows
+                     "total_attended_kv_tokens", "total_packed_rows"):
+            setattr(self, name, 0)
         self.engine_started_at = time.perf_counter()
-        self._abort_lock = threading.Lock()
-        self._pending_aborts: set = set()
-        self.throughput_window_s = 5.0
-        self._recent_tokens: Deque[float] = deque()
+        self._aborts = _AbortRequests()
+        self._throughput = _ThroughputWindow(5.0)
+        weight_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
+        self._meter = DataPathMeter(self.spec, model.config.num_attention_heads, block_size, weight_bytes,
+                                    every=telemetry_sample_every)
+
+    @property
+    def throughput_window_s(self) -> float:
+        return self._throughput.seconds
+
+    @throughput_window_s.setter
+    def throughput_window_s(self, seconds: float) -> None:
+        self._throughput.seconds = float(seconds)
 
     # ------------------------------------------------------------------ setup
 
@@ -299,6 +373,14 @@ class ContinuousBatchingEngine:
             "chunked_prefill": self.max_prefill_tokens_per_step > 0,
             "eos_token_ids": sorted(self.eos_token_ids),
             "kv_pool": self.pool.describe(),
+            "data_path": {
+                "library": nat.LIB_PATH.name,
+                "arch": "gfx950",
+                "step": "one packed varlen pass (ragged pack, per-layer KV write and paged attention)",
+                "speculative_resolve": "one mf_spec_verify launch per round" if self._batched_resolve
+                                       else "one row at a time",
+                "telemetry_sample_every": self._meter.every,
+            },
         }
 
     # ------------------------------------------------------------- submission
@@ -328,32 +410,26 @@ class ContinuousBatchingEngine:
         return seq_id
 
     def abort(self, seq_id: int) -> bool:
-        """Request abandonment from any thread; applied at the top of the next step."""
+        """Ask, from any thread, for a running request to be abandoned; it is
+        applied at the top of the next step. False if it is unknown or done."""
         rt = self.runtimes.get(seq_id)
         if rt is None or rt.done:
             return False
-        with self._abort_lock:
-            self._pending_aborts.add(seq_id)
+        self._aborts.add(seq_id)
         return True
 
     def _process_pending_aborts(self) -> None:
-        with self._abort_lock:
-            if not self._pending_aborts:
-                return
-            pending, self._pending_aborts = self._pending_aborts, set()
-        for seq_id in pending:
+        for seq_id in self._aborts.take():
             rt = self.runtimes.get(seq_id)
-            if rt is None or rt.done:
-                continue
-            self.scheduler.abort_sequence(seq_id)
-            self._finish(rt, "aborted")
+            if rt is not None and not rt.done:
+                self.scheduler.abort_sequence(seq_id)
+                self._finish(rt, "aborted")
 
     # ------------------------------------------------------------------ steps
 
     def has_work(self) -> bool:
-        with self._abort_lock:
-            if self._pending_aborts:
-                return True
+        if self._aborts:
+            return True
         return self.scheduler.has_unfinished_sequences() or any(not rt.done for rt in self.runtimes.values())
 
     @property
@@ -403,12 +479,17 @@ class ContinuousBatchingEngine:
             else:
                 plan.append({"rt": rt, "kind": "decode", "tokens": [rt.tokens[-1]],
                              "start": rt.cache.position, "table": rt.cache.block_table})
-        if plan and n_prefill == 0 and self._paged_graph is not None:
-            events.extend(self._run_graphed(plan))
-        elif plan:
-            events.extend(self._run_packed(plan))
-            if n_prefill and len(plan) > n_prefill:
-                self.total_fused_steps += 1
+        if plan:
+            # a sampled step is timed the way it runs: kernel by kernel when
+            # eager, as a whole replay when graphed (sampling never changes
+            # which path a step takes, so it never changes the results)
+            sampled = self._meter.arm()
+            if n_prefill == 0 and self._paged_graph is not None:
+                events.extend(self._run_graphed(plan, sampled))
+            else:
+                events.extend(self._run_packed(plan, sampled))
+                if n_prefill and len(plan) > n_prefill:
+                    self.total_fused_steps += 1
         if spec_rts:
             events.extend(self._run_speculative(spec_rts))
 
@@ -478,16 +559,20 @@ class ContinuousBatchingEngine:
 
     # ------------------------------------------------------------ packed pass
 
-    def _run_packed(self, plan: List[dict]) -> List[TokenEvent]:
+    def _run_packed(self, plan: List[dict], sampled: bool = False) -> List[TokenEvent]:
         """One forward over every entry of ``plan`` (prefill chunks, then decodes)."""
         q_lens = [len(e["tokens"]) for e in plan]
         cu = np.concatenate([[0], np.cumsum(q_lens)])
         # only rows that produce a token go through the LM head
         emit = [i for i, e in enumerate(plan) if e["kind"] == "decode" or e["is_final"]]
+        timer = None
+        if sampled:
+            kv = [e["start"] + n for e, n in zip(plan, q_lens)]
+            timer = self._meter.begin("eager", self._meter.layer_bytes(kv, int(cu[-1])))
         try:
             res = packed_forward(self.model, self.pool, [e["tokens"] for e in plan],
                                  [e["start"] for e in plan], [e["table"] for e in plan],
-                                 [int(cu[i + 1]) - 1 for i in emit])
+                                 [int(cu[i + 1]) - 1 for i in emit], timer=timer)
         except IndexError as exc:
             raise IndexError(f"{exc} (sequences {[e['rt'].seq_id for e in plan]})") from None
         self.total_forward_passes += 1
@@ -497,10 +582,17 @@ class ContinuousBatchingEngine:
         self.total_packed_rows += res.num_tokens
         return self._emit(plan, emit, res.logits)
 
-    def _run_graphed(self, plan: List[dict]) -> List[TokenEvent]:
+    def _run_graphed(self, plan: List[dict], sampled: bool = False) -> List[TokenEvent]:
         """A decode-only step as one replay of the captured packed pass."""
         ctx = [e["start"] for e in plan]
+        timer = began = None
+        if sampled:
+            nbytes = self._meter.step_bytes([c + 1 for c in ctx], len(plan))
+            timer = self._meter.begin("graph", {"decode_graph": nbytes})
+            began = timer.start()
         logits = self._paged_graph.logits_view([e["tokens"][0] for e in plan], ctx, [e["table"] for e in plan])
+        if timer is not None:
+            timer.stop("decode_graph", began)
         self.total_forward_passes += 1
         self.total_blockwise_layers += self.spec.num_layers
         self.total_fused_tokens += len(plan)
@@ -527,9 +619,10 @@ class ContinuousBatchingEngine:
                     row = row.cpu()
                 tokens[j] = sample_logits(row, rt.params, rt.generator)
 
+        now = time.perf_counter()
         events: List[TokenEvent] = []
         j = 0
-        for i, entry in enumerate(plan):
+        for entry in plan:
             rt = entry["rt"]
             if entry["kind"] == "prefill":
                 rt.cache.position = entry["chunk_end"]
@@ -542,10 +635,8 @@ class ContinuousBatchingEngine:
                     self.prefix_cache.register_full_blocks(rt.tokens, entry["table"])
             else:
                 rt.cache.position += 1
-            ev = self._accept_token(rt, tokens[j], source="target")
+            events.extend(self._commit(rt, (tokens[j],), ("target",), now))
             j += 1
-            if ev is not None:
-                events.append(ev)
         return events
 
     # ----------------------------------------------------- speculative decode
@@ -556,13 +647,11 @@ class ContinuousBatchingEngine:
             return False
         return len(rt.generated) + span <= rt.params.max_new_tokens
 
-    def _run_speculative(self, rts: List[SequenceRuntime]) -> List[TokenEvent]:
-        """Draft proposals, one batched verify pass, rejection, confirmed-prefix
-        write (continuous_engine.py:1212-1341)."""
+    def _propose(self, rts: List[SequenceRuntime]):
+        """Every row's K draft candidates and their draft distributions."""
         k = self.lookahead_k
         proposals: List[List[int]] = [[] for _ in rts]
         draft_probs: List[List[torch.Tensor]] = [[] for _ in rts]
-        token_counts = [len(rt.tokens) for rt in rts]
         for rt in rts:
             if rt.draft is None:
                 rt.draft = self._draft_pool.acquire() if self._draft_pool is not None else DraftState()
@@ -581,38 +670,74 @@ class ContinuousBatchingEngine:
             for row, rt in enumerate(rts):
                 proposals[row], draft_probs[row] = propose_draft_tokens(
                     self.draft_model, rt.draft, rt.tokens, k, rt.params.temperature, self.device)
+        return proposals, draft_probs
+
+    def _run_speculative(self, rts: List[SequenceRuntime]) -> List[TokenEvent]:
+        """Draft proposals, one batched verify pass, rejection, confirmed-prefix
+        write (continuous_engine.py:1212-1341)."""
+        k = self.lookahead_k
+        proposals, draft_probs = self._propose(rts)
+        token_counts = [len(rt.tokens) for rt in rts]
         ctx = [rt.cache.position for rt in rts]
-        tables = [rt.cache.block_table_tensor(self.device) for rt in rts]
+        tables = [list(rt.cache.block_table) for rt in rts]
         queries = [[rt.tokens[-1]] + cand for rt, cand in zip(rts, proposals)]
-        logits, new_kv, _ = verify_candidates_batched(self.model, self.pool, None, tables, ctx, queries, self.device)
+        logits, new_kv = verify_pass(self.model, self.pool, tables, ctx, queries, self.device)
         self.total_forward_passes += 1
         self.total_attended_kv_tokens += sum(c + k + 1 for c in ctx)
         self.total_packed_rows += (k + 1) * len(rts)
         self.total_speculative_rounds += 1
         self.total_speculative_sequence_rounds += len(rts)
+        if not self._batched_resolve:
+            return self._resolve_rows_one_by_one(rts, proposals, draft_probs, logits, new_kv, ctx, token_counts)
+
+        rounds = resolve_rounds_global_rng(
+            [rt.seq_id for rt in rts], proposals,
+            torch.stack([torch.stack(p) for p in draft_probs]).float(), logits,
+            [rt.params.temperature for rt in rts])
+        now = time.perf_counter()
+        events: List[TokenEvent] = []
+        confirmed: List[int] = []
+        for rt, rnd in zip(rts, rounds):
+            got = self._commit(rt, rnd.accepted, ["draft" if f else "target" for f in rnd.is_draft], now)
+            events.extend(got)
+            self._count_round(rt, rnd)
+            # a request that stopped has no use for its K/V (its blocks go
+            # back to the allocator on the next step): nothing is written
+            confirmed.append(0 if rt.done else len(got))
+        if any(confirmed):
+            slots = confirmed_slot_mapping(tables, ctx, confirmed, k + 1, self.block_size)
+            scatter_confirmed_rows(self.pool, new_kv, nat.upload([slots], self.device)[0])
+        for rt, rnd, n, count in zip(rts, rounds, confirmed, token_counts):
+            if not rt.done:
+                rt.cache.position += n
+                rt.draft.rollback_to(count + rnd.num_accepted_draft)
+        return events
+
+    def _resolve_rows_one_by_one(self, rts, proposals, draft_probs, logits, new_kv, ctx, token_counts):
+        """The per-row form of the same step: ``resolve_round`` and
+        ``scatter_accepted_kv`` for one row after the other."""
         events: List[TokenEvent] = []
         for row, rt in enumerate(rts):
-            round_ = resolve_round(rt.seq_id, proposals[row], draft_probs[row],
-                                   [x.float() for x in logits[row]], rt.params.temperature)
-            confirmed = 0
-            for position, token_id in enumerate(round_.accepted):
-                source = "draft" if round_.is_draft[position] else "target"
-                ev = self._accept_token(rt, token_id, source=source)
-                confirmed += 1
-                if ev is not None:
-                    events.append(ev)
-                if rt.done:
-                    break
-            rt.num_draft_proposed += len(round_.candidates)
-            rt.num_draft_accepted += round_.num_accepted_draft
-            self.total_draft_tokens_proposed += len(round_.candidates)
-            self.total_draft_tokens_accepted += round_.num_accepted_draft
+            rnd = resolve_round(rt.seq_id, proposals[row], draft_probs[row],
+                                [x.float() for x in logits[row]], rt.params.temperature)
+            table = rt.cache.block_table_tensor(self.device)
+            got = self._commit(rt, rnd.accepted, ["draft" if f else "target" for f in rnd.is_draft],
+                               time.perf_counter())
+            events.extend(got)
+            self._count_round(rt, rnd)
             if rt.done:
                 continue
-            scatter_accepted_kv(self.pool, tables[row], ctx[row], new_kv, row, confirmed)
-            rt.cache.position += confirmed
-            rt.draft.rollback_to(token_counts[row] + round_.num_accepted_draft)
+            scatter_accepted_kv(self.pool, table, ctx[row], new_kv, row, len(got))
+            rt.cache.position += len(got)
+            rt.draft.rollback_to(token_counts[row] + rnd.num_accepted_draft)
         return events
+
+    def _count_round(self, rt: SequenceRuntime, rnd) -> None:
+        proposed = len(rnd.candidates)
+        rt.num_draft_proposed += proposed
+        rt.num_draft_accepted += rnd.num_accepted_draft
+        self.total_draft_tokens_proposed += proposed
+        self.total_draft_tokens_accepted += rnd.num_accepted_draft
 
     # ------------------------------------------------------------ bookkeeping
 
@@ -621,31 +746,59 @@ class ContinuousBatchingEngine:
             self._draft_pool.release(rt.draft)
         rt.draft = None
 
-    def _accept_token(self, rt: SequenceRuntime, token_id: int, source: str) -> Optional[TokenEvent]:
-        now = time.perf_counter()
+    def _commit(self, rt: SequenceRuntime, token_ids: Sequence[int], sources: Sequence[str],
+                now: float) -> List[TokenEvent]:
+        """Append a run of tokens to one request -- one token from a packed
+        pass, or a speculative round's confirmed run -- up to the first that
+        ends it: an end-of-sequence token (when the request stops on EOS) or
+        the one that spends its token budget. Every appended token is reported
+        to the scheduler and gets an event with its new text. Returns the
+        events, one per appended token."""
+        if rt.done or not token_ids:
+            return []
         if rt.first_token_at is None:
             rt.first_token_at = now
-        rt.tokens.append(token_id)
-        rt.generated.append(token_id)
-        rt.sources.append(source)
-        self.total_tokens_generated += 1
-        self._recent_tokens.append(now)
-        is_eos = rt.params.stop_on_eos and token_id in self.eos_token_ids
-        hit_limit = len(rt.generated) >= rt.params.max_new_tokens
-        self.scheduler.update_sequence(rt.seq_id, token_id, bool(is_eos))
-        event = TokenEvent(seq_id=rt.seq_id, index=len(rt.generated) - 1, token_id=token_id,
-                           text=self._decode_delta(rt), source=source)
-        rt.events.append(event)
-        if is_eos:
-            self._finish(rt, "stop")
-        elif hit_limit:
-            self._finish(rt, "length")
-        return event
+        budget = rt.params.max_new_tokens
+        stop_ids = self.eos_token_ids if rt.params.stop_on_eos else ()
+        produced: List[TokenEvent] = []
+        reason = None
+        for token_id, source in zip(token_ids, sources):
+            token_id = int(token_id)
+            ends = token_id in stop_ids
+            rt.tokens.append(token_id)
+            rt.generated.append(token_id)
+            rt.sources.append(source)
+            self.scheduler.update_sequence(rt.seq_id, token_id, ends)
+            produced.append(TokenEvent(seq_id=rt.seq_id, index=len(rt.generated) - 1, token_id=token_id,
+                                       text=self._text_delta(rt), source=source))
+            if ends:
+                reason = "stop"
+            elif len(rt.generated) >= budget:
+                reason = "length"
+            if reason:
+                break
+        rt.events.extend(produced)
+        self.total_tokens_generated += len(produced)
+        self._throughput.mark(now, len(produced))
+        if reason:
+            self._finish(rt, reason)
+        return produced
 
-    def _decode_delta(self, rt: SequenceRuntime) -> str:
-        full = self.tokenizer.decode(rt.generated, skip_special_tokens=True)
-        delta = full[rt.decoded_chars:]
-        rt.decoded_chars = len(full)
+    def _text_delta(self, rt: SequenceRuntime) -> str:
+        """The text the newest token adds, decoded over a short window:
+        generated[text_from:] against generated[text_from:text_to], the part
+        already shown. A window ending in an incomplete character (U+FFFD)
+        shows nothing yet; the character appears with the token that completes
+        it. Decoding from the window's start token on both sides keeps the
+        tokenizer's own handling of leading spaces, so the deltas add up to
+        the full decode."""
+        shown = self.tokenizer.decode(rt.generated[rt.text_from:rt.text_to], skip_special_tokens=True)
+        window = self.tokenizer.decode(rt.generated[rt.text_from:], skip_special_tokens=True)
+        if len(window) <= len(shown) or window.endswith("\ufffd"):
+            return ""
+        rt.text_from, rt.text_to = rt.text_to, len(rt.generated)
+        delta = window[len(shown):]
+        rt.decoded_chars += len(delta)
         return delta
 
     def _finish(self, rt: SequenceRuntime, reason: str) -> None:
@@ -660,113 +813,91 @@ class ContinuousBatchingEngine:
 
     def result_for(self, seq_id: int) -> Dict[str, Any]:
         rt = self.runtimes[seq_id]
-        elapsed = (rt.finished_at or time.perf_counter()) - rt.submitted_at
-        ttft = (rt.first_token_at - rt.submitted_at) if rt.first_token_at else None
+        end = rt.finished_at if rt.finished_at is not None else time.perf_counter()
+        elapsed = end - rt.submitted_at
+        first = None if rt.first_token_at is None else rt.first_token_at - rt.submitted_at
+        made = len(rt.generated)
         return {
             "seq_id": seq_id,
             "prompt_tokens": rt.prompt_len,
-            "generated_tokens": len(rt.generated),
+            "generated_tokens": made,
             "text": self.tokenizer.decode(rt.generated, skip_special_tokens=True),
-            "token_ids": list(rt.generated),
-            "token_sources": list(rt.sources),
+            "token_ids": rt.generated[:],
+            "token_sources": rt.sources[:],
             "finish_reason": rt.finish_reason,
-            "time_to_first_token_ms": round(ttft * 1000, 2) if ttft else None,
+            "time_to_first_token_ms": round(first * 1e3, 2) if first else None,
             "total_time_s": round(elapsed, 4),
-            "tokens_per_second": round(len(rt.generated) / elapsed, 2) if elapsed > 0 else 0.0,
+            "tokens_per_second": round(made / elapsed, 2) if elapsed > 0 else 0.0,
             "num_prefills": rt.num_prefills,
             "num_preemptions": rt.num_preemptions,
         }
 
     def drain_events(self, seq_id: int) -> List[TokenEvent]:
+        """Hand over (and forget) the request's events not yet drained."""
         rt = self.runtimes[seq_id]
-        out = list(rt.events)
-        rt.events.clear()
-        return out
+        pending, rt.events = rt.events, deque()
+        return list(pending)
 
     def recent_tokens_per_second(self) -> float:
-        cutoff = time.perf_counter() - self.throughput_window_s
-        while self._recent_tokens and self._recent_tokens[0] < cutoff:
-            self._recent_tokens.popleft()
-        if len(self._recent_tokens) < 2:
-            return 0.0
-        span = self._recent_tokens[-1] - self._recent_tokens[0]
-        return round(len(self._recent_tokens) / span, 2) if span > 0 else 0.0
+        return self._throughput.rate(time.perf_counter())
 
-    def _device_telemetry(self) -> Dict[str, Any]:
-        """Where the pool lives and what the device holds (continuous_engine.py:1432-1483)."""
-        pool = self.pool.describe()
-        mb = 1024 * 1024
-        free_bytes, total_bytes = torch.cuda.mem_get_info()
+    def _counters(self, uptime: float) -> Dict[str, Any]:
+        spec_rounds = self.total_speculative_rounds
         return {
-            "device": pool["device"],
-            "dtype": pool["dtype"],
-            "num_blocks": pool["num_blocks"],
-            "block_size": pool["block_size"],
-            "capacity_tokens": pool["capacity_tokens"],
-            "pool_mb": pool["total_mb"],
-            "cuda_available": True,
-            "device_name": torch.cuda.get_device_name(0),
-            "allocated_mb": round(torch.cuda.memory_allocated() / mb, 2),
-            "peak_memory_mb": round(torch.cuda.max_memory_allocated() / mb, 2),
-            "reserved_mb": round(torch.cuda.memory_reserved() / mb, 2),
-            "vram_total_mb": round(total_bytes / mb, 2),
-            "vram_free_mb": round(free_bytes / mb, 2),
-        }
-
-    def telemetry(self) -> Dict[str, Any]:
-        uptime = time.perf_counter() - self.engine_started_at
-        free = self.allocator.get_num_free_blocks()
-        total = self.allocator.get_total_blocks()
-        sharing = sharing_telemetry(self.allocator, self.pool, self.prefix_cache, owners=self.block_owners())
-        return {
-            **sharing,
-            **self._device_telemetry(),
             "uptime_s": round(uptime, 2),
             "steps": self.total_steps,
             "forward_passes": self.total_forward_passes,
             "tokens_generated": self.total_tokens_generated,
             "prefill_tokens": self.total_prefill_tokens,
             "tokens_per_second": self.recent_tokens_per_second(),
-            "lifetime_tokens_per_second": round(self.total_tokens_generated / uptime, 2) if uptime > 0 else 0.0,
-            "tokens_per_forward_pass": (round(self.total_tokens_generated / self.total_forward_passes, 3)
-                                        if self.total_forward_passes else 0.0),
-            "active_sequences": sum(1 for rt in self.runtimes.values() if not rt.done),
+            "lifetime_tokens_per_second": _share(self.total_tokens_generated, uptime, 2),
+            "tokens_per_forward_pass": _share(self.total_tokens_generated, self.total_forward_passes, 3),
+            "active_sequences": sum(not rt.done for rt in self.runtimes.values()),
             "waiting_sequences": self.scheduler.get_num_waiting(),
             "running_sequences": self.scheduler.get_num_running(),
             "preemptions": self.total_preemptions,
             "cached_prefix_tokens": self.total_cached_prefix_tokens,
             "cow_copies": self.total_cow_copies,
             "prefill_chunks": self.total_prefill_chunks,
-            "fused_prefill_enabled": True,
             "fused_steps": self.total_fused_steps,
             "fused_tokens": self.total_fused_tokens,
-            "chunked_prefill_enabled": self.max_prefill_tokens_per_step > 0,
-            "max_prefill_tokens_per_step": self.max_prefill_tokens_per_step,
-            "speculation_enabled": self.speculation_enabled,
-            "lookahead_k": self.lookahead_k,
-            "speculative_rounds": self.total_speculative_rounds,
-            "speculative_sequences_per_round": (round(self.total_speculative_sequence_rounds
-                                                      / self.total_speculative_rounds, 3)
-                                                if self.total_speculative_rounds else 0.0),
+            "speculative_rounds": spec_rounds,
+            "speculative_sequences_per_round": _share(self.total_speculative_sequence_rounds, spec_rounds, 3),
             "draft_tokens_proposed": self.total_draft_tokens_proposed,
             "draft_tokens_accepted": self.total_draft_tokens_accepted,
-            "draft_acceptance_rate": (round(self.total_draft_tokens_accepted / self.total_draft_tokens_proposed, 4)
-                                      if self.total_draft_tokens_proposed else 0.0),
-            "decode_view_cache_enabled": False,
-            "block_attention_enabled": True,
-            "paged_cuda_graph_enabled": self._paged_graph is not None,
-            "graph_replays": self._paged_graph.replays if self._paged_graph is not None else 0,
-            "graph_captures": self._paged_graph.captures if self._paged_graph is not None else 0,
-            "draft_graph_enabled": self._draft_pool is not None,
-            "draft_graph_replays": self._draft_pool.replays if self._draft_pool is not None else 0,
+            "draft_acceptance_rate": _share(self.total_draft_tokens_accepted, self.total_draft_tokens_proposed, 4),
             "blockwise_layer_calls": self.total_blockwise_layers,
             "blockwise_fallbacks": self.total_blockwise_fallbacks,
             "attended_kv_tokens": self.total_attended_kv_tokens,
             "packed_rows": self.total_packed_rows,
+        }
+
+    def _features(self) -> Dict[str, Any]:
+        graph, drafts = self._paged_graph, self._draft_pool
+        return {
+            "fused_prefill_enabled": True,
+            "chunked_prefill_enabled": self.max_prefill_tokens_per_step > 0,
+            "max_prefill_tokens_per_step": self.max_prefill_tokens_per_step,
+            "speculation_enabled": self.speculation_enabled,
+            "lookahead_k": self.lookahead_k,
+            "decode_view_cache_enabled": False,
+            "block_attention_enabled": True,
+            "paged_cuda_graph_enabled": graph is not None,
+            "graph_replays": graph.replays if graph is not None else 0,
+            "graph_captures": graph.captures if graph is not None else 0,
+            "draft_graph_enabled": drafts is not None,
+            "draft_graph_replays": drafts.replays if drafts is not None else 0,
+            # the reference's decode mirror is not built: its figures stay at zero
             "view_cache_mb_in_use": 0.0,
             "view_cache_budget_mb": 0.0,
             "view_cache_grants": 0,
             "view_cache_denials": 0,
+        }
+
+    def _pool_figures(self) -> Dict[str, Any]:
+        total = self.allocator.get_total_blocks()
+        free = self.allocator.get_num_free_blocks()
+        return {
             "total_blocks": total,
             "free_blocks": free,
             "allocated_blocks": total - free,
@@ -775,17 +906,31 @@ class ContinuousBatchingEngine:
             "kv_pool_mb": self.pool.describe()["total_mb"],
         }
 
+    def telemetry(self) -> Dict[str, Any]:
+        """Every figure a dashboard reads, under the reference's keys
+        (continuous_engine.py:1485-1569), plus the measured data-path
+        bandwidth (attention, KV write and graph-replayed decode steps)."""
+        figures: Dict[str, Any] = {}
+        figures.update(sharing_telemetry(self.allocator, self.pool, self.prefix_cache, owners=self.block_owners()))
+        figures.update(device_figures(self.pool))
+        figures.update(self._counters(time.perf_counter() - self.engine_started_at))
+        figures.update(self._features())
+        figures.update(self._pool_figures())
+        figures.update(self._meter.snapshot())
+        return figures
+
     def _live_block_tables(self) -> List[Any]:
         return [(seq_id, rt.cache.block_table) for seq_id, rt in self.runtimes.items()
                 if not rt.done and rt.cache is not None]
 
     def block_occupancy(self) -> List[int]:
-        occupancy = [0] * self.allocator.get_total_blocks()
+        """Owner of every physical block (0 = none), one owner per block:
+        where tables share a block, the last live request listed holds it."""
+        owner = np.zeros(self.allocator.get_total_blocks(), dtype=np.int64)
         for seq_id, table in self._live_block_tables():
-            for block_id in table:
-                if 0 <= block_id < len(occupancy):
-                    occupancy[block_id] = seq_id
-        return occupancy
+            ids = np.asarray(table, dtype=np.int64)
+            owner[ids[(ids >= 0) & (ids < owner.size)]] = seq_id
+        return owner.tolist()
 
     def block_owners(self) -> Dict[str, List[int]]:
         return block_owners(self._live_block_tables(), self.allocator.get_total_blocks())
@@ -793,15 +938,14 @@ class ContinuousBatchingEngine:
     # ------------------------------------------------------- blocking helpers
 
     def run_until_idle(self, max_steps: int = 100_000) -> List[StepReport]:
-        reports = []
-        steps = 0
-        while self.has_work() and steps < max_steps:
+        reports: List[StepReport] = []
+        while len(reports) < max_steps and self.has_work():
             reports.append(self.step())
-            steps += 1
         return reports
 
     def generate(self, prompts, params: Optional[SamplingParams] = None) -> List[Dict[str, Any]]:
-        prompt_list = [prompts] if isinstance(prompts, str) else list(prompts)
-        ids = [self.submit(p, params) for p in prompt_list]
+        """Submit one prompt or many, step until all are done, return their results."""
+        batch = (prompts,) if isinstance(prompts, str) else tuple(prompts)
+        ids = [self.submit(prompt, params) for prompt in batch]
         self.run_until_idle()
-        return [self.result_for(i) for i in ids]
+        return list(map(self.result_for, ids))

@@ -150,4 +150,10 @@ class PagedKVPool:
             "head_dim": self.spec.head_dim,
             "dtype": str(self.spec.dtype),
             "device": self.spec.device,
+            # how the kernels address it: one layer of one pool tensor is
+            # blocks x block_size x kv_heads x head_dim, head_dim contiguous
+            "layout": "(layers, blocks, block_size, kv_heads, head_dim)",
+            "element_bytes": self.key_pool.element_size(),
+            "block_table_dtype": "int32",
+            "slot_mapping_dtype": "int64",
         }

@@ -35,11 +35,13 @@ class PackedPassResult:
 
 @torch.no_grad()
 def packed_forward(model, pool, tokens: Sequence[Sequence[int]], starts: Sequence[int],
-                   tables: Sequence[Sequence[int]], keep_rows: Sequence[int]) -> PackedPassResult:
+                   tables: Sequence[Sequence[int]], keep_rows: Sequence[int], timer=None) -> PackedPassResult:
     """Run ``model`` once over every sequence's ``tokens`` (written at
     ``starts[i]`` onward through ``tables[i]``) and return the logits of the
     packed rows ``keep_rows``. Raises IndexError when a run does not fit its
-    table, and RuntimeError when a layer did not use the varlen kernel."""
+    table, and RuntimeError when a layer did not use the varlen kernel. With
+    ``timer`` (a sampled pass's event record) every layer's KV write and
+    attention launch is bracketed by HIP events."""
     bs = pool.block_size
     spec = pool.spec
     B = len(tokens)
@@ -79,6 +81,7 @@ def packed_forward(model, pool, tokens: Sequence[Sequence[int]], starts: Sequenc
             "plan": attn_plan}
     binding = attention_backend._VarlenBinding.from_packed(pool, meta, T)
     cache = VarlenPackedCache.from_slot_mapping(pool, spec.num_layers, packed.slot_mapping)
+    binding.timer = cache.timer = timer
     with attention_backend.backend_enabled_on(model) as routed:
         if not routed:
             raise RuntimeError("the packed pass needs the attention registry")

@@ -6,6 +6,7 @@ prefix_sharing.py:27-140). Which blocks are shared is decided by the C++
 
 from __future__ import annotations
 
+import itertools
 from typing import Any, Dict, Iterable, List, Optional, Sequence, Tuple
 
 from memforge_amd import _native
@@ -33,15 +34,12 @@ def copy_blocks(pool: PagedKVPool, pairs: Sequence[Tuple[int, int]]) -> None:
 
 def block_owners(runtimes: Iterable[Tuple[int, List[int]]], total_blocks: int) -> Dict[str, List[int]]:
     """Every in-range physical block mapped to all sequences whose table holds
-    it, owners sorted; keys are strings (JSON)."""
-    owners: Dict[str, List[int]] = {}
-    for seq_id, table in runtimes:
-        for block_id in table:
-            if 0 <= block_id < total_blocks:
-                owners.setdefault(str(block_id), []).append(seq_id)
-    for ids in owners.values():
-        ids.sort()
-    return owners
+    it (a sequence once per table entry), owners sorted; keys are the block
+    ids as strings (JSON), in block order."""
+    holdings = sorted((int(b), int(seq_id)) for seq_id, table in runtimes for b in table
+                      if 0 <= int(b) < total_blocks)
+    return {str(block): [seq for _, seq in group]
+            for block, group in itertools.groupby(holdings, key=lambda h: h[0])}
 
 
 def sharing_telemetry(allocator: Any, pool: PagedKVPool, prefix_cache: Optional[Any],

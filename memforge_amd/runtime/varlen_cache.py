@@ -51,7 +51,11 @@ class VarlenPackedCacheLayer(CacheLayerMixin):
         if self.owner.hold_new_kv:
             self.owner.new_kv[self.layer_idx] = (key_states, value_states)
         else:
+            timer = self.owner.timer
+            began = timer.start() if timer is not None else None
             self.owner.pool.write_flat(self.layer_idx, self.owner.write_index, key_states, value_states)
+            if timer is not None:
+                timer.stop("kv_write", began)
         return key_states, value_states
 
     def get_mask_sizes(self, query_length: int) -> Tuple[int, int]:
@@ -137,6 +141,9 @@ def build_write_index(pool, block_tables: Sequence, seq_ids: Sequence[int],
 
 class VarlenPackedCache(Cache):
     """Cache for a single fused forward pass over tokens from many sequences."""
+
+    # a sampled pass's event record (engine telemetry); None: nothing is timed
+    timer = None
 
     def __init__(self, pool, num_layers: int, block_tables: Sequence[torch.Tensor], seq_ids: Sequence[int],
                  positions: Sequence[int]):

@@ -585,3 +585,60 @@ def test_graphed_decode_with_a_batch_limit_that_is_not_a_power_of_two(model, tok
     for r, exp in zip(res, expected(model, tok, PROMPTS[:3], 10, stop_on_eos=False)):
         assert r["token_ids"] == exp
     assert 3 in eng._paged_graph._buckets and eng.telemetry()["graph_replays"] > 0
+
+
+@pytest.mark.parametrize("draft_cuda_graph", [False, "batched"])
+def test_batched_speculative_resolve_keeps_seeded_output(model, draft, tok, draft_cuda_graph):
+    """The speculative step resolves every row with one rejection launch and
+    writes every row's confirmed K/V with one launch per layer. From the same
+    global seeds, sampled (temperature 0.8) and greedy requests produce the
+    same tokens, sources and acceptance counts as resolving the rows one at a
+    time with per-row writes."""
+    from memforge_amd.runtime.sampling import SamplingParams
+
+    runs = []
+    for batched in (True, False):
+        eng = make_engine(model, tok, num_blocks=256, max_num_seqs=4, max_model_len=256, draft_model=draft,
+                          lookahead_k=3, draft_cuda_graph=draft_cuda_graph)
+        eng._batched_resolve = batched
+        torch.manual_seed(11)
+        torch.cuda.manual_seed(11)
+        ids = [eng.submit(p, SamplingParams(max_new_tokens=14, temperature=0.8 if i % 2 else 0.0, top_p=1.0,
+                                            stop_on_eos=False))
+               for i, p in enumerate(DRAFT_PROMPTS)]
+        eng.run_until_idle()
+        t = eng.telemetry()
+        runs.append(([eng.runtimes[i].generated for i in ids], [eng.runtimes[i].sources for i in ids],
+                     t["draft_tokens_proposed"], t["draft_tokens_accepted"], t["speculative_rounds"]))
+    assert runs[0] == runs[1]
+    assert runs[0][4] > 0 and runs[0][3] < runs[0][2]
+
+
+def test_telemetry_reports_measured_data_path_bandwidth(model, tok):
+    """telemetry() carries the data path's measured figures (HIP events on
+    sampled passes): attention and KV-write GB/s and fraction of the HBM peak
+    on eager passes, and the bytes-roofline fraction of graph-replayed decode
+    steps; describe() names the pool layout."""
+    engine = make_engine(model, tok, paged_cuda_graph=True, telemetry_sample_every=1)
+    engine.generate(PROMPTS, greedy(6, stop_on_eos=False))
+    t = engine.telemetry()
+    for family in ("attention", "kv_write", "decode_graph"):
+        assert t[f"{family}_samples"] > 0, family
+        assert t[f"{family}_gbps"] > 0 and 0 < t[f"{family}_hbm_frac"] < 1, (family, t[f"{family}_gbps"])
+        assert t[f"{family}_us_per_launch"] > 0 and t[f"{family}_bytes_per_launch"] > 0
+    assert t["hbm_peak_gbps"] == 8000.0 and t["data_path_sample_every"] == 1
+    pool = engine.describe()["kv_pool"]
+    assert pool["layout"] == "(layers, blocks, block_size, kv_heads, head_dim)" and pool["dtype"] == "torch.float32"
+    off = make_engine(model, tok, telemetry_sample_every=0)
+    off.generate(PROMPTS[:1], greedy(3))
+    assert off.telemetry()["attention_samples"] == 0 and off.telemetry()["attention_gbps"] is None
+
+
+def test_streamed_text_adds_up_to_the_final_text(model, tok):
+    engine = make_engine(model, tok)
+    sid = engine.submit(PROMPTS[1], greedy(12, stop_on_eos=False))
+    streamed = []
+    while engine.has_work():
+        engine.step()
+        streamed.extend(ev.text for ev in engine.drain_events(sid))
+    assert "".join(streamed) == engine.result_for(sid)["text"] and len(streamed) == 12

@@ -190,3 +190,62 @@ def test_greedy_round_truncates_at_the_first_wrong_candidate(device):
         draft[i][t] = 1.0
     r = resolve_round(1, [3, 9, 2], draft, target, 0.0)
     assert r.accepted == [3, 8] and r.is_draft == [True, False] and r.num_accepted_draft == 1
+
+
+@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("temps", [(1.0,), (0.0,), (0.7, 0.0, 1.3)])
+def test_global_rng_batched_resolve_equals_row_by_row(device, seed, temps):
+    """resolve_rounds_global_rng (one launch for every row) against
+    resolve_round applied row after row, from the same global seeds: same
+    rounds for every row, and both leave torch's CPU and GPU generators in
+    the same state (the batched form consumes exactly what the rows would).
+    Target logits are wider than the draft vocabulary (clipped first)."""
+    from memforge_amd.runtime.batched_speculative import resolve_round, resolve_rounds_global_rng
+
+    g = torch.Generator().manual_seed(seed)
+    B, K, V, Vt = 6, 4, 3000, 3072
+    target = (torch.randn((B, K + 1, Vt), generator=g) * 2).to(device)
+    mix = (seed % 3) / 2.0
+    dlog = torch.randn((B, K, V), generator=g) * 2
+    dprobs = torch.softmax(mix * target[:, :K, :V].cpu() + (1 - mix) * dlog, dim=-1).to(device)
+    cand = [[int(torch.multinomial(dprobs[b, i].cpu(), 1, generator=g)) for i in range(K)] for b in range(B)]
+    t_rows = [temps[b % len(temps)] for b in range(B)]
+
+    torch.manual_seed(seed)
+    torch.cuda.manual_seed(seed)
+    want = [resolve_round(b, cand[b], list(dprobs[b]), list(target[b]), t_rows[b]) for b in range(B)]
+    cpu_after, gpu_after = torch.get_rng_state(), torch.cuda.get_rng_state()
+
+    torch.manual_seed(seed)
+    torch.cuda.manual_seed(seed)
+    got = resolve_rounds_global_rng(list(range(B)), cand, dprobs, target, t_rows)
+    assert [(r.accepted, r.is_draft, r.num_accepted_draft) for r in got] == \
+           [(r.accepted, r.is_draft, r.num_accepted_draft) for r in want]
+    assert torch.equal(torch.get_rng_state(), cpu_after)
+    assert torch.equal(torch.cuda.get_rng_state(), gpu_after)
+
+
+def test_confirmed_prefix_scatter_writes_only_confirmed_rows(device):
+    """One KV write per layer for every row's confirmed prefix: the pool
+    holds exactly the rows scatter_accepted_kv would write one sequence at a
+    time, and nothing else changes."""
+    from memforge_amd.runtime.batched_speculative import (confirmed_slot_mapping, scatter_accepted_kv,
+                                                           scatter_confirmed_rows)
+    from memforge_amd.runtime.kv_pool import ModelKVSpec, PagedKVPool
+
+    spec = ModelKVSpec(num_layers=3, num_kv_heads=2, head_dim=64, dtype=torch.bfloat16, device=str(device))
+    bs, W = 16, 5
+    a, b = PagedKVPool(spec, 40, bs), PagedKVPool(spec, 40, bs)
+    g = torch.Generator().manual_seed(4)
+    tables = [[3, 17, 5], [8, 1], [30, 31, 32, 33]]
+    ctx = [30, 14, 60]
+    confirmed = [5, 0, 2]
+    new_kv = [(torch.randn((3, 2, W, 64), generator=g).to(torch.bfloat16).to(device),
+               torch.randn((3, 2, W, 64), generator=g).to(torch.bfloat16).to(device)) for _ in range(3)]
+    slots = confirmed_slot_mapping(tables, ctx, confirmed, W, bs)
+    assert slots.shape == (3 * W,) and (slots[W:2 * W] == -1).all() and (slots[2 * W + 2:] == -1).all()
+    scatter_confirmed_rows(a, new_kv, torch.from_numpy(slots).to(device))
+    for row in range(3):
+        scatter_accepted_kv(b, torch.tensor(tables[row], device=device), ctx[row], new_kv, row, confirmed[row])
+    assert torch.equal(a.key_pool, b.key_pool) and torch.equal(a.value_pool, b.value_pool)
+    assert int((a.key_pool != 0).any(dim=(0, 2, 3, 4)).sum()) > 0
