@@ -66,7 +66,7 @@ def parse_args():
     ap.add_argument("--e2e-eager", action="store_true",
                     help="run decode steps eagerly instead of replaying the captured decode graph")
     ap.add_argument("--no-mixed", action="store_true", help="skip the C2 mixed-step and C3 verify measurements")
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "kv-write", "draft"],
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "kv-write", "draft", "c3-engine"],
                     help="run only one section (C2 mixed step, C3 verify, large KV write) and print its JSON")
     return ap.parse_args()
 
@@ -144,6 +144,36 @@ def check_output(ctx, tables, kpool, vpool, q, out) -> dict:
             "ok": max(errs) <= 2e-2 and max(rels) <= 1e-2}
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_time(fn, seconds: float, max_reps: int = 200):
+    """Mean wall seconds of fn() on all host cores over about ``seconds``
+    (after one untimed call), and the number of timed calls."""
+    torch.set_num_threads(os.cpu_count() or 1)
+    fn()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds or reps >= max_reps:
+            return dt / reps, reps
+
+
+def _cpu_leg(value: float, unit: str, sample: str) -> dict:
+    return {"value": value, "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "cpu_model": _cpu_model(), "sample": sample}
+
+
 def cpu_baseline(ctx, tables, kpool, vpool, q, seconds: float):
     from oracle.cpu_baseline import decode_attention_cpu
 
@@ -176,15 +206,10 @@ def cpu_baseline(ctx, tables, kpool, vpool, q, seconds: float):
             break
     dt = time.perf_counter() - t0
     nbytes = int(cs.sum()) * HKV * D * 2 * 2 * passes
-    return {
-        "value": round(nbytes / dt / 1e9, 3),
-        "unit": "GB/s",
-        "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": (f"{len(sample)} of {B} sequences ({int(cs.sum())} context tokens), 1 layer, "
-                   f"{passes} passes in {dt:.1f}s; reference gather+materialised attention ported "
-                   f"to torch-CPU float32, bytes counted as the bf16 workload's"),
-    }
+    return _cpu_leg(round(nbytes / dt / 1e9, 3), "GB/s",
+                    f"{len(sample)} of {B} sequences ({int(cs.sum())} context tokens), 1 layer, "
+                    f"{passes} passes in {dt:.1f}s; reference gather+materialised attention ported "
+                    f"to torch-CPU float32, bytes counted as the bf16 workload's")
 
 
 # ------------------------------------------------------------- C2 / C3 steps
@@ -313,6 +338,15 @@ def run_c1(dev, reps=50):
         times[name] = _event_us(ev)
     kv_bytes = sum(ctx) * SM_HKV * SM_D * 4 * 2
     graph_us = _graph_us(lambda i: varlen(), 16)
+
+    # CPU baseline: the reference operator (read_kv's per-block slices and
+    # cat, fp32 softmax, value product), one call per sequence, on the host
+    from oracle.cpu_baseline import operator_cpu
+
+    kc, vc = cache.key_cache.cpu(), cache.value_cache.cpu()
+    qs_cpu = [x.cpu() for x in qs]
+    cpu_s, cpu_reps = _cpu_time(lambda: [operator_cpu(qs_cpu[i], kc, vc, tables[i], ctx[i]) for i in range(8)],
+                                3.0)
     return {
         "workload": "C1: SmolLM2 decode, fp32, 8 sequences, ctx U[17,512], 15q/5kv, D 64, pool 1024x16 "
                     "random placement, scale 1/8",
@@ -324,6 +358,9 @@ def run_c1(dev, reps=50):
         "tolerance": 1e-5,
         "kv_bytes": kv_bytes,
         "context_tokens": sum(ctx),
+        "cpu_baseline": _cpu_leg(round(cpu_s * 1e6, 1), "us per 8 operator calls",
+                                 f"the whole C1 step (8 PagedAttention.forward calls, fp32), {cpu_reps} timed "
+                                 "repetitions; beside operator_8_calls_us"),
     }
 
 
@@ -434,7 +471,31 @@ def run_c2(dev, layers=SM_LAYERS, reps=3):
         "graph_step_layer_us": round(graph_whole_us, 2),
         "graph_step_note": "the same layer as the engine runs it: KV write, then one attention call with the "
                            "whole plan (decode and prefill items in one launch, then the merge)",
+        "cpu_baseline": _c2_c3_cpu_leg(kp[0], vp[0], knew[0], vnew[0], slot_t, q, tables, cu, positions,
+                                       "C2 layer: KV scatter of 2076 rows + the materialised varlen attention "
+                                       "of 2076 rows (4 causal chunks of 512 + 28 decodes); beside "
+                                       "graph_step_layer_us"),
     }
+
+
+def _c2_c3_cpu_leg(kp, vp, knew, vnew, slots, q, tables, cu, positions, what: str) -> dict:
+    """CPU baseline of one C2/C3 layer: the reference's KV scatter
+    (index_copy_ through slot_mapping) and its materialised varlen attention,
+    in fp32 on the host cores, on the same data as the GPU leg."""
+    from oracle.cpu_baseline import varlen_cpu
+
+    kpc, vpc = kp.float().cpu(), vp.float().cpu()
+    kn, vn, sl = knew.float().cpu(), vnew.float().cpu(), slots.cpu()
+    qc = q.float().cpu()
+    H, D = kpc.shape[2], kpc.shape[3]
+
+    def layer():
+        kpc.view(-1, H, D).index_copy_(0, sl, kn)
+        vpc.view(-1, H, D).index_copy_(0, sl, vn)
+        varlen_cpu(qc, kpc, vpc, tables, cu, positions, BS)
+
+    secs, reps = _cpu_time(layer, 4.0)
+    return _cpu_leg(round(secs * 1e6, 1), "us per layer", f"{what}; fp32, {reps} timed layers")
 
 
 def run_kv_write_large(dev, tokens=33792, reps=20):
@@ -563,7 +624,33 @@ def run_c3(dev, layers=SM_LAYERS, reps=3):
         "rejection_us": round(ver_us, 2),
         "rejection_gbps": round(ver_bytes / ver_us / 1e3, 1),
         "accepted_per_row": res.num_accepted.cpu().tolist(),
+        # the candidates' K/V go through the same scatter the CPU path would
+        # do before attending them (the reference writes them to the pool)
+        "cpu_baseline": _c2_c3_cpu_leg(kp[0], vp[0], nk[0], nv[0], torch.tensor(
+            [tables[b][p // BS] * BS + p % BS for b, c in enumerate(ctx) for p in range(c, c + K + 1)]),
+            q, tables, cu, positions, "C3 layer: scatter of the 80 verify rows + the materialised varlen "
+            "attention of 16 x 5 rows; beside graph_verify_attn_us"),
+        "rejection_cpu_baseline": _rejection_cpu_leg(dtok, dprobs, tl, u, noise),
     }
+
+
+def _rejection_cpu_leg(dtok, dprobs, tl, u, noise) -> dict:
+    """CPU baseline of the C3 rejection step: the reference's per-row
+    resolve (vocabulary clip, fp32 softmax of the target, the accept walk in
+    double and the final multinomial draw as argmax(p / E)), restated in
+    numpy, on the same logits, uniforms and noise."""
+    from oracle import rejection as orj
+
+    dp, tlog, un, nz = dprobs.numpy(), tl.numpy(), u.numpy(), noise.numpy()
+    cand = dtok.tolist()
+
+    def rows():
+        for b in range(len(cand)):
+            orj.resolve_round(cand[b], list(dp[b]), list(tlog[b]), 1.0, list(un[b]), nz[b])
+
+    secs, reps = _cpu_time(rows, 3.0, max_reps=20)
+    return _cpu_leg(round(secs * 1e6, 1), "us per verify step",
+                    f"16 rows x 4 candidates, vocab 49152, temperature 1; {reps} timed steps; beside rejection_us")
 
 
 # --------------------------------------------------------------------- C4 E2E
@@ -683,7 +770,31 @@ def run_e2e(args, dev):
             "note": "algorithmic bytes of the saturated run (weights once per pass + visible K/V + K/V "
                     "writes) at 8 TB/s over its wall time",
         },
+        "telemetry": {k: v for k, v in engine.telemetry().items()
+                      if k.startswith(("attention_", "kv_write_", "decode_graph_", "data_path_"))},
+        "cpu_baseline": _e2e_cpu_leg(cfg, prompts),
     }
+
+
+def _e2e_cpu_leg(cfg, prompts, n_requests: int = 2, new_tokens: int = 8) -> dict:
+    """CPU baseline of C4: the same model shape in fp32 on the host cores,
+    greedy, requests one after another with their own transformers cache (the
+    forward the reference engine runs, on its CPU device), on the first
+    requests of the same workload."""
+    from transformers import LlamaForCausalLM
+
+    from oracle.cpu_baseline import greedy_cpu
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).float().eval()
+    sample = prompts[:n_requests]
+    t0 = time.perf_counter()
+    greedy_cpu(model, sample, new_tokens)
+    dt = time.perf_counter() - t0
+    return _cpu_leg(round(n_requests * new_tokens / dt, 2), "output tok/s",
+                    f"{n_requests} requests (prompts of {[len(p) for p in sample]} tokens) x {new_tokens} greedy "
+                    f"tokens, SmolLM2-360M shape, fp32, {dt:.1f} s; beside saturated_tok_s")
 
 
 # --------------------------------------------------- draft proposals (C3 shape)
@@ -756,6 +867,63 @@ def run_draft(dev, rounds=8, warm=2, batch=16, k=4):
     return res
 
 
+def run_c3_engine(dev, batch=16, k=4, rounds=8):
+    """Engine-level C3 round: a SmolLM2-360M-shaped target with a
+    SmolLM2-135M-shaped draft (bf16, random init), 16 requests with contexts
+    U[128, 2048], lookahead 4. One timed step is one speculative round for all
+    16 rows: batched graphed draft proposals, one verify pass with the
+    candidates attended in flight, the rejection step and the confirmed-prefix
+    KV write. Timed with the rows resolved by one rejection launch and one
+    KV write per layer, then (same seeds) one row at a time."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from memforge_amd.runtime import ContinuousBatchingEngine, SamplingParams
+
+    def build(shape, seed):
+        cfg = LlamaConfig(**shape, max_position_embeddings=4096, tie_word_embeddings=True, bos_token_id=1,
+                          eos_token_id=2, pad_token_id=0)
+        torch.manual_seed(seed)
+        with torch.device(dev):
+            m = LlamaForCausalLM(cfg)
+        return m.to(torch.bfloat16).eval()
+
+    target, draft = build(E2E_MODEL, 0), build(DRAFT_MODEL, 1)
+    gen = torch.Generator().manual_seed(5)
+    lens = torch.randint(128, 2049, (batch,), generator=gen).tolist()
+    prompts = [torch.randint(3, E2E_MODEL["vocab_size"], (n,), generator=gen).tolist() for n in lens]
+    out = {"workload": f"C3 engine round: {batch} requests, ctx U[128,2048], lookahead {k}, SmolLM2-360M-shaped "
+                       "target + SmolLM2-135M-shaped draft, bf16 random init, greedy and T=0.8 rows alternating"}
+    for name, batched in (("batched", True), ("per_row", False)):
+        eng = ContinuousBatchingEngine(target, _NullTokenizer(), block_size=BS, kv_budget_mb=2048,
+                                       max_num_seqs=batch, max_model_len=2048 + 64, dtype=torch.bfloat16,
+                                       draft_model=draft, lookahead_k=k, draft_cuda_graph="batched",
+                                       paged_cuda_graph=True)
+        eng._batched_resolve = batched
+        torch.manual_seed(7)
+        torch.cuda.manual_seed(7)
+        for i, p in enumerate(prompts):
+            eng.submit(p, SamplingParams(max_new_tokens=60, temperature=0.8 if i % 2 else 0.0, top_p=1.0,
+                                         stop_on_eos=False))
+        while eng.total_speculative_rounds < 2:  # prefill, then two warm rounds
+            eng.step()
+        times, toks = [], 0
+        for _ in range(rounds):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            rep = eng.step()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+            toks += rep.tokens_emitted
+        t = eng.telemetry()
+        out[f"{name}_round_ms"] = round(float(np.median(times)) * 1e3, 3)
+        out[f"{name}_tokens_per_round"] = round(toks / rounds, 2)
+        out[f"{name}_acceptance_rate"] = t["draft_acceptance_rate"]
+        del eng
+        torch.cuda.empty_cache()
+    out["speedup"] = round(out["per_row_round_ms"] / out["batched_round_ms"], 3)
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -781,7 +949,8 @@ def main():
         print(json.dumps({"e2e": run_e2e(args, dev)}))
         return
     if args.only:
-        section = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "kv-write": run_kv_write_large, "draft": run_draft}[args.only]
+        section = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "kv-write": run_kv_write_large, "draft": run_draft,
+                   "c3-engine": run_c3_engine}[args.only]
         print(json.dumps({args.only: section(dev)}))
         return
     ctx, tables, kpool, vpool, q = make_workload(args.sigma, dev)
@@ -904,6 +1073,8 @@ def main():
         result["c3"] = run_c3(dev)
         torch.cuda.empty_cache()
         result["c3"]["draft"] = run_draft(dev)
+        torch.cuda.empty_cache()
+        result["c3"]["engine_round"] = run_c3_engine(dev)
         torch.cuda.empty_cache()
     if not args.no_e2e:
         kpool = vpool = partials = None

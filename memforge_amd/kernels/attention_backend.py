@@ -221,7 +221,7 @@ def _varlen_forward(module, query, key, value, scaling, binding: _VarlenBinding)
         nk = key[0].to(dtype).permute(1, 0, 2)
         nv = value[0].to(dtype).permute(1, 0, 2)
     timer = binding.timer
-    began = timer.start() if timer is not None else None
+    began = timer.start(layer) if timer is not None else None
     nat.paged_attention(
         q_rows, out[0], pool.layer_view(layer), meta["block_tables"], meta["cu_seqlens"],
         meta["kv_lens"], meta["positions"], meta["plan"],

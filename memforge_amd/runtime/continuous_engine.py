@@ -568,7 +568,7 @@ class ContinuousBatchingEngine:
         timer = None
         if sampled:
             kv = [e["start"] + n for e, n in zip(plan, q_lens)]
-            timer = self._meter.begin("eager", self._meter.layer_bytes(kv, int(cu[-1])))
+            timer = self._meter.begin(self._meter.layer_bytes(kv, int(cu[-1])))
         try:
             res = packed_forward(self.model, self.pool, [e["tokens"] for e in plan],
                                  [e["start"] for e in plan], [e["table"] for e in plan],
@@ -585,14 +585,12 @@ class ContinuousBatchingEngine:
     def _run_graphed(self, plan: List[dict], sampled: bool = False) -> List[TokenEvent]:
         """A decode-only step as one replay of the captured packed pass."""
         ctx = [e["start"] for e in plan]
-        timer = began = None
+        timer = None
         if sampled:
             nbytes = self._meter.step_bytes([c + 1 for c in ctx], len(plan))
-            timer = self._meter.begin("graph", {"decode_graph": nbytes})
-            began = timer.start()
-        logits = self._paged_graph.logits_view([e["tokens"][0] for e in plan], ctx, [e["table"] for e in plan])
-        if timer is not None:
-            timer.stop("decode_graph", began)
+            timer = self._meter.begin({"decode_graph": nbytes}, whole=True)
+        logits = self._paged_graph.logits_view([e["tokens"][0] for e in plan], ctx, [e["table"] for e in plan],
+                                               timer=timer)
         self.total_forward_passes += 1
         self.total_blockwise_layers += self.spec.num_layers
         self.total_fused_tokens += len(plan)

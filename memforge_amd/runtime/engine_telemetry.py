@@ -6,11 +6,17 @@ keys, so they keep their names. On top, ``DataPathMeter`` measures the
 bandwidth the data-path kernels reach inside the engine, without a profiler:
 
 * every ``every``-th forward pass is sampled;
-* on a sampled eager pass, HIP events bracket each layer's KV write and
-  attention launch on the stream those kernels run on; on a sampled graph
-  replay (a captured decode step) they bracket the whole replay, whose bytes
-  are then the step's: every weight once, plus every layer's attention and
-  KV-write bytes (the decode step's bytes roofline);
+* on a sampled eager pass, one layer's KV write and attention launch are
+  timed with HIP events on the stream the kernels run on. An eager pass is
+  usually host-bound -- the GPU waits for each launch -- so an event recorded
+  just before a launch would time the host's enqueue latency too. The timed
+  launch is therefore preceded by a short GPU spin (about 40 us, recalibrated
+  from each sample): the start event is recorded after the spin, by which
+  time the launch is already queued behind it, so start-to-end is the
+  kernel's own time;
+* on a sampled graph replay (a captured decode step) the events bracket the
+  replay itself; its bytes are the step's: every weight once, plus every
+  layer's attention and KV-write bytes (the decode step's bytes roofline);
 * events are read back only once they have completed (``Event.query``), so
   sampling never makes the host wait for the GPU;
 * the bytes are algorithmic: attention reads every visible K and V row once,
@@ -29,6 +35,7 @@ from typing import Any, Deque, Dict, List, Optional, Tuple
 import torch
 
 HBM_PEAK_GBPS = 8000.0
+_SPIN_TARGET_US = 40.0
 
 
 def device_figures(pool) -> Dict[str, Any]:
@@ -53,28 +60,44 @@ def device_figures(pool) -> Dict[str, Any]:
     }
 
 
+def _event() -> torch.cuda.Event:
+    ev = torch.cuda.Event(enable_timing=True)
+    ev.record()
+    return ev
+
+
 class _PassRecord:
-    """The events of one sampled pass, grouped by kernel family."""
+    """The events of one sampled pass: per kernel family a list of
+    (spin start, kernel start, kernel end) events; the spin start is None
+    where nothing precedes the timed work."""
 
-    __slots__ = ("kind", "bytes", "events")
+    __slots__ = ("bytes", "layer", "spin_cycles", "events")
 
-    def __init__(self, kind: str, nbytes: Dict[str, int]):
-        self.kind = kind
+    def __init__(self, nbytes: Dict[str, int], layer: Optional[int], spin_cycles: int):
         self.bytes = nbytes
-        self.events: Dict[str, List[Tuple[torch.cuda.Event, torch.cuda.Event]]] = {}
+        self.layer = layer
+        self.spin_cycles = spin_cycles
+        self.events: Dict[str, List[Tuple[Optional[torch.cuda.Event], torch.cuda.Event, torch.cuda.Event]]] = {}
 
-    def start(self) -> torch.cuda.Event:
-        ev = torch.cuda.Event(enable_timing=True)
-        ev.record()
-        return ev
+    def start(self, layer: Optional[int] = None):
+        """Before a launch of layer ``layer``: spin, then the start event (only
+        for the record's timed layer; None for every other layer)."""
+        if layer != self.layer:
+            return None
+        spin = _event()
+        torch.cuda._sleep(self.spin_cycles)
+        return spin, _event()
 
-    def stop(self, family: str, begin: torch.cuda.Event) -> None:
-        end = torch.cuda.Event(enable_timing=True)
-        end.record()
-        self.events.setdefault(family, []).append((begin, end))
+    def stop(self, family: str, began) -> None:
+        if began is not None:
+            self.events.setdefault(family, []).append((began[0], began[1], _event()))
+
+    def start_whole(self):
+        """Before a whole graph replay (no spin: one launch, no host gap)."""
+        return None, _event()
 
     def done(self) -> bool:
-        return all(e.query() for pairs in self.events.values() for _, e in pairs)
+        return all(e.query() for trips in self.events.values() for _, _, e in trips)
 
 
 class DataPathMeter:
@@ -88,15 +111,17 @@ class DataPathMeter:
         self.q_row = num_q_heads * spec.head_dim * self.elt
         self.block_size = block_size
         self.num_layers = spec.num_layers
+        self.timed_layer = spec.num_layers // 2
+        self.spin_cycles = 100_000
         self._passes = 0
         self._pending: Deque[_PassRecord] = deque()
-        # per family: [samples, launches, bytes, seconds, last bytes per launch, last us per launch]
+        # per family: [samples, bytes, seconds, last bytes per launch, last us per launch]
         self._totals: Dict[str, List[float]] = {}
 
     def arm(self) -> bool:
         """Whether the coming pass is a sampled one."""
         self._passes += 1
-        return self.every > 0 and self._passes % self.every == 1 % self.every
+        return self.every > 0 and (self._passes - 1) % self.every == 0
 
     def layer_bytes(self, kv_lens: List[int], rows: int) -> Dict[str, int]:
         """Algorithmic bytes of one layer's attention and KV write."""
@@ -110,8 +135,10 @@ class DataPathMeter:
         per_layer = self.layer_bytes(kv_lens, rows)
         return self.weight_bytes + self.num_layers * (per_layer["attention"] + per_layer["kv_write"])
 
-    def begin(self, kind: str, nbytes: Dict[str, int]) -> _PassRecord:
-        rec = _PassRecord(kind, nbytes)
+    def begin(self, nbytes: Dict[str, int], whole: bool = False) -> _PassRecord:
+        """A record for one sampled pass: one timed layer of an eager pass, or
+        (``whole``) a graph replay."""
+        rec = _PassRecord(nbytes, None if whole else self.timed_layer, self.spin_cycles)
         self._pending.append(rec)
         return rec
 
@@ -119,16 +146,21 @@ class DataPathMeter:
         """Fold the completed records into the totals (never waits)."""
         while self._pending and self._pending[0].done():
             rec = self._pending.popleft()
-            for family, pairs in rec.events.items():
-                secs = sum(a.elapsed_time(b) for a, b in pairs) / 1e3
+            for family, trips in rec.events.items():
+                secs = sum(b.elapsed_time(e) for _, b, e in trips) / 1e3
+                spins = [s.elapsed_time(b) * 1e3 for s, b, _ in trips if s is not None]
+                if spins:  # keep the spin near its target as clocks change
+                    mean = sum(spins) / len(spins)
+                    if mean > 0:
+                        scaled = self.spin_cycles * _SPIN_TARGET_US / mean
+                        self.spin_cycles = int(min(max(scaled, 10_000), 2_000_000))
                 nbytes = rec.bytes.get(family, 0)
-                t = self._totals.setdefault(family, [0, 0, 0, 0.0, 0, 0.0])
+                t = self._totals.setdefault(family, [0, 0, 0.0, 0, 0.0])
                 t[0] += 1
-                t[1] += len(pairs)
-                t[2] += nbytes * len(pairs)
-                t[3] += secs
-                t[4] = nbytes
-                t[5] = secs / len(pairs) * 1e6
+                t[1] += nbytes * len(trips)
+                t[2] += secs
+                t[3] = nbytes
+                t[4] = secs / len(trips) * 1e6
 
     def snapshot(self) -> Dict[str, Any]:
         """The measured figures, one group of keys per kernel family."""
@@ -136,16 +168,16 @@ class DataPathMeter:
         out: Dict[str, Any] = {"data_path_sample_every": self.every, "hbm_peak_gbps": HBM_PEAK_GBPS}
         for family in ("attention", "kv_write", "decode_graph"):
             t = self._totals.get(family)
-            if t is None or t[3] <= 0:
+            if t is None or t[2] <= 0:
                 out.update({f"{family}_samples": 0, f"{family}_gbps": None, f"{family}_hbm_frac": None,
                             f"{family}_us_per_launch": None, f"{family}_bytes_per_launch": None})
                 continue
-            gbps = t[2] / t[3] / 1e9
+            gbps = t[1] / t[2] / 1e9
             out.update({
                 f"{family}_samples": int(t[0]),
                 f"{family}_gbps": round(gbps, 1),
                 f"{family}_hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-                f"{family}_us_per_launch": round(t[5], 2),
-                f"{family}_bytes_per_launch": int(t[4]),
+                f"{family}_us_per_launch": round(t[4], 2),
+                f"{family}_bytes_per_launch": int(t[3]),
             })
         return out

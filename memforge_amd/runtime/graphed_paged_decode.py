@@ -216,11 +216,13 @@ class GraphedPagedDecoder:
     @torch.no_grad()
     def logits_view(self, tokens: Sequence[int], ctx_lens: Sequence[int],
                     block_tables: Sequence[Sequence[int]],
-                    device_tokens: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    device_tokens: Optional[torch.Tensor] = None, timer=None) -> torch.Tensor:
         """Like ``step`` but returns a view of the graph's output, valid until
         the next call. With ``device_tokens`` (n integers on the GPU, e.g. the
         previous step's argmax) the input tokens are taken from there by a
-        device copy, and ``tokens`` is ignored: nothing waits for the host."""
+        device copy, and ``tokens`` is ignored: nothing waits for the host.
+        With ``timer`` (a sampled pass's event record) the replay is bracketed
+        by HIP events."""
         n = len(ctx_lens)
         if device_tokens is None and len(tokens) != n:
             raise ValueError(f"{len(tokens)} tokens for {n} rows")
@@ -231,7 +233,10 @@ class GraphedPagedDecoder:
             bk.tokens[:n].copy_(device_tokens.view(-1)[:n])
         if bk.graph is None:
             self._capture(bk)
+        began = timer.start_whole() if timer is not None else None
         bk.graph.replay()
+        if timer is not None:
+            timer.stop("decode_graph", began)
         self.replays += 1
         return bk.logits[:n]
 

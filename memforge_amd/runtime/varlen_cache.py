@@ -52,7 +52,7 @@ class VarlenPackedCacheLayer(CacheLayerMixin):
             self.owner.new_kv[self.layer_idx] = (key_states, value_states)
         else:
             timer = self.owner.timer
-            began = timer.start() if timer is not None else None
+            began = timer.start(self.layer_idx) if timer is not None else None
             self.owner.pool.write_flat(self.layer_idx, self.owner.write_index, key_states, value_states)
             if timer is not None:
                 timer.stop("kv_write", began)

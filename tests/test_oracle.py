@@ -157,6 +157,46 @@ def test_cpu_baseline_port_equals_the_oracle():
     np.testing.assert_allclose(got, want.transpose(1, 0, 2), atol=1e-12)
 
 
+def test_cpu_baseline_operator_and_varlen_ports_equal_the_oracle():
+    """The C1 operator port against the operator oracle (itself pinned by
+    SDPA), and the C2/C3 materialised varlen port -- causal chunks on a prior
+    context beside decode rows, GQA 3:1 -- against the varlen oracle."""
+    rng = np.random.default_rng(8)
+    kc = rng.standard_normal((10, 3, 16, 32))
+    vc = rng.standard_normal((10, 3, 16, 32))
+    q = rng.standard_normal((1, 3, 2, 32))
+    got = cpu_baseline.operator_cpu(torch.from_numpy(q), torch.from_numpy(kc), torch.from_numpy(vc), [6, 2, 9], 37)
+    # the softmax runs in float32 (paged_attention.py:133), whatever the input dtype
+    np.testing.assert_allclose(got.numpy(), oat.paged_operator(q, kc, vc, [6, 2, 9], 37), atol=1e-6)
+
+    kp, vp = _pool(rng, 30, 16, 2, 32)
+    tables = [[3, 9, 1, 12], [4], [7, 8, 10, 11, 20, 21]]
+    q_lens, starts = [20, 1, 7], [30, 9, 80]
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).tolist()
+    positions = [s + i for s, n in zip(starts, q_lens) for i in range(n)]
+    seq_ids = [e for e, n in enumerate(q_lens) for _ in range(n)]
+    qr = rng.standard_normal((sum(q_lens), 6, 32))
+    got = cpu_baseline.varlen_cpu(torch.from_numpy(qr).float(), torch.from_numpy(kp).float(),
+                                  torch.from_numpy(vp).float(), tables, cu, positions, 16).double().numpy()
+    want = oat.varlen_attention(qr.astype(np.float32).transpose(1, 0, 2), kp.astype(np.float32),
+                                vp.astype(np.float32), tables, seq_ids, positions, 16)
+    np.testing.assert_allclose(got, want.transpose(1, 0, 2), atol=1e-5)
+
+
+def test_cpu_baseline_greedy_equals_transformers_generate():
+    """The C4 CPU baseline's greedy loop against transformers' own generate
+    on a tiny random Llama (CPU)."""
+    from tests.tiny_models import tiny_llama
+
+    model = tiny_llama(num_layers=2, seed=3, device="cpu")
+    prompts = [[5, 9, 33, 2, 7], [100, 3]]
+    got = cpu_baseline.greedy_cpu(model, prompts, 6)
+    for p, toks in zip(prompts, got):
+        ref = model.generate(torch.tensor([p]), max_new_tokens=6, do_sample=False, min_new_tokens=6,
+                             pad_token_id=0)[0, len(p):].tolist()
+        assert toks == ref
+
+
 # --------------------------------------------------------------------- paging
 
 
