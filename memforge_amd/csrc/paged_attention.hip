@@ -340,6 +340,29 @@ constexpr int attn_waves_per_eu() {
 #define MF_NARROW_DEPTH 3
 #endif
 
+// LDS of the attention kernels: one dynamically sized arena per workgroup.
+// A workgroup uses at most one of its two layouts -- the wide items'
+// double-buffered K/V stages (workgroup-shared key loop) or the cooperative
+// units' softmax states (narrow items) -- so a launch that runs both kinds of
+// workgroup (attn_mixed_kernel) sizes the arena for the larger, not for both.
+extern __shared__ __attribute__((aligned(16))) char attn_lds[];
+
+template <int DT, int DP>
+constexpr int wide_lds_bytes() {
+    constexpr int rb = DP * (DT == MF_F32 ? 4 : 2);
+    if constexpr (DT == MF_F32) return 0;  // the workgroup-shared loop is 16-bit only
+    else return 2 * (rb == 128 ? 4 : 2) * 32 * rb + 16;
+}
+template <int DP>
+constexpr int coop_lds_bytes() {
+    return (kWaves * 4 * (DP / 16) * 64 + 2 * kWaves * 16) * 4;
+}
+template <int DT, int DP, int NT, bool FAST>
+constexpr int attn_lds_bytes() {
+    if constexpr (NT == 1) return coop_lds_bytes<DP>();
+    else return FAST ? wide_lds_bytes<DT, DP>() : 0;
+}
+
 // The body of one workgroup of the attention kernel: `block` is its index
 // among the workgroups that run items of this column-tile width.
 template <int DT, int DP, int NT, bool FAST>
@@ -762,8 +785,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
             // kernel past 128 registers (three waves per SIMD), so other row
             // sizes use two.
             constexpr int TPS = RB == 128 ? 4 : 2;
-            __shared__ __attribute__((aligned(16))) char smem[2 * TPS * STAGE];
-            __shared__ int s_end[kWaves];
+            static_assert(wide_lds_bytes<DT, DP>() == 2 * TPS * STAGE + 16, "LDS arena layout");
+            char* smem = attn_lds;
+            int* s_end = reinterpret_cast<int*>(attn_lds + 2 * TPS * STAGE);
             if (lane == 0) s_end[wave] = fast_end;
             __syncthreads();
             const int wg_end = __builtin_amdgcn_readfirstlane(
@@ -947,8 +971,10 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // normalised output, or one partial of a longer split.
     if constexpr (NT == 1) {
         if (it[11] != 0) {  // the planner flags all four items of a cooperative workgroup
-            __shared__ float s_acc[kWaves][4 * VCH][64];
-            __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+            static_assert(coop_lds_bytes<DP>() == (kWaves * 4 * VCH * 64 + 2 * kWaves * 16) * 4, "LDS arena layout");
+            auto s_acc = reinterpret_cast<float (*)[4 * VCH][64]>(attn_lds);
+            auto s_m = reinterpret_cast<float (*)[16]>(attn_lds + kWaves * 4 * VCH * 64 * 4);
+            auto s_l = reinterpret_cast<float (*)[16]>(attn_lds + (kWaves * 4 * VCH * 64 + kWaves * 16) * 4);
             const float lt = group_sum4(l[0]);
 #pragma unroll
             for (int r = 0; r < 4; ++r)
@@ -1084,10 +1110,22 @@ void attn_kernel(AttnArgs a) {
 // layer as two launches, 62.7 us with the wide workgroups first, 58.6 us with
 // the single-tile ones first. Each workgroup is entirely one kind, so the
 // barriers of either body stay workgroup-uniform.
+//
+// Occupancy: with 16-bit rows of 128 bytes (D 64) the launch asks
+// for four waves per SIMD. Its LDS is one arena sized for the larger of the
+// two bodies (32.8 KB at D 64, so four workgroups fit a CU), and the compiler
+// then keeps it to 128 registers with a few spills; three waves per SIMD, the
+// single-tile body's own need (140 registers), left the C2 step's 1,104
+// workgroups in more than one round of three per CU. Measured on the C2
+// engine layer as graph replays: 55.1-56.3 us at four, 56.0-57.3 at three.
 template <int DT, int DP, int NTW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
-    attn_waves_per_eu<DT, DP, NTW>() < attn_waves_per_eu<DT, DP, 1>() ? attn_waves_per_eu<DT, DP, NTW>()
-                                                                      : attn_waves_per_eu<DT, DP, 1>())))
+constexpr int mixed_waves_per_eu() {
+    if constexpr (DT != MF_F32 && DP == 64) return 4;
+    else return attn_waves_per_eu<DT, DP, NTW>() < attn_waves_per_eu<DT, DP, 1>() ? attn_waves_per_eu<DT, DP, NTW>()
+                                                                                 : attn_waves_per_eu<DT, DP, 1>();
+}
+template <int DT, int DP, int NTW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(mixed_waves_per_eu<DT, DP, NTW>())))
 void attn_mixed_kernel(AttnArgs narrow, AttnArgs wide, int wide_blocks) {
     const int b = blockIdx.x;
     const int narrow_blocks = (int)gridDim.x - wide_blocks;
@@ -1178,7 +1216,9 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
             aw.dev_count = dev_counts ? dev_counts + 1 : nullptr;
             const int64_t wide_blocks = (n_wide + kWaves - 1) / kWaves;
             const dim3 grid((unsigned)(wide_blocks + (n_narrow + kWaves - 1) / kWaves));
-            hipLaunchKernelGGL((attn_mixed_kernel<DT, DP, NTW>), grid, dim3(256), 0, stream, an, aw,
+            constexpr int lds = attn_lds_bytes<DT, DP, 1, true>() > attn_lds_bytes<DT, DP, NTW, true>()
+                                    ? attn_lds_bytes<DT, DP, 1, true>() : attn_lds_bytes<DT, DP, NTW, true>();
+            hipLaunchKernelGGL((attn_mixed_kernel<DT, DP, NTW>), grid, dim3(256), lds, stream, an, aw,
                                (int)wide_blocks);
             if (int st = check_launch()) return st;
             n_narrow = n_wide = 0;
@@ -1190,8 +1230,12 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
         a.num_items = (int)n_narrow;
         a.dev_count = dev_counts ? dev_counts + 0 : nullptr;
         const dim3 grid((unsigned)((n_narrow + kWaves - 1) / kWaves));
-        if (fast) hipLaunchKernelGGL((attn_kernel<DT, DP, 1, true>), grid, dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL((attn_kernel<DT, DP, 1, false>), grid, dim3(256), 0, stream, a);
+        if (fast)
+            hipLaunchKernelGGL((attn_kernel<DT, DP, 1, true>), grid, dim3(256), (attn_lds_bytes<DT, DP, 1, true>()),
+                               stream, a);
+        else
+            hipLaunchKernelGGL((attn_kernel<DT, DP, 1, false>), grid, dim3(256), (attn_lds_bytes<DT, DP, 1, false>()),
+                               stream, a);
         if (int st = check_launch()) return st;
     }
     if constexpr (NTW > 1) {
@@ -1200,8 +1244,12 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
             a.num_items = (int)n_wide;
             a.dev_count = dev_counts ? dev_counts + 1 : nullptr;
             const dim3 grid((unsigned)((n_wide + kWaves - 1) / kWaves));
-            if (fast) hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, true>), grid, dim3(256), 0, stream, a);
-            else hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, false>), grid, dim3(256), 0, stream, a);
+            if (fast)
+                hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, true>), grid, dim3(256),
+                                   (attn_lds_bytes<DT, DP, NTW, true>()), stream, a);
+            else
+                hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, false>), grid, dim3(256),
+                                   (attn_lds_bytes<DT, DP, NTW, false>()), stream, a);
             if (int st = check_launch()) return st;
         }
     } else {
