@@ -18,6 +18,7 @@ average duration, measured with HIP events on the stream it runs on.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import math
 import os
@@ -37,10 +38,14 @@ HBM_PEAK_GBPS = 8000.0
 B, HQ, HKV, D, BS, LAYERS = 256, 40, 8, 128, 16, 48
 
 # HBM traffic of one attention launch on the default workload, from two
-# rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch). Each is
-# scaled by what the same counter reads for a plain copy of exactly 1 GiB on
-# the MI355X: FETCH_SIZE reports half the bytes (x2.0), WRITE_SIZE all (x1.0).
-PMC_DEFAULT = {"fetch_kib": 1619051.2, "write_kib": 3210.7, "fetch_scale": 2.0, "write_scale": 1.0}
+# rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), per
+# plan form. Each is scaled by what the same counter reads for a plain copy of
+# exactly 1 GiB on the MI355X: FETCH_SIZE reports half the bytes (x2.0),
+# WRITE_SIZE all (x1.0). None: not measured for that kernel yet.
+PMC_DEFAULT = {
+    "ranges": {"fetch_kib": 1619051.2, "write_kib": 3210.7, "fetch_scale": 2.0, "write_scale": 1.0},
+    "slices": None,
+}
 
 
 def parse_args():
@@ -50,7 +55,10 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--sigma", type=float, default=1.0, help="lognormal sigma of context lengths")
-    ap.add_argument("--partition-tiles", type=int, default=0, help="split-K partition (16-key tiles), 0=auto")
+    ap.add_argument("--partition-tiles", type=int, default=0,
+                    help="split-K partition (16-key tiles) of a per-range plan; 0=auto")
+    ap.add_argument("--ranges", action="store_true",
+                    help="run C5 with the per-range plan (mf_attention_plan) instead of the decode slice plan")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline duration")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-check", action="store_true",
@@ -959,16 +967,18 @@ def main():
     cu = torch.arange(B + 1, dtype=torch.int32, device=dev)
     kv_lens = ctx.to(torch.int32).to(dev)
     positions = (ctx - 1).to(dev)
+    # The decode slice plan unless a per-range plan is asked for (a forced
+    # partition or the fused merge are per-range features).
+    slices = not (args.ranges or args.partition_tiles or args.fused)
     plan = nat.plan_attention(list(range(B + 1)), ctx.tolist(), HQ, HKV, D, torch.bfloat16, dev,
-                              args.partition_tiles)
+                              args.partition_tiles, decode_slices=slices)
+    form = "slices" if plan.sliced else "ranges"
     pool = nat.PoolView.from_bshd(kpool, vpool)
     partials = torch.empty(max(plan.partials_floats, 1), dtype=torch.float32, device=dev)
     counters = torch.zeros(max(plan.n_merges, 1), dtype=torch.int32, device=dev)
     scale = 1.0 / math.sqrt(D)
-    merges_only = nat.AttentionPlan(plan.items, plan.merges, 0, 0, plan.n_merges, plan.partials_floats,
-                                    plan.items_host, plan.merges_host)
-    items_only = nat.AttentionPlan(plan.items, plan.merges, plan.n_narrow, plan.n_wide, 0,
-                                   plan.partials_floats, plan.items_host, plan.merges_host)
+    merges_only = dataclasses.replace(plan, n_narrow=0, n_wide=0)
+    items_only = dataclasses.replace(plan, n_merges=0)
 
     def run(p, fused):
         nat.paged_attention(q, out, pool, bt, cu, kv_lens, positions, p, scale, HKV, partials=partials,
@@ -1013,9 +1023,9 @@ def main():
     per_layer = attn_bytes(ctx)
     total = per_layer * args.layers * args.steps
     traffic = None
-    if args.sigma == 1.0 and args.partition_tiles == 0 and not args.fused:
-        traffic = int(PMC_DEFAULT["fetch_kib"] * 1024 * PMC_DEFAULT["fetch_scale"]
-                      + PMC_DEFAULT["write_kib"] * 1024 * PMC_DEFAULT["write_scale"])
+    pmc = PMC_DEFAULT[form]
+    if args.sigma == 1.0 and args.partition_tiles == 0 and not args.fused and pmc is not None:
+        traffic = int(pmc["fetch_kib"] * 1024 * pmc["fetch_scale"] + pmc["write_kib"] * 1024 * pmc["write_scale"])
     value = total / wall / 1e9
     attn_avg_s = float(np.mean(attn_ms)) / 1e3
     achieved = per_layer / attn_avg_s / 1e9
@@ -1041,6 +1051,7 @@ def main():
             "context_tokens": int(ctx.sum()),
             "max_context": int(ctx.max()),
             "pool_blocks": int(kpool.shape[0]),
+            "plan": form,
             "partition_tiles": args.partition_tiles,
             "plan_items": plan.n_narrow + plan.n_wide,
             "plan_merges": plan.n_merges,
@@ -1053,7 +1064,8 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "kernel": "attn_kernel<bf16,128,1,fast>" + (" (split-K merge fused)" if args.fused else ""),
+            "kernel": ("attn_slice_kernel<bf16,128>" if plan.sliced else
+                       "attn_kernel<bf16,128,1,fast>" + (" (split-K merge fused)" if args.fused else "")),
             "kernel_avg_us": round(attn_avg_s * 1e6, 2),
             "merge_avg_us": round(float(np.mean(merge_ms)) * 1e3, 2),
             "bytes_per_launch": per_layer,

@@ -25,6 +25,10 @@ DTYPE_CODES = {torch.float32: MF_F32, torch.float16: MF_F16, torch.bfloat16: MF_
 
 PLAN_ITEM_INTS = 12
 PLAN_MERGE_INTS = 8
+SLICE_INTS = 8
+SLICE_MAX_TILES = 256
+SLICE_MAX_SEGMENTS = 64
+SLICE_MIN_TILES = 64
 # 16-key tiles one wave of a plan may cover (MF_MAX_ITEM_TILES in
 # paged_attention.hip); a cooperative unit of four waves covers four times that
 MAX_ITEM_TILES = 128
@@ -65,6 +69,13 @@ _SIGNATURES = {
         _c_int, _c_f32, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp]),
     "mf_attention_plan": (_c_int, [_c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                    _vp, _c_i64, _vp, _c_i64, _vp]),
+    "mf_attention_plan_slices": (_c_int, [_c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_i64,
+                                          _c_int, _vp, _c_i64, _vp, _c_i64, _vp]),
+    "mf_paged_attention_slices": (_c_int, [
+        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
+        _c_int, _vp, _c_i64, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_f32, _vp, _c_i64, _c_i64,
+        _vp, _c_i64, _vp, _c_i64, _vp]),
+    "mf_attention_slice_occupancy": (_c_int, [_c_int, _c_int, ctypes.POINTER(ctypes.c_int)]),
     "mf_spec_verify_workspace_size": (_c_i64, [_c_int, _c_int]),
     "mf_spec_verify": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _c_i64, _c_i64, _vp, _c_int,
                                 _c_i64, _c_i64, _c_f32, _c_int, _vp, _vp, _c_i64, _vp, _vp, _vp,
@@ -323,14 +334,15 @@ def upload(parts: Sequence[np.ndarray], device) -> List[torch.Tensor]:
 class AttentionPlan:
     """Work list for one mf_paged_attention call (valid for its dtype/head_dim)."""
 
-    items: torch.Tensor      # int32 device, (n_items, 8)
-    merges: torch.Tensor     # int32 device, (n_merges, 8)
-    n_narrow: int
-    n_wide: int
+    items: torch.Tensor      # int32 device, (n_items, PLAN_ITEM_INTS); slice plans: (n_slices + n_segments, SLICE_INTS)
+    merges: torch.Tensor     # int32 device, (n_merges, PLAN_MERGE_INTS)
+    n_narrow: int            # slice plans: slices
+    n_wide: int              # slice plans: segments
     n_merges: int
     partials_floats: int
     items_host: np.ndarray
     merges_host: np.ndarray
+    sliced: bool = False     # a decode slice plan (mf_attention_plan_slices)
 
 
 def plan_attention_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int,
@@ -380,18 +392,86 @@ def plan_upload_parts(items: np.ndarray, merges: np.ndarray) -> List[np.ndarray]
 
 
 def plan_from_parts(items: np.ndarray, merges: np.ndarray, counts: np.ndarray,
-                    dev_items: torch.Tensor, dev_merges: torch.Tensor) -> AttentionPlan:
+                    dev_items: torch.Tensor, dev_merges: torch.Tensor, sliced: bool = False) -> AttentionPlan:
     return AttentionPlan(dev_items, dev_merges, int(counts[0]), int(counts[1]), int(counts[2]),
-                         int(counts[3]), items, merges)
+                         int(counts[3]), items, merges, sliced)
+
+
+def plan_slices_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int,
+                     num_kv_heads: int, head_dim: int, dtype: torch.dtype, resident_waves: int,
+                     min_tiles: int = SLICE_MIN_TILES) -> Optional[Tuple[np.ndarray, np.ndarray, np.ndarray]]:
+    """mf_attention_plan_slices on host arrays: (slices [n_slices + n_segments,
+    SLICE_INTS], merges [m, PLAN_MERGE_INTS], counts [n_slices, n_segments,
+    n_merges, partials_floats]), or None when the launch does not qualify
+    (not a pure decode step, or fewer than ``min_tiles`` tiles per resident
+    wave)."""
+    cu = np.ascontiguousarray(np.asarray(cu_seqlens, dtype=np.int32))
+    kv = np.ascontiguousarray(np.asarray(kv_lens, dtype=np.int32))
+    B = kv.shape[0]
+    if cu.shape[0] != B + 1:
+        raise ValueError("cu_seqlens must have one more entry than kv_lens")
+    counts = np.zeros(4, dtype=np.int64)
+    L = lib()
+    args = (B, cu.ctypes.data, kv.ctypes.data, num_q_heads, num_kv_heads, head_dim, dtype_code(dtype),
+            int(resident_waves), int(min_tiles))
+    st = L.mf_attention_plan_slices(*args, None, 0, None, 0, counts.ctypes.data)
+    if st == -2:  # MF_ERR_UNSUPPORTED: not a decode step this plan form serves
+        return None
+    if st not in (0, -3):
+        _check(st, "mf_attention_plan_slices")
+    if counts[0] == 0:
+        return None
+    n_rec, n_merges = int(counts[0] + counts[1]), int(counts[2])
+    slices = np.empty((n_rec, SLICE_INTS), dtype=np.int32)
+    merges = np.empty((max(n_merges, 1), PLAN_MERGE_INTS), dtype=np.int32)
+    _check(L.mf_attention_plan_slices(*args, slices.ctypes.data, n_rec, merges.ctypes.data, n_merges,
+                                      counts.ctypes.data), "mf_attention_plan_slices")
+    return slices, merges[:n_merges], counts
+
+
+_SLICE_WAVES: dict = {}
+
+
+def slice_resident_waves(dtype: torch.dtype, head_dim: int, device) -> int:
+    """Waves of the slice kernel for (dtype, head_dim) the whole device holds
+    at once: its compute units times mf_attention_slice_occupancy."""
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (dtype, head_dim, idx)
+    if key not in _SLICE_WAVES:
+        per_cu = ctypes.c_int(0)
+        with torch.cuda.device(idx):
+            _check(lib().mf_attention_slice_occupancy(dtype_code(dtype), head_dim, ctypes.byref(per_cu)),
+                   "mf_attention_slice_occupancy")
+        _SLICE_WAVES[key] = per_cu.value * torch.cuda.get_device_properties(idx).multi_processor_count
+    return _SLICE_WAVES[key]
+
+
+def plan_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int, num_kv_heads: int,
+              head_dim: int, dtype: torch.dtype, device=None, partition_tiles: int = 0,
+              decode_slices: bool = False) -> Tuple[np.ndarray, np.ndarray, np.ndarray, bool]:
+    """Host plan arrays (items or slices, merges, counts) and whether they are
+    a slice plan. With ``decode_slices`` (the caller's launch has 16-token
+    blocks, no row map and no in-flight keys) a decode step large enough to
+    fill the GPU on ``device`` more than once gets a slice plan; every other
+    call, and an explicit ``partition_tiles``, the per-range plan."""
+    if decode_slices and partition_tiles <= 0 and device is not None and torch.device(device).type == "cuda":
+        made = plan_slices_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim, dtype,
+                                slice_resident_waves(dtype, head_dim, device))
+        if made is not None:
+            return (*made, True)
+    return (*plan_attention_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim, dtype,
+                                 partition_tiles), False)
 
 
 def plan_attention(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int,
                    num_kv_heads: int, head_dim: int, dtype: torch.dtype, device,
-                   partition_tiles: int = 0) -> AttentionPlan:
-    items, merges, counts = plan_attention_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim,
-                                                dtype, partition_tiles)
+                   partition_tiles: int = 0, decode_slices: bool = False) -> AttentionPlan:
+    """A plan for ``paged_attention`` (``plan_host``, then one upload)."""
+    items, merges, counts, sliced = plan_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim, dtype,
+                                              device, partition_tiles, decode_slices)
     dev_items, dev_merges = upload(plan_upload_parts(items, merges), device)
-    return plan_from_parts(items, merges, counts, dev_items, dev_merges)
+    return plan_from_parts(items, merges, counts, dev_items, dev_merges, sliced)
 
 
 class CountedPlan:
@@ -504,6 +584,21 @@ def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView
                                         plan, scale, num_kv_heads, row_map, pool_lens, new_k_rows, new_v_rows)
     if partials is None:
         partials = _WORKSPACE.partials(plan.partials_floats, q_rows.device)
+    if plan.sliced:
+        if row_map is not None or pool_lens is not None or fused_merge:
+            raise ValueError("a slice plan takes no row map, in-flight keys or fused merge")
+        bt_stride = block_tables.shape[1] if block_tables.dim() == 2 else 0
+        _check(lib().mf_paged_attention_slices(
+            _ptr(q_rows), q_rows.stride(0), q_rows.stride(1),
+            _ptr(out_rows), out_rows.stride(0), out_rows.stride(1),
+            dtype_code(q_rows.dtype), _ptr(pool.k), _ptr(pool.v),
+            pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size,
+            _ptr(block_tables), bt_stride, _ptr(cu_seqlens), _ptr(kv_lens), _ptr(positions),
+            Hq, num_kv_heads, D, float(scale),
+            _ptr(plan.items), plan.n_narrow, plan.n_wide, _ptr(plan.merges), plan.n_merges,
+            _ptr(partials), partials.numel() if partials is not None else 0, _stream(q_rows.device),
+        ), "mf_paged_attention_slices")
+        return
     if fused_merge and counters is None:
         counters = _WORKSPACE.counters(plan.n_merges, q_rows.device)
     if not fused_merge:
@@ -545,6 +640,8 @@ def paged_attention_noalloc(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: 
     partials live in the library's own per-GPU array, so the call allocates
     nothing (neither here nor in the library). Plans needing more than
     NOALLOC_PARTIALS_FLOATS partial floats are refused."""
+    if getattr(plan, "sliced", False):
+        raise ValueError("the no-allocation entry point takes per-range plans (mf_attention_plan)")
     _rows_ok(q_rows, "q_rows")
     _rows_ok(out_rows, "out_rows")
     require_device(q_rows, out_rows, pool.k, block_tables, cu_seqlens, kv_lens, positions)
@@ -576,7 +673,7 @@ def paged_attention_packed(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: P
                            offsets: Sequence[int], num_seqs: int, bt_stride: int, counts: np.ndarray,
                            scale: float, num_kv_heads: int, has_row_map: bool, has_pool_lens: bool,
                            new_k_rows: Optional[torch.Tensor] = None,
-                           new_v_rows: Optional[torch.Tensor] = None) -> None:
+                           new_v_rows: Optional[torch.Tensor] = None, sliced: bool = False) -> None:
     """mf_paged_attention on index arrays that one ``upload`` placed in the
     device buffer ``buf`` at ``offsets`` (int32 words, as ``_layout`` gives
     them): the padded block tables, the plan's items, its merges, cu_seqlens
@@ -584,7 +681,8 @@ def paged_attention_packed(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: P
     positions, then the row map and the pool lengths when present. The caller
     built all of them, so only the tensors it did not build (query, output,
     pool, in-flight rows) are checked, and the launch takes addresses inside
-    ``buf`` instead of building a tensor view per array."""
+    ``buf`` instead of building a tensor view per array. ``sliced``: the plan
+    is a slice plan (mf_paged_attention_slices; no row map or pool lengths)."""
     _rows_ok(q_rows, "q_rows")
     _rows_ok(out_rows, "out_rows")
     require_device(q_rows, out_rows, pool.k, buf)
@@ -603,6 +701,20 @@ def paged_attention_packed(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: P
     n_narrow, n_wide, n_merges, floats = (int(x) for x in counts)
     partials = _WORKSPACE.partials(floats, dev)
     addr = [buf.data_ptr() + 4 * o for o in offsets]
+    if sliced:
+        if has_row_map or has_pool_lens:
+            raise ValueError("a slice plan takes no row map or in-flight keys")
+        _check(lib().mf_paged_attention_slices(
+            _ptr(q_rows), q_rows.stride(0), q_rows.stride(1),
+            _ptr(out_rows), out_rows.stride(0), out_rows.stride(1),
+            dtype_code(q_rows.dtype), _ptr(pool.k), _ptr(pool.v),
+            pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size,
+            addr[0], bt_stride, addr[3], addr[3] + 4 * (num_seqs + 1), addr[4],
+            q_rows.shape[1], num_kv_heads, q_rows.shape[2], float(scale),
+            addr[1], n_narrow, n_wide, addr[2], n_merges,
+            _ptr(partials), partials.numel() if partials is not None else 0, _stream(dev),
+        ), "mf_paged_attention_slices")
+        return
     row_map = addr[5] if has_row_map else None
     pool_lens = addr[5 + int(has_row_map)] if has_pool_lens else None
     _check(lib().mf_paged_attention(

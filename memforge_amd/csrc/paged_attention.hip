@@ -336,6 +336,10 @@ constexpr int attn_waves_per_eu() {
 #define MF_MIXED_LAUNCH 1
 #endif
 
+#ifndef MF_SLICE_MERGE_WG
+#define MF_SLICE_MERGE_WG 0
+#endif
+
 #ifndef MF_NARROW_DEPTH
 #define MF_NARROW_DEPTH 3
 #endif
@@ -1133,6 +1137,285 @@ void attn_mixed_kernel(AttnArgs narrow, AttnArgs wide, int wide_blocks) {
     else attn_body<DT, DP, NTW, true>(wide, b - narrow_blocks);
 }
 
+// ------------------------------------------------------------ decode slices
+// A large decode launch as one resident round of waves (mf_attention_plan_slices).
+// The plan cuts the concatenated (sequence, 16-key tile) order into equal
+// slices; one wave per (slice, kv head) streams the slice's tiles for its head
+// and the waves of a slice sit next to each other in the grid (four to a
+// workgroup), so every block's rows are read for all kv heads at about the
+// same time and no workgroup waits for another to leave. Measured on MI355X
+// with a load-only kernel over the C5 block tables: the per-range plan
+// (cooperative units: one CU reading one head's quarters, several rounds of
+// workgroups) streams at 5.9 TB/s, the same tiles in one round with a
+// workgroup per four heads of a range at 6.5-6.8 TB/s.
+//
+// A slice is a list of segments, each one sequence's tiles [kt0, kt1) (a
+// whole range or a piece of one; pieces leave split-K partials for the merge
+// kernel). Each lane holds four of the slice's block-table entries (tile
+// lane + 64k), so the register ring below runs across segment boundaries
+// without a drain: every segment is padded to a multiple of the ring depth
+// with dummy tiles (entry stored as ~block: a one-line load, every key
+// masked), which keeps the ring's slot of a tile fixed at tile % depth. Lane
+// i holds segment i's record and query position, and each segment start
+// loads the next segment's query.
+constexpr int kSliceRecordInts = MF_SLICE_INTS;
+constexpr int kSliceMaxTiles = MF_SLICE_MAX_TILES;        // 4 table entries per lane
+constexpr int kSliceMaxSegments = MF_SLICE_MAX_SEGMENTS;  // one record per lane at set-up
+static_assert(kSliceMaxTiles == 4 * 64 && kSliceMaxSegments <= 64, "slice limits");
+
+template <int DT, int DP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<DT, DP, 1>())))
+void attn_slice_kernel(AttnArgs a, int num_slices, int hkv) {
+    constexpr int ES = DT == MF_F32 ? 4 : 2;
+    constexpr int EPL = 16 / ES;
+    constexpr int NL = DP * ES / 64;
+    constexpr int VCH = DP / 16;
+    constexpr int VB = VCH * ES;
+    constexpr int VWD = VB / 4;
+    constexpr int NB = MF_NARROW_DEPTH;
+    constexpr float kNegInf = -__builtin_huge_valf();
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int w = blockIdx.x * kWaves + wave;
+    if (w >= num_slices * hkv) return;
+    const int sl = w / hkv;
+    const int h = w - sl * hkv;
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;
+    const int j = lane & 15;
+
+    // ---- set-up: the slice's segment records, one per lane, then its
+    // block-table entries (4 per lane) and the first ring tiles
+    const int32_t* hdr = a.items + (int64_t)sl * kSliceRecordInts;
+    const int seg0 = hdr[0], nseg = hdr[1], ntiles = hdr[2];
+    if (nseg <= 0 || ntiles <= 0) return;  // (the planner makes no empty slice)
+    const int32_t* segs = a.items + ((int64_t)num_slices + seg0) * kSliceRecordInts;
+    // Lane i keeps segment i's record (and its query position) for the whole
+    // slice: a segment start reads it with readlane, no memory wait.
+    const int32_t* rec = segs + (int64_t)min(lane, nseg - 1) * kSliceRecordInts;
+    const int4 r0 = *(const int4*)rec;        // s, kt0, kt1, row
+    const int4 r1 = *(const int4*)(rec + 4);  // kv_len, slot0, pieces, piece
+    int tbl[4];
+    {
+        const int len = lane < nseg ? r0.z - r0.y : 0;
+        const int plen = (len + NB - 1) / NB * NB;
+        int pend = plen;  // inclusive scan of the padded lengths
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(pend, off, 64);
+            if (lane >= off) pend += v;
+        }
+        const int pstart = pend - plen;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int t = min(lane + 64 * k, ntiles - 1);
+            int idx = 0;  // last segment starting at or before t
+#pragma unroll
+            for (int step = 32; step >= 1; step >>= 1) {
+                const int c = idx + step;
+                const int ps = __shfl(pstart, min(c, 63), 64);
+                if (c < nseg && ps <= t) idx = c;
+            }
+            const int ts = __shfl(r0.x, idx, 64);
+            const int tk0 = __shfl(r0.y, idx, 64);
+            const int tlen = __shfl(len, idx, 64);
+            const int o = t - __shfl(pstart, idx, 64);
+            const bool real = o < tlen;
+            const int e = a.block_tables[(int64_t)ts * a.bt_stride + tk0 + (real ? o : tlen - 1)];
+            tbl[k] = real ? e : ~e;
+        }
+    }
+    auto tbl_at = [&](int i) -> int {  // wave-uniform i
+        const int k = i >> 6;
+        const int l = i & 63;
+        return k == 0 ? __builtin_amdgcn_readlane(tbl[0], l)
+             : k == 1 ? __builtin_amdgcn_readlane(tbl[1], l)
+             : k == 2 ? __builtin_amdgcn_readlane(tbl[2], l)
+                      : __builtin_amdgcn_readlane(tbl[3], l);
+    };
+
+    const uint32_t k_lane_off = (uint32_t)(((int64_t)j * a.p_ss + g * EPL) * ES);
+    const uint32_t v_row_bytes = (uint32_t)(a.p_ss * ES);
+    const uint32_t v_lane_off = (uint32_t)(((int64_t)(4 * g) * a.p_ss + j * VCH) * ES);
+    uint32_t v_off[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v_off[r] = v_lane_off + (uint32_t)r * v_row_bytes;
+    // Tile i of the slice; `past` (wave-uniform): a prefetch slot beyond the
+    // slice's last tile. Dummy and past tiles load one line per chunk.
+    auto load_tile = [&](int i, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD], bool past) {
+        const int e = tbl_at(i);
+        const int phys = e < 0 ? ~e : e;
+        const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
+        const char* kb = a.k_pool + boff;
+        const char* vb = a.v_pool + boff;
+        const uint32_t sel = (past || e < 0) ? 0u : 0xffffffffu;
+        const uint32_t ko = k_lane_off & sel;
+        if constexpr (DP * ES >= 256) {
+#pragma unroll
+            for (int c = 0; c < NL; ++c) kf[c] = ld_nt16(kb + ko + c * 4 * 16);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ld_words_nt<VB>(vb + (v_off[r] & sel), vf[r]);
+        } else {
+#pragma unroll
+            for (int c = 0; c < NL; ++c) kf[c] = *(const uint4*)(kb + ko + c * 4 * 16);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ld_words<VB>(vb + (v_off[r] & sel), vf[r]);
+        }
+    };
+
+    // Query position of lane i's segment; then the first segment's query
+    // (MFMA B operand: lane (g, j) holds column j's head_dim chunks c*4 + g;
+    // padding columns j >= G read column 0's, whose scores are never stored)
+    // and the first ring tiles. A segment loads the next one's query when it
+    // starts, so no segment start waits on memory.
+    const int lpos = reinterpret_cast<const int32_t*>(a.positions)[2 * (int64_t)r0.w];
+    const bool colv = j < a.G;  // decode: one row, columns 0..G-1 are its heads
+    const int qhead = h * a.G + (colv ? j : 0);
+    uint4 qn[NL];
+    auto load_q = [&](int row) {
+#pragma unroll
+        for (int c = 0; c < NL; ++c)
+            qn[c] = *(const uint4*)(a.q + ((int64_t)row * a.q_sr + (int64_t)qhead * a.q_sh + (c * 4 + g) * EPL) * ES);
+    };
+    load_q(__builtin_amdgcn_readlane(r0.w, 0));
+    uint4 kR[NB][NL];
+    uint32_t vR[NB][4][VWD];
+#pragma unroll
+    for (int i = 0; i < NB - 1; ++i) load_tile(min(i, ntiles - 1), kR[i], vR[i], i > ntiles - 1);
+
+    // ---- per-segment state (the lambdas below read it by reference)
+    uint4 qf[NL];
+    float m, l, thr;
+    f32x4 acc[VCH];
+    int lim = -1, minpos = -1, key_end = 0;
+
+    auto process = [&](int kt, const uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
+        if ((kt + 1) * 16 > key_end) {
+            // keys past the segment (padding, or slots past the context,
+            // which may hold anything): p = 0 there, and 0 * NaN is NaN
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool live = kt * 16 + 4 * g + r < key_end;
+#pragma unroll
+                for (int x = 0; x < VWD; ++x) vf[r][x] = live ? vf[r][x] : 0u;
+            }
+        }
+        f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NL; ++c) st = mfma_qk<DT>(kf[c], qf[c], st);
+        float sv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sv[r] = st[r];
+        if (!(kt * 16 + 15 <= minpos && (kt + 1) * 16 <= key_end)) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sv[r] = kt * 16 + 4 * g + r <= lim ? sv[r] : kNegInf;
+        }
+        // lazy rescale, exactly as the per-range kernel does it
+        const float lmax = fmax_prop(fmax_prop(sv[0], sv[1]), fmax_prop(sv[2], sv[3]));
+        if (__builtin_amdgcn_ballot_w64(lmax > thr) != 0) {
+            const float mn = fmaxf(m, group_max4(lmax) * a.scale_log2);
+            const float alpha = __builtin_amdgcn_exp2f(m - mn);
+            l *= alpha;
+#pragma unroll
+            for (int c = 0; c < VCH; ++c) acc[c] *= alpha;
+            m = mn;
+            thr = (mn + kLazyLog2) * a.inv_scale_log2;
+        }
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[r], a.scale_log2, -m));
+        l += (p[0] + p[1]) + (p[2] + p[3]);
+        if constexpr (DT == MF_F32) {
+#pragma unroll
+            for (int c = 0; c < VCH; ++c)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(vf[r][c]), p[r], acc[c], 0, 0, 0);
+        } else {
+            uint2 p16;
+            if constexpr (DT == MF_BF16) {
+                p16 = make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){p[0], p[1]}, bf16x2)),
+                                 __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){p[2], p[3]}, bf16x2)));
+            } else {
+                p16 = make_uint2(f32_to_bits<DT>(p[0]) | (f32_to_bits<DT>(p[1]) << 16),
+                                 f32_to_bits<DT>(p[2]) | (f32_to_bits<DT>(p[3]) << 16));
+            }
+#pragma unroll
+            for (int c = 0; c < VCH; ++c) {
+                const int wd = c >> 1;
+                const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+                const uint2 va = make_uint2(__builtin_amdgcn_perm(vf[1][wd], vf[0][wd], sel),
+                                            __builtin_amdgcn_perm(vf[3][wd], vf[2][wd], sel));
+                acc[c] = mfma_pv16<DT>(va, p16, acc[c]);
+            }
+        }
+    };
+
+    const int dbase = 4 * g * VCH;
+    int t = 0;  // slice index of the next tile to process
+    for (int si = 0; si < nseg; ++si) {
+        const int kt0 = __builtin_amdgcn_readlane(r0.y, si);
+        const int kt1 = __builtin_amdgcn_readlane(r0.z, si);
+        const int row = __builtin_amdgcn_readlane(r0.w, si);
+        const int kv_len = __builtin_amdgcn_readlane(r1.x, si);
+        const int pos = __builtin_amdgcn_readlane(lpos, si);
+#pragma unroll
+        for (int c = 0; c < NL; ++c)
+            qf[c] = make_uint4(qn[c].x ^ a.q_sign, qn[c].y ^ a.q_sign, qn[c].z ^ a.q_sign, qn[c].w ^ a.q_sign);
+        // the next segment's query (the last segment re-reads its own, so
+        // every segment issues the same loads)
+        load_q(__builtin_amdgcn_readlane(r0.w, min(si + 1, nseg - 1)));
+        key_end = min(kv_len, kt1 * 16);
+        lim = colv && pos >= 0 ? min(pos, key_end - 1) : -1;
+        minpos = pos;
+        m = kMinM;
+        thr = (kMinM + kLazyLog2) * a.inv_scale_log2;
+        l = 0.f;
+#pragma unroll
+        for (int c = 0; c < VCH; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        const int seg_start = t;
+        const int rounds = (kt1 - kt0 + NB - 1) / NB;
+        for (int r = rounds; r > 0; --r) {
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const int nx = t + NB - 1;
+                load_tile(min(nx, ntiles - 1), kR[(u + NB - 1) % NB], vR[(u + NB - 1) % NB], nx > ntiles - 1);
+                process(kt0 + (t - seg_start), kR[u], vR[u]);
+                ++t;
+            }
+        }
+
+        // ---- finish the segment: the normalised output, or its partial
+        const float lt = group_sum4(l);
+        if (colv && pos >= 0) {
+            const int slot0 = __builtin_amdgcn_readlane(r1.y, si);
+            if (slot0 < 0) {
+                const float inv = lt > 0.f ? 1.f / lt : 0.f;
+                float vals[4 * VCH];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int c = 0; c < VCH; ++c) vals[r * VCH + c] = acc[c][r] * inv;
+                store_out_chunk<DT, VCH>(a.out + ((int64_t)row * a.o_sr + (int64_t)qhead * a.o_sh + dbase) * ES, vals);
+            } else {
+                const int pslot = slot0 + h * __builtin_amdgcn_readlane(r1.z, si) + __builtin_amdgcn_readlane(r1.w, si);
+                float* ps = a.partials + (int64_t)pslot * (16 * (a.part_dstride + 2));
+                float vals[4 * VCH];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int c = 0; c < VCH; ++c) vals[r * VCH + c] = acc[c][r];
+                store_out_chunk<MF_F32, VCH>((char*)(ps + j * a.part_dstride + dbase), vals);
+                if (g == 0) {
+                    ps[16 * a.part_dstride + j] = m;
+                    ps[16 * a.part_dstride + 16 + j] = lt;
+                }
+            }
+        }
+    }
+}
+
 // --------------------------------------------------------------- merge kernel
 // One workgroup per merge record: wave w merges partitions w, w+4, ... and the
 // four partial results are combined through LDS by wave 0.
@@ -1196,6 +1479,20 @@ __global__ __launch_bounds__(256) void merge_wave_kernel(AttnArgs a, const int32
     merge_tile<DT, DP>(a, merges + (int64_t)mi * MF_PLAN_MERGE_INTS, lane >> 4, lane & 15);
 }
 
+// The split-K merge launch: one wave per record for large launches, one
+// workgroup per record (four waves splitting its partitions) for small ones.
+template <int DT, int DP>
+int launch_merge(const AttnArgs& a, const int32_t* merges, int64_t n_merges, hipStream_t stream) {
+    if (n_merges >= MF_MERGE_WAVE_MIN) {
+        const dim3 grid((unsigned)((n_merges + kWaves - 1) / kWaves));
+        hipLaunchKernelGGL((merge_wave_kernel<DT, DP>), grid, dim3(256), 0, stream, a, merges, (int)n_merges);
+    } else {
+        const dim3 grid((unsigned)n_merges);
+        hipLaunchKernelGGL((merge_kernel<DT, DP>), grid, dim3(256), 0, stream, a, merges, (int)n_merges);
+    }
+    return check_launch();
+}
+
 template <int DT, int DP>
 int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t n_wide,
                      const int32_t* merges, int64_t n_merges, bool fast, const int32_t* dev_counts,
@@ -1257,14 +1554,31 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
     }
     if (n_merges > 0 && !fused) {
         a.dev_count = dev_counts ? dev_counts + 2 : nullptr;
-        if (n_merges >= MF_MERGE_WAVE_MIN) {
-            const dim3 grid((unsigned)((n_merges + kWaves - 1) / kWaves));
-            hipLaunchKernelGGL((merge_wave_kernel<DT, DP>), grid, dim3(256), 0, stream, a, merges, (int)n_merges);
-        } else {
-            const dim3 grid((unsigned)n_merges);
-            hipLaunchKernelGGL((merge_kernel<DT, DP>), grid, dim3(256), 0, stream, a, merges, (int)n_merges);
-        }
+        if (int st = launch_merge<DT, DP>(a, merges, n_merges, stream)) return st;
+    }
+    return MF_OK;
+}
+
+// A slice plan (mf_attention_plan_slices): one wave per (slice, kv head),
+// then the merge of the sequences split across slices.
+template <int DT, int DP>
+int launch_slices(AttnArgs a, const int32_t* slices, int64_t n_slices, int hkv, const int32_t* merges,
+                  int64_t n_merges, hipStream_t stream) {
+    if (n_slices > 0) {
+        a.items = slices;
+        const int64_t waves = n_slices * hkv;
+        const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves));
+        hipLaunchKernelGGL((attn_slice_kernel<DT, DP>), grid, dim3(256), 0, stream, a, (int)n_slices, hkv);
         if (int st = check_launch()) return st;
+    }
+    if (n_merges > 0) {
+#if MF_SLICE_MERGE_WG
+        hipLaunchKernelGGL((merge_kernel<DT, DP>), dim3((unsigned)n_merges), dim3(256), 0, stream, a, merges,
+                           (int)n_merges);
+        if (int st = check_launch()) return st;
+#else
+        if (int st = launch_merge<DT, DP>(a, merges, n_merges, stream)) return st;
+#endif
     }
     return MF_OK;
 }
@@ -1607,6 +1921,158 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     return MF_OK;
 }
 
+// Slice plan for a large decode launch (attn_slice_kernel). The sequences'
+// 16-key tiles, in sequence order, are cut into slices of about
+// total / (resident_waves / Hkv) tiles, so one wave per (slice, kv head)
+// fills the GPU exactly once. A slice holds at most MF_SLICE_MAX_SEGMENTS
+// segments and MF_SLICE_MAX_TILES tiles once each segment is padded to a
+// multiple of the kernel's ring depth; a workload whose even share would
+// exceed that gets more slices (a second round). A sequence cut across
+// slices leaves one partial per piece and kv head, merged afterwards.
+extern "C" int mf_attention_plan_slices(int num_seqs, const int32_t* cu_seqlens, const int32_t* kv_lens,
+                                        int num_q_heads, int num_kv_heads, int head_dim, int dtype,
+                                        int64_t resident_waves, int min_tiles_per_wave, int32_t* slices,
+                                        int64_t slices_capacity, int32_t* merges, int64_t merges_capacity,
+                                        int64_t* counts) {
+    if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || !counts || resident_waves <= 0 ||
+        min_tiles_per_wave < 0)
+        return MF_ERR_ARG;
+    if (num_q_heads % num_kv_heads) return MF_ERR_ARG;
+    if (num_seqs > 0 && (!cu_seqlens || !kv_lens)) return MF_ERR_ARG;
+    const int DP = mf::padded_head_dim(dtype, head_dim);
+    if (!mf::dtype_ok(dtype) || !DP) return MF_ERR_UNSUPPORTED;
+    const int G = num_q_heads / num_kv_heads;
+    const int Hkv = num_kv_heads;
+    counts[0] = counts[1] = counts[2] = counts[3] = 0;
+    // Decode only: one query row per sequence, whose heads fit one column
+    // tile, and head_dim at one of the kernel's sizes.
+    if (DP != head_dim || G > 16) return MF_ERR_UNSUPPORTED;
+    int64_t total = 0;
+    for (int s = 0; s < num_seqs; ++s) {
+        const int qlen = cu_seqlens[s + 1] - cu_seqlens[s];
+        if (qlen < 0) return MF_ERR_ARG;
+        if (kv_lens[s] <= 0 || qlen == 0) continue;
+        if (qlen != 1) return MF_ERR_UNSUPPORTED;
+        total += (kv_lens[s] + 15) / 16;
+    }
+    // Launches whose tiles give each resident wave fewer than
+    // min_tiles_per_wave get no slice plan (counts stay zero): at
+    // MF_SLICE_MIN_TILES and below, per-range items fit them in one round.
+    if (total == 0 || total * Hkv < (int64_t)min_tiles_per_wave * resident_waves) return MF_OK;
+
+    // Slices per round fill the GPU once; a workload whose even share would
+    // not fit one slice runs whole rounds of equal slices (a round with only
+    // a few slices would leave the GPU idle for its whole length). A slice's
+    // real tiles stay below MF_SLICE_MAX_TILES by enough for the padding of
+    // sixteen segments, so padding rarely closes a slice early.
+    constexpr int NB = MF_NARROW_DEPTH;
+    const int64_t base_slices = std::max<int64_t>(1, resident_waves / Hkv);
+    const int64_t fill_cap = mf::kSliceMaxTiles - 16 * (NB - 1);
+    const int64_t rounds = (total + base_slices * fill_cap - 1) / (base_slices * fill_cap);
+    const int64_t want = rounds * base_slices;
+    const int64_t target = (total + want - 1) / want;
+
+    // First walk: cut the slices (segment = sequence, kt0, kt1).
+    struct Seg { int s, kt0, kt1; };
+    std::vector<Seg> segs;
+    std::vector<int64_t> begins;  // first segment of each slice
+    std::vector<int> padded;      // padded tiles of each slice
+    int64_t cur_real = 0;
+    int cur_pad = 0, cur_n = 0;
+    auto open_slice = [&]() {
+        begins.push_back((int64_t)segs.size());
+        padded.push_back(0);
+        cur_real = 0;
+        cur_pad = 0;
+        cur_n = 0;
+    };
+    open_slice();
+    for (int s = 0; s < num_seqs; ++s) {
+        const int qlen = cu_seqlens[s + 1] - cu_seqlens[s];
+        if (kv_lens[s] <= 0 || qlen == 0) continue;
+        const int T = (kv_lens[s] + 15) / 16;
+        int kt = 0;
+        while (kt < T) {
+            const int64_t room_pad = mf::kSliceMaxTiles - cur_pad;
+            if (cur_n == mf::kSliceMaxSegments || cur_real >= target || room_pad < NB) {
+                open_slice();
+                continue;
+            }
+            const int64_t take = std::min<int64_t>({(int64_t)(T - kt), target - cur_real, room_pad / NB * NB});
+            segs.push_back({s, kt, (int)(kt + take)});
+            cur_real += take;
+            cur_pad += (int)((take + NB - 1) / NB * NB);
+            padded.back() = cur_pad;
+            ++cur_n;
+            kt += (int)take;
+        }
+    }
+    if (padded.back() == 0) {  // a slice opened after the last segment
+        begins.pop_back();
+        padded.pop_back();
+    }
+    const int64_t n_slices = (int64_t)begins.size();
+    const int64_t n_segs = (int64_t)segs.size();
+
+    // Pieces per sequence: slot ranges and merge records for split ones.
+    std::vector<int> pieces(num_seqs, 0);
+    for (const Seg& g : segs) ++pieces[g.s];
+    int64_t n_merges = 0, n_slots = 0;
+    for (int s = 0; s < num_seqs; ++s)
+        if (pieces[s] > 1) {
+            n_merges += Hkv;
+            n_slots += (int64_t)Hkv * pieces[s];
+        }
+    counts[0] = n_slices;
+    counts[1] = n_segs;
+    counts[2] = n_merges;
+    counts[3] = n_slots * 16 * (int64_t)(mf::part_dstride_for(head_dim) + 2);
+    if (n_slices + n_segs > slices_capacity || n_merges > merges_capacity) return MF_ERR_WORKSPACE;
+    if (!slices || (n_merges > 0 && !merges)) return MF_ERR_ARG;
+
+    constexpr int R = MF_SLICE_INTS;
+    for (int64_t i = 0; i < n_slices; ++i) {
+        int32_t* o = slices + i * R;
+        const int64_t end = i + 1 < n_slices ? begins[i + 1] : n_segs;
+        std::fill(o, o + R, 0);
+        o[0] = (int32_t)begins[i];
+        o[1] = (int32_t)(end - begins[i]);
+        o[2] = padded[i];
+    }
+    std::vector<int64_t> slot0(num_seqs, -1);
+    int64_t slots = 0, wm = 0;
+    for (int s = 0; s < num_seqs; ++s) {
+        if (pieces[s] <= 1) continue;
+        slot0[s] = slots;
+        for (int h = 0; h < Hkv; ++h) {
+            int32_t* o = merges + (wm++) * MF_PLAN_MERGE_INTS;
+            o[0] = s;
+            o[1] = h;
+            o[2] = 0;
+            o[3] = pieces[s];
+            o[4] = (int32_t)(slots + (int64_t)h * pieces[s]);
+            o[5] = 1;
+            o[6] = cu_seqlens[s];
+            o[7] = 1;
+        }
+        slots += (int64_t)Hkv * pieces[s];
+    }
+    std::vector<int> part(num_seqs, 0);
+    for (int64_t i = 0; i < n_segs; ++i) {
+        const Seg& g = segs[i];
+        int32_t* o = slices + (n_slices + i) * R;
+        o[0] = g.s;
+        o[1] = g.kt0;
+        o[2] = g.kt1;
+        o[3] = cu_seqlens[g.s];
+        o[4] = kv_lens[g.s];
+        o[5] = (int32_t)slot0[g.s];
+        o[6] = pieces[g.s];
+        o[7] = part[g.s]++;
+    }
+    return MF_OK;
+}
+
 namespace {
 int paged_attention_impl(
     const void* q, int64_t q_stride_row, int64_t q_stride_head, void* out, int64_t out_stride_row,
@@ -1618,7 +2084,7 @@ int paged_attention_impl(
     int64_t new_stride_head, int num_q_heads, int num_kv_heads, int head_dim, float scale,
     const int32_t* plan_items, int64_t num_items_narrow, int64_t num_items_wide,
     const int32_t* plan_merges, int64_t num_merges, float* partials, int64_t partials_floats,
-    int32_t* merge_counters, const int32_t* device_counts, mf_stream_t stream) {
+    int32_t* merge_counters, const int32_t* device_counts, mf_stream_t stream, bool sliced = false) {
     using namespace mf;
     if (!(std::fabs(scale) < INFINITY)) return MF_ERR_ARG;  // NaN or infinite
     if (!dtype_ok(dtype) || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
@@ -1690,10 +2156,13 @@ int paged_attention_impl(
     const bool fast = block_size == 16 && head_dim == DP;
     hipStream_t st = (hipStream_t)stream;
 
+    if (sliced && (!fast || row_map || pool_lens || merge_counters || device_counts)) return MF_ERR_UNSUPPORTED;
 #define MF_ATTN_CASE(DT, DPV)                                                                  \
     if (dtype == DT && DP == DPV)                                                              \
-        return launch_attention<DT, DPV>(a, plan_items, num_items_narrow, num_items_wide,      \
-                                         plan_merges, num_merges, fast, device_counts, st);
+        return sliced ? launch_slices<DT, DPV>(a, plan_items, num_items_narrow, num_kv_heads,  \
+                                               plan_merges, num_merges, st)                    \
+                      : launch_attention<DT, DPV>(a, plan_items, num_items_narrow, num_items_wide, \
+                                                  plan_merges, num_merges, fast, device_counts, st);
     MF_ATTN_CASE(MF_F32, 16)
     MF_ATTN_CASE(MF_F32, 32)
     MF_ATTN_CASE(MF_F32, 64)
@@ -1729,6 +2198,53 @@ extern "C" int mf_paged_attention(
                                 num_kv_heads, head_dim, scale, plan_items, num_items_narrow, num_items_wide,
                                 plan_merges, num_merges, partials, partials_floats, merge_counters, nullptr,
                                 stream);
+}
+
+extern "C" int mf_paged_attention_slices(
+    const void* q, int64_t q_stride_row, int64_t q_stride_head, void* out, int64_t out_stride_row,
+    int64_t out_stride_head, int dtype, const void* k_pool, const void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head, int block_size,
+    const int32_t* block_tables, int64_t block_table_stride, const int32_t* cu_seqlens,
+    const int32_t* kv_lens, const int64_t* positions, int num_q_heads, int num_kv_heads, int head_dim,
+    float scale, const int32_t* slices, int64_t num_slices, int64_t num_segments,
+    const int32_t* plan_merges, int64_t num_merges, float* partials, int64_t partials_floats,
+    mf_stream_t stream) {
+    return paged_attention_impl(q, q_stride_row, q_stride_head, out, out_stride_row, out_stride_head, dtype,
+                                k_pool, v_pool, pool_stride_block, pool_stride_slot, pool_stride_head,
+                                block_size, block_tables, block_table_stride, cu_seqlens, kv_lens, positions,
+                                nullptr, nullptr, nullptr, nullptr, 0, 0, num_q_heads, num_kv_heads, head_dim,
+                                scale, slices, num_slices, num_segments, plan_merges, num_merges, partials,
+                                partials_floats, nullptr, nullptr, stream, /*sliced=*/true);
+}
+
+extern "C" int mf_attention_slice_occupancy(int dtype, int head_dim, int* waves_per_cu) {
+    if (!waves_per_cu) return MF_ERR_ARG;
+    const int DP = mf::padded_head_dim(dtype, head_dim);
+    if (!mf::dtype_ok(dtype) || !DP || DP != head_dim) return MF_ERR_UNSUPPORTED;
+    int blocks = 0;
+    hipError_t err = hipErrorInvalidValue;
+#define MF_OCC_CASE(DT, DPV)                                                                              \
+    if (dtype == DT && DP == DPV)                                                                         \
+        err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, mf::attn_slice_kernel<DT, DPV>, 256, 0);
+    MF_OCC_CASE(MF_F32, 16)
+    MF_OCC_CASE(MF_F32, 32)
+    MF_OCC_CASE(MF_F32, 64)
+    MF_OCC_CASE(MF_F32, 128)
+    MF_OCC_CASE(MF_BF16, 32)
+    MF_OCC_CASE(MF_BF16, 64)
+    MF_OCC_CASE(MF_BF16, 128)
+    MF_OCC_CASE(MF_BF16, 256)
+    MF_OCC_CASE(MF_F16, 32)
+    MF_OCC_CASE(MF_F16, 64)
+    MF_OCC_CASE(MF_F16, 128)
+    MF_OCC_CASE(MF_F16, 256)
+#undef MF_OCC_CASE
+    if (err != hipSuccess) {
+        mf::set_last_hip_error((int)err);
+        return MF_ERR_HIP;
+    }
+    *waves_per_cu = blocks * mf::kWaves;
+    return MF_OK;
 }
 
 extern "C" int mf_paged_attention_counted(

@@ -76,7 +76,10 @@ def run_varlen(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: nat.PoolView,
         if ids.size and (int(ids.min()) < 0 or int(ids.max()) >= nblocks):
             raise IndexError(f"block table of sequence {s} names a block outside the pool of {nblocks}")
     nat.require_device(q_rows, out_rows, pool.k)
-    items, merges, counts = nat.plan_attention_host(cu, kvl, hq, num_kv_heads, d, q_rows.dtype)
+    # a large decode step on 16-token blocks runs as one round of slices
+    sliceable = identity and pool_lens is None and pool.block_size == 16
+    items, merges, counts, sliced = nat.plan_host(cu, kvl, hq, num_kv_heads, d, q_rows.dtype, dev,
+                                                  decode_slices=sliceable)
     # tables, plan, cu/kv lengths, positions, row map and pool lengths cross
     # to the device in one copy, and the launch addresses them inside that
     # one buffer
@@ -92,5 +95,5 @@ def run_varlen(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: nat.PoolView,
         q_rows, out_rows, pool, buf, offsets, len(order), tables_host.shape[1], counts,
         scale if scale is not None else 1.0 / math.sqrt(d), num_kv_heads,
         has_row_map=not identity, has_pool_lens=pool_lens is not None,
-        new_k_rows=new_k_rows, new_v_rows=new_v_rows,
+        new_k_rows=new_k_rows, new_v_rows=new_v_rows, sliced=sliced,
     )

@@ -128,9 +128,11 @@ class _VarlenBinding:
                     f"sequence {s} reads up to position {kvl[-1] - 1}, needing {needed} blocks, "
                     f"but its block table has {len(tables[s])} entries"
                 )
-        items, merges, counts = nat.plan_attention_host(cu, kvl, num_q_heads, self.pool.spec.num_kv_heads,
-                                                        head_dim, dtype)
         identity = row_map == list(range(len(row_map)))
+        # a large decode step on 16-token blocks runs as one round of slices
+        sliceable = identity and self.pool_lens is None and self.pool.block_size == 16
+        items, merges, counts, sliced = nat.plan_host(cu, kvl, num_q_heads, self.pool.spec.num_kv_heads,
+                                                      head_dim, dtype, device, decode_slices=sliceable)
         # everything the launch reads crosses to the device in one copy
         parts = [padded_tables_host([tables[s] for s in order]), *nat.plan_upload_parts(items, merges),
                  np.asarray(cu + kvl, dtype=np.int32), np.asarray(list(self.positions), dtype=np.int64)]
@@ -142,13 +144,14 @@ class _VarlenBinding:
         dev = nat.upload(parts, device)
         if host_pool_lens:
             self.pool_lens = dev[-1]
+        plan = nat.plan_from_parts(items, merges, counts, dev[1], dev[2], sliced)
         self._meta = {
             "block_tables": dev[0],
             "cu_seqlens": dev[3][: len(cu)],
             "kv_lens": dev[3][len(cu):],
             "positions": dev[4],
             "row_map": None if identity else dev[5],
-            "plan": nat.plan_from_parts(items, merges, counts, dev[1], dev[2]),
+            "plan": plan,
         }
         return self._meta
 

@@ -85,6 +85,34 @@ def gpu_varlen(q: torch.Tensor, kpool: torch.Tensor, vpool: torch.Tensor,
     return out.permute(1, 0, 2)
 
 
+def gpu_decode_slices(q: torch.Tensor, kpool: torch.Tensor, vpool: torch.Tensor,
+                      tables: Sequence[Sequence[int]], positions: Sequence[int], resident_waves: int,
+                      kv_lens: Optional[Sequence[int]] = None, scale: Optional[float] = None):
+    """One decode row per sequence (row s is sequence s) through a decode
+    slice plan made for ``resident_waves`` resident waves -- a small value
+    cuts even a small batch into many slices and split sequences. q: (Hq, B,
+    D); pools one layer (N, 16, Hkv, D). Returns ((Hq, B, D) output, plan)."""
+    dev = q.device
+    hq, B, d = q.shape
+    pool = nat.PoolView.from_bshd(kpool, vpool)
+    hkv = pool.num_heads
+    cu = list(range(B + 1))
+    kvl = list(kv_lens) if kv_lens is not None else [p + 1 for p in positions]
+    made = nat.plan_slices_host(cu, kvl, hq, hkv, d, q.dtype, resident_waves, min_tiles=0)
+    assert made is not None, "not a decode step"
+    items, merges, counts = made
+    dev_items, dev_merges = nat.upload(nat.plan_upload_parts(items, merges), dev)
+    plan = nat.plan_from_parts(items, merges, counts, dev_items, dev_merges, sliced=True)
+    out = torch.full((B, hq, d), float("nan"), dtype=q.dtype, device=dev)
+    nat.paged_attention(
+        q.permute(1, 0, 2), out, pool, pad_tables(tables, dev),
+        torch.tensor(cu, dtype=torch.int32, device=dev), torch.tensor(kvl, dtype=torch.int32, device=dev),
+        torch.tensor(list(positions), dtype=torch.int64, device=dev),
+        plan, scale if scale is not None else 1.0 / float(np.sqrt(d)), hkv,
+    )
+    return out.permute(1, 0, 2), plan
+
+
 def assert_close_bf16(got: np.ndarray, want: np.ndarray, max_abs: float = 2e-2, mean_rel: float = 1e-2):
     err = np.abs(got - want)
     assert np.isfinite(got).all(), "non-finite output"

@@ -6,8 +6,10 @@ sample of rows (all of them where the oracle is cheap) is checked against the
 float64 oracle:
 
 * C5, the headline: 256 sequences at the 14B GQA shape, lognormal contexts up
-  to 32,768 keys, the auto plan (128-tile waves, 512-tile cooperative units,
-  split-K merge records, the one-wave-per-record merge);
+  to 32,768 keys, through both plan forms: the decode slice plan the bench
+  measures (one round of slices, sequences split across slices, merged) and
+  the per-range plan (128-tile waves, 512-tile cooperative units, split-K
+  merge records, the one-wave-per-record merge);
 * the second block-table register of 65-128-tile waves, in fp32 at D 128;
 * C2's mixed step through the engine's one-launch plan, after the KV scatter
   of its 2,076 new tokens;
@@ -44,18 +46,24 @@ def _compact(kpool, vpool, tables, rows):
     return kp, vp, [[remap[int(x)] for x in tables[r]] for r in rows]
 
 
-def test_c5_headline_plan_matches_the_oracle_on_sampled_rows(device):
+@pytest.mark.parametrize("form", ["slices", "ranges"])
+def test_c5_headline_plan_matches_the_oracle_on_sampled_rows(device, form):
     import bench
 
     ctx, tables, kpool, vpool, q = bench.make_workload(1.0, device)
     B = bench.B
     plan = nat.plan_attention(list(range(B + 1)), ctx.tolist(), bench.HQ, bench.HKV, bench.D,
-                              torch.bfloat16, device)
-    # the plan the headline figure is measured on
-    assert plan.n_wide == 0 and plan.n_merges == 136, (plan.n_narrow, plan.n_merges)
-    items = plan.items_host[: plan.n_narrow]
-    assert (items[:, 11] == 1).any()                   # cooperative units
-    assert int((items[:, 5] - items[:, 4]).max()) == 128  # 128-tile waves
+                              torch.bfloat16, device, decode_slices=form == "slices")
+    if form == "slices":
+        # the plan the headline figure is measured on: one round of slices
+        resident = nat.slice_resident_waves(torch.bfloat16, bench.D, device)
+        assert plan.sliced and plan.n_narrow <= resident // bench.HKV and plan.n_merges > 0
+        assert int(plan.merges_host[:, 3].max()) > 4  # a merge of more than one batch
+    else:
+        assert not plan.sliced and plan.n_wide == 0 and plan.n_merges == 136, (plan.n_narrow, plan.n_merges)
+        items = plan.items_host[: plan.n_narrow]
+        assert (items[:, 11] == 1).any()                   # cooperative units
+        assert int((items[:, 5] - items[:, 4]).max()) == 128  # 128-tile waves
     out = torch.full_like(q, float("nan"))
     pool = nat.PoolView.from_bshd(kpool, vpool)
     nat.paged_attention(q, out, pool, tables.to(device), torch.arange(B + 1, dtype=torch.int32, device=device),
@@ -72,7 +80,17 @@ def test_c5_headline_plan_matches_the_oracle_on_sampled_rows(device):
                                  list(range(len(rows))), (ctx[rows] - 1).tolist(), 16)
     got = to_np64(out[rows].permute(1, 0, 2))
     assert_close_bf16(got, want)
-    print(f"C5 rows {rows} (contexts {ctx[rows].tolist()}): max-abs {np.abs(got - want).max():.3e}")
+    print(f"C5 {form} rows {rows} (contexts {ctx[rows].tolist()}): max-abs {np.abs(got - want).max():.3e}")
+    if form == "slices":
+        # every row against the per-range plan: the two forms differ only in
+        # where fp32 sums are split, so they agree to bf16 output rounding
+        ranges = nat.plan_attention(list(range(B + 1)), ctx.tolist(), bench.HQ, bench.HKV, bench.D,
+                                    torch.bfloat16, device)
+        ref = torch.full_like(q, float("nan"))
+        nat.paged_attention(q, ref, pool, tables.to(device), torch.arange(B + 1, dtype=torch.int32, device=device),
+                            ctx.to(torch.int32).to(device), (ctx - 1).to(device), ranges,
+                            1.0 / math.sqrt(bench.D), bench.HKV)
+        assert_close_bf16(to_np64(out), to_np64(ref), max_abs=4e-3, mean_rel=1e-3)
 
 
 def test_long_waves_use_both_table_registers_fp32_d128(device):
