@@ -44,7 +44,7 @@ B, HQ, HKV, D, BS, LAYERS = 256, 40, 8, 128, 16, 48
 # WRITE_SIZE all (x1.0). None: not measured for that kernel yet.
 PMC_DEFAULT = {
     "ranges": {"fetch_kib": 1619051.2, "write_kib": 3210.7, "fetch_scale": 2.0, "write_scale": 1.0},
-    "slices": {"fetch_kib": 1616575.9, "write_kib": 9345.2, "fetch_scale": 2.0, "write_scale": 1.0},
+    "slices": {"fetch_kib": 1609361.8, "write_kib": 6224.9, "fetch_scale": 2.0, "write_scale": 1.0},
 }
 
 
@@ -112,8 +112,8 @@ def attn_bytes(ctx: torch.Tensor) -> int:
 
 def check_rows(ctx: torch.Tensor) -> list:
     """Rows of the C5 batch that cover every kind of work in either plan form:
-    the shortest and the longest (32,768 keys, cut into eleven slice pieces or
-    merged units), rows of 1,025-2,048 keys (per-range single waves whose
+    the shortest and the longest (32,768 keys, cut into several slice pieces
+    or merged units), rows of 1,025-2,048 keys (per-range single waves whose
     lanes hold two block-table entries; slices hold several of them),
     2,049-8,192 keys (cooperative units; cut across slices) and more than
     8,192 keys (merged in both forms), the ends of the batch and three seeded

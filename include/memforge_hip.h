@@ -307,14 +307,15 @@ int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const int32_t* kv
  * several times over.
  *
  * mf_attention_plan_slices (host) cuts the sequences' 16-key tiles, in
- * sequence order, into slices of equal size: about
- * resident_waves / num_kv_heads of them, so that one wave per (slice, kv
- * head) fills the GPU once. resident_waves is the GPU's compute units times
- * the waves per unit that mf_attention_slice_occupancy reports. A slice holds
- * at most MF_SLICE_MAX_SEGMENTS sequence pieces and MF_SLICE_MAX_TILES tiles
- * once each piece is padded to a multiple of three. Each sequence cut across
- * slices leaves one fp32 partial per piece and kv head, merged by the records
- * written to merges (MF_PLAN_MERGE_INTS ints each).
+ * sequence order, into slices of equal size: num_cus * MF_SLICE_WAVES_PER_CU
+ * / num_kv_heads of them, so that one wave per (slice, kv head) fills the GPU
+ * once at one workgroup (one wave per SIMD) per compute unit; num_cus is the
+ * device's compute units (hipDeviceProp_t::multiProcessorCount). A workload
+ * whose even share exceeds a slice runs whole rounds of such slices. A slice
+ * holds at most MF_SLICE_MAX_SEGMENTS sequence pieces and MF_SLICE_MAX_TILES
+ * tiles once each piece is padded to a multiple of three. Each sequence cut
+ * across slices leaves one fp32 partial per piece and kv head, merged by the
+ * records written to merges (MF_PLAN_MERGE_INTS ints each).
  * slices receives MF_SLICE_INTS ints per record: num_slices slice records
  * (first segment, segments, padded tiles, 0...) followed by num_segments
  * segment records (sequence, first tile, end tile, query row, kv length,
@@ -323,8 +324,8 @@ int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const int32_t* kv
  * Only decode steps qualify: every sequence with keys has one query row,
  * num_q_heads / num_kv_heads <= 16, and head_dim is one of the kernel's sizes
  * (32-256 for 16-bit types, 16-128 for fp32, powers of two); otherwise
- * MF_ERR_UNSUPPORTED. A launch whose tiles give each resident wave fewer
- * than min_tiles_per_wave gets no slice plan (MF_OK with counts all zero);
+ * MF_ERR_UNSUPPORTED. A launch whose tiles give each of its waves fewer than
+ * min_tiles_per_wave gets no slice plan (MF_OK with counts all zero);
  * MF_SLICE_MIN_TILES is the measured choice (below it mf_attention_plan's
  * items fit the launch in one round), 0 plans every decode step. Returns
  * MF_ERR_WORKSPACE if a capacity is too small (counts holds the required
@@ -335,17 +336,15 @@ int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const int32_t* kv
  * with block_size 16; the plan carries the rows, kv lengths and split
  * pieces, and cu_seqlens / kv_lens must hold the values it was made from.
  * Partials need counts[3] floats. Any other block size is
- * MF_ERR_UNSUPPORTED.
- *
- * mf_attention_slice_occupancy reports how many waves of the slice kernel
- * for (dtype, head_dim) fit one compute unit of the current device. */
+ * MF_ERR_UNSUPPORTED. */
 #define MF_SLICE_INTS 8
-#define MF_SLICE_MAX_TILES 256
+#define MF_SLICE_MAX_TILES 512
 #define MF_SLICE_MAX_SEGMENTS 64
 #define MF_SLICE_MIN_TILES 64
+#define MF_SLICE_WAVES_PER_CU 4
 int mf_attention_plan_slices(int num_seqs, const int32_t* cu_seqlens, const int32_t* kv_lens,
                              int num_q_heads, int num_kv_heads, int head_dim, int dtype,
-                             int64_t resident_waves, int min_tiles_per_wave, int32_t* slices,
+                             int num_cus, int min_tiles_per_wave, int32_t* slices,
                              int64_t slices_capacity, int32_t* merges, int64_t merges_capacity,
                              int64_t* counts);
 int mf_paged_attention_slices(const void* q, int64_t q_stride_row, int64_t q_stride_head,
@@ -360,7 +359,6 @@ int mf_paged_attention_slices(const void* q, int64_t q_stride_row, int64_t q_str
                               int64_t num_slices, int64_t num_segments,
                               const int32_t* plan_merges, int64_t num_merges, float* partials,
                               int64_t partials_floats, mf_stream_t stream);
-int mf_attention_slice_occupancy(int dtype, int head_dim, int* waves_per_cu);
 
 /* ----------------------------------------------------- rejection verify
  * Speculative rejection sampling for B rows of K draft candidates, with the

@@ -26,9 +26,10 @@ DTYPE_CODES = {torch.float32: MF_F32, torch.float16: MF_F16, torch.bfloat16: MF_
 PLAN_ITEM_INTS = 12
 PLAN_MERGE_INTS = 8
 SLICE_INTS = 8
-SLICE_MAX_TILES = 256
+SLICE_MAX_TILES = 512
 SLICE_MAX_SEGMENTS = 64
 SLICE_MIN_TILES = 64
+SLICE_WAVES_PER_CU = 4
 # 16-key tiles one wave of a plan may cover (MF_MAX_ITEM_TILES in
 # paged_attention.hip); a cooperative unit of four waves covers four times that
 MAX_ITEM_TILES = 128
@@ -69,13 +70,12 @@ _SIGNATURES = {
         _c_int, _c_f32, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp]),
     "mf_attention_plan": (_c_int, [_c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                    _vp, _c_i64, _vp, _c_i64, _vp]),
-    "mf_attention_plan_slices": (_c_int, [_c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_i64,
+    "mf_attention_plan_slices": (_c_int, [_c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                           _c_int, _vp, _c_i64, _vp, _c_i64, _vp]),
     "mf_paged_attention_slices": (_c_int, [
         _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
         _c_int, _vp, _c_i64, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_f32, _vp, _c_i64, _c_i64,
         _vp, _c_i64, _vp, _c_i64, _vp]),
-    "mf_attention_slice_occupancy": (_c_int, [_c_int, _c_int, ctypes.POINTER(ctypes.c_int)]),
     "mf_spec_verify_workspace_size": (_c_i64, [_c_int, _c_int]),
     "mf_spec_verify": (_c_int, [_c_int, _c_int, _c_int, _vp, _vp, _c_i64, _c_i64, _vp, _c_int,
                                 _c_i64, _c_i64, _c_f32, _c_int, _vp, _vp, _c_i64, _vp, _vp, _vp,
@@ -398,13 +398,13 @@ def plan_from_parts(items: np.ndarray, merges: np.ndarray, counts: np.ndarray,
 
 
 def plan_slices_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int,
-                     num_kv_heads: int, head_dim: int, dtype: torch.dtype, resident_waves: int,
+                     num_kv_heads: int, head_dim: int, dtype: torch.dtype, num_cus: int,
                      min_tiles: int = SLICE_MIN_TILES) -> Optional[Tuple[np.ndarray, np.ndarray, np.ndarray]]:
-    """mf_attention_plan_slices on host arrays: (slices [n_slices + n_segments,
-    SLICE_INTS], merges [m, PLAN_MERGE_INTS], counts [n_slices, n_segments,
-    n_merges, partials_floats]), or None when the launch does not qualify
-    (not a pure decode step, or fewer than ``min_tiles`` tiles per resident
-    wave)."""
+    """mf_attention_plan_slices on host arrays for a GPU of ``num_cus``
+    compute units: (slices [n_slices + n_segments, SLICE_INTS], merges [m,
+    PLAN_MERGE_INTS], counts [n_slices, n_segments, n_merges,
+    partials_floats]), or None when the launch does not qualify (not a pure
+    decode step, or fewer than ``min_tiles`` tiles per wave of one round)."""
     cu = np.ascontiguousarray(np.asarray(cu_seqlens, dtype=np.int32))
     kv = np.ascontiguousarray(np.asarray(kv_lens, dtype=np.int32))
     B = kv.shape[0]
@@ -413,7 +413,7 @@ def plan_slices_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_he
     counts = np.zeros(4, dtype=np.int64)
     L = lib()
     args = (B, cu.ctypes.data, kv.ctypes.data, num_q_heads, num_kv_heads, head_dim, dtype_code(dtype),
-            int(resident_waves), int(min_tiles))
+            int(num_cus), int(min_tiles))
     st = L.mf_attention_plan_slices(*args, None, 0, None, 0, counts.ctypes.data)
     if st == -2:  # MF_ERR_UNSUPPORTED: not a decode step this plan form serves
         return None
@@ -429,22 +429,11 @@ def plan_slices_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_he
     return slices, merges[:n_merges], counts
 
 
-_SLICE_WAVES: dict = {}
-
-
-def slice_resident_waves(dtype: torch.dtype, head_dim: int, device) -> int:
-    """Waves of the slice kernel for (dtype, head_dim) the whole device holds
-    at once: its compute units times mf_attention_slice_occupancy."""
+def device_cus(device) -> int:
+    """Compute units of ``device`` (a slice plan's size is set by it)."""
     dev = torch.device(device)
-    idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    key = (dtype, head_dim, idx)
-    if key not in _SLICE_WAVES:
-        per_cu = ctypes.c_int(0)
-        with torch.cuda.device(idx):
-            _check(lib().mf_attention_slice_occupancy(dtype_code(dtype), head_dim, ctypes.byref(per_cu)),
-                   "mf_attention_slice_occupancy")
-        _SLICE_WAVES[key] = per_cu.value * torch.cuda.get_device_properties(idx).multi_processor_count
-    return _SLICE_WAVES[key]
+    return torch.cuda.get_device_properties(dev.index if dev.index is not None
+                                            else torch.cuda.current_device()).multi_processor_count
 
 
 def plan_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int, num_kv_heads: int,
@@ -457,7 +446,7 @@ def plan_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: in
     call, and an explicit ``partition_tiles``, the per-range plan."""
     if decode_slices and partition_tiles <= 0 and device is not None and torch.device(device).type == "cuda":
         made = plan_slices_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim, dtype,
-                                slice_resident_waves(dtype, head_dim, device))
+                                device_cus(device))
         if made is not None:
             return (*made, True)
     return (*plan_attention_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim, dtype,

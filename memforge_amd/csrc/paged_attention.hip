@@ -1147,11 +1147,14 @@ void attn_mixed_kernel(AttnArgs narrow, AttnArgs wide, int wide_blocks) {
 // with a load-only kernel over the C5 block tables: the per-range plan
 // (cooperative units: one CU reading one head's quarters, several rounds of
 // workgroups) streams at 5.9 TB/s, the same tiles in one round with a
-// workgroup per four heads of a range at 6.5-6.8 TB/s.
+// workgroup per four heads of a range at 6.5-6.8 TB/s. The plan counts one
+// workgroup per CU (one wave per SIMD, MF_SLICE_WAVES_PER_CU): with two per
+// CU the C5 layer took 521 us against 505, fewer streams keeping the HBM
+// busier (three per CU at head_dim 64: 303 against 287 us).
 //
 // A slice is a list of segments, each one sequence's tiles [kt0, kt1) (a
 // whole range or a piece of one; pieces leave split-K partials for the merge
-// kernel). Each lane holds four of the slice's block-table entries (tile
+// kernel). Each lane holds eight of the slice's block-table entries (tile
 // lane + 64k), so the register ring below runs across segment boundaries
 // without a drain: every segment is padded to a multiple of the ring depth
 // with dummy tiles (entry stored as ~block: a one-line load, every key
@@ -1159,9 +1162,10 @@ void attn_mixed_kernel(AttnArgs narrow, AttnArgs wide, int wide_blocks) {
 // i holds segment i's record and query position, and each segment start
 // loads the next segment's query.
 constexpr int kSliceRecordInts = MF_SLICE_INTS;
-constexpr int kSliceMaxTiles = MF_SLICE_MAX_TILES;        // 4 table entries per lane
+constexpr int kSliceMaxTiles = MF_SLICE_MAX_TILES;        // table entries per lane: tiles / 64
+constexpr int kSliceTableRegs = kSliceMaxTiles / 64;
 constexpr int kSliceMaxSegments = MF_SLICE_MAX_SEGMENTS;  // one record per lane at set-up
-static_assert(kSliceMaxTiles == 4 * 64 && kSliceMaxSegments <= 64, "slice limits");
+static_assert(kSliceMaxTiles % 64 == 0 && kSliceMaxSegments <= 64, "slice limits");
 
 template <int DT, int DP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<DT, DP, 1>())))
@@ -1195,7 +1199,7 @@ void attn_slice_kernel(AttnArgs a, int num_slices, int hkv) {
     const int32_t* rec = segs + (int64_t)min(lane, nseg - 1) * kSliceRecordInts;
     const int4 r0 = *(const int4*)rec;        // s, kt0, kt1, row
     const int4 r1 = *(const int4*)(rec + 4);  // kv_len, slot0, pieces, piece
-    int tbl[4];
+    int tbl[kSliceTableRegs];
     {
         const int len = lane < nseg ? r0.z - r0.y : 0;
         const int plen = (len + NB - 1) / NB * NB;
@@ -1207,7 +1211,7 @@ void attn_slice_kernel(AttnArgs a, int num_slices, int hkv) {
         }
         const int pstart = pend - plen;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < kSliceTableRegs; ++k) {
             const int t = min(lane + 64 * k, ntiles - 1);
             int idx = 0;  // last segment starting at or before t
 #pragma unroll
@@ -1228,10 +1232,10 @@ void attn_slice_kernel(AttnArgs a, int num_slices, int hkv) {
     auto tbl_at = [&](int i) -> int {  // wave-uniform i
         const int k = i >> 6;
         const int l = i & 63;
-        return k == 0 ? __builtin_amdgcn_readlane(tbl[0], l)
-             : k == 1 ? __builtin_amdgcn_readlane(tbl[1], l)
-             : k == 2 ? __builtin_amdgcn_readlane(tbl[2], l)
-                      : __builtin_amdgcn_readlane(tbl[3], l);
+        int e = __builtin_amdgcn_readlane(tbl[0], l);
+#pragma unroll
+        for (int q = 1; q < kSliceTableRegs; ++q) e = k == q ? __builtin_amdgcn_readlane(tbl[q], l) : e;
+        return e;
     };
 
     const uint32_t k_lane_off = (uint32_t)(((int64_t)j * a.p_ss + g * EPL) * ES);
@@ -1923,20 +1927,21 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
 
 // Slice plan for a large decode launch (attn_slice_kernel). The sequences'
 // 16-key tiles, in sequence order, are cut into slices of about
-// total / (resident_waves / Hkv) tiles, so one wave per (slice, kv head)
-// fills the GPU exactly once. A slice holds at most MF_SLICE_MAX_SEGMENTS
+// total / (num_cus * MF_SLICE_WAVES_PER_CU / Hkv) tiles, so one wave per
+// (slice, kv head) fills the GPU exactly once at one workgroup per CU. A slice holds at most MF_SLICE_MAX_SEGMENTS
 // segments and MF_SLICE_MAX_TILES tiles once each segment is padded to a
 // multiple of the kernel's ring depth; a workload whose even share would
 // exceed that gets more slices (a second round). A sequence cut across
 // slices leaves one partial per piece and kv head, merged afterwards.
 extern "C" int mf_attention_plan_slices(int num_seqs, const int32_t* cu_seqlens, const int32_t* kv_lens,
                                         int num_q_heads, int num_kv_heads, int head_dim, int dtype,
-                                        int64_t resident_waves, int min_tiles_per_wave, int32_t* slices,
+                                        int num_cus, int min_tiles_per_wave, int32_t* slices,
                                         int64_t slices_capacity, int32_t* merges, int64_t merges_capacity,
                                         int64_t* counts) {
-    if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || !counts || resident_waves <= 0 ||
+    if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || !counts || num_cus <= 0 ||
         min_tiles_per_wave < 0)
         return MF_ERR_ARG;
+    const int64_t resident_waves = (int64_t)num_cus * MF_SLICE_WAVES_PER_CU;
     if (num_q_heads % num_kv_heads) return MF_ERR_ARG;
     if (num_seqs > 0 && (!cu_seqlens || !kv_lens)) return MF_ERR_ARG;
     const int DP = mf::padded_head_dim(dtype, head_dim);
@@ -1970,16 +1975,18 @@ extern "C" int mf_attention_plan_slices(int num_seqs, const int32_t* cu_seqlens,
     const int64_t fill_cap = mf::kSliceMaxTiles - 16 * (NB - 1);
     const int64_t rounds = (total + base_slices * fill_cap - 1) / (base_slices * fill_cap);
     const int64_t want = rounds * base_slices;
-    const int64_t target = (total + want - 1) / want;
+    // slice i carries total / want tiles, one more for the first total % want
+    const int64_t share = total / want, extra = total % want;
 
     // First walk: cut the slices (segment = sequence, kt0, kt1).
     struct Seg { int s, kt0, kt1; };
     std::vector<Seg> segs;
     std::vector<int64_t> begins;  // first segment of each slice
     std::vector<int> padded;      // padded tiles of each slice
-    int64_t cur_real = 0;
+    int64_t cur_real = 0, target = 0;
     int cur_pad = 0, cur_n = 0;
     auto open_slice = [&]() {
+        target = std::max<int64_t>(1, share + ((int64_t)begins.size() < extra ? 1 : 0));
         begins.push_back((int64_t)segs.size());
         padded.push_back(0);
         cur_real = 0;
@@ -2215,36 +2222,6 @@ extern "C" int mf_paged_attention_slices(
                                 nullptr, nullptr, nullptr, nullptr, 0, 0, num_q_heads, num_kv_heads, head_dim,
                                 scale, slices, num_slices, num_segments, plan_merges, num_merges, partials,
                                 partials_floats, nullptr, nullptr, stream, /*sliced=*/true);
-}
-
-extern "C" int mf_attention_slice_occupancy(int dtype, int head_dim, int* waves_per_cu) {
-    if (!waves_per_cu) return MF_ERR_ARG;
-    const int DP = mf::padded_head_dim(dtype, head_dim);
-    if (!mf::dtype_ok(dtype) || !DP || DP != head_dim) return MF_ERR_UNSUPPORTED;
-    int blocks = 0;
-    hipError_t err = hipErrorInvalidValue;
-#define MF_OCC_CASE(DT, DPV)                                                                              \
-    if (dtype == DT && DP == DPV)                                                                         \
-        err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, mf::attn_slice_kernel<DT, DPV>, 256, 0);
-    MF_OCC_CASE(MF_F32, 16)
-    MF_OCC_CASE(MF_F32, 32)
-    MF_OCC_CASE(MF_F32, 64)
-    MF_OCC_CASE(MF_F32, 128)
-    MF_OCC_CASE(MF_BF16, 32)
-    MF_OCC_CASE(MF_BF16, 64)
-    MF_OCC_CASE(MF_BF16, 128)
-    MF_OCC_CASE(MF_BF16, 256)
-    MF_OCC_CASE(MF_F16, 32)
-    MF_OCC_CASE(MF_F16, 64)
-    MF_OCC_CASE(MF_F16, 128)
-    MF_OCC_CASE(MF_F16, 256)
-#undef MF_OCC_CASE
-    if (err != hipSuccess) {
-        mf::set_last_hip_error((int)err);
-        return MF_ERR_HIP;
-    }
-    *waves_per_cu = blocks * mf::kWaves;
-    return MF_OK;
 }
 
 extern "C" int mf_paged_attention_counted(

@@ -86,19 +86,20 @@ def gpu_varlen(q: torch.Tensor, kpool: torch.Tensor, vpool: torch.Tensor,
 
 
 def gpu_decode_slices(q: torch.Tensor, kpool: torch.Tensor, vpool: torch.Tensor,
-                      tables: Sequence[Sequence[int]], positions: Sequence[int], resident_waves: int,
+                      tables: Sequence[Sequence[int]], positions: Sequence[int], num_cus: int,
                       kv_lens: Optional[Sequence[int]] = None, scale: Optional[float] = None):
     """One decode row per sequence (row s is sequence s) through a decode
-    slice plan made for ``resident_waves`` resident waves -- a small value
-    cuts even a small batch into many slices and split sequences. q: (Hq, B,
-    D); pools one layer (N, 16, Hkv, D). Returns ((Hq, B, D) output, plan)."""
+    slice plan made for a GPU of ``num_cus`` compute units -- a small count
+    makes few waves per round, so even a small batch is cut into several
+    slices and split sequences. q: (Hq, B, D); pools one layer
+    (N, 16, Hkv, D). Returns ((Hq, B, D) output, plan)."""
     dev = q.device
     hq, B, d = q.shape
     pool = nat.PoolView.from_bshd(kpool, vpool)
     hkv = pool.num_heads
     cu = list(range(B + 1))
     kvl = list(kv_lens) if kv_lens is not None else [p + 1 for p in positions]
-    made = nat.plan_slices_host(cu, kvl, hq, hkv, d, q.dtype, resident_waves, min_tiles=0)
+    made = nat.plan_slices_host(cu, kvl, hq, hkv, d, q.dtype, num_cus, min_tiles=0)
     assert made is not None, "not a decode step"
     items, merges, counts = made
     dev_items, dev_merges = nat.upload(nat.plan_upload_parts(items, merges), dev)

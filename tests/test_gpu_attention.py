@@ -397,11 +397,11 @@ def test_cooperative_units(device, dtype, d, partition_tiles, fused):
 # ------------------------------------------------------------ decode slices
 # Slice plans (mf_attention_plan_slices + mf_paged_attention_slices): one
 # wave per (slice, kv head) streams an equal share of the batch's tiles. A
-# small resident-wave count cuts these small batches into many slices, so
+# small compute-unit count cuts these small batches into many slices, so
 # every slice case occurs: several sequences per slice, sequences cut into
 # pieces (split-K partials, merged), padded segments, the segment cap.
 
-def _slice_case(device, dt, ctx, hq, hkv, d, resident, seed, positions=None, kv_lens=None, scale=None):
+def _slice_case(device, dt, ctx, hq, hkv, d, cus, seed, positions=None, kv_lens=None, scale=None):
     from tests.gpu_helpers import gpu_decode_slices
 
     gen = torch.Generator().manual_seed(seed)
@@ -412,7 +412,7 @@ def _slice_case(device, dt, ctx, hq, hkv, d, resident, seed, positions=None, kv_
     B = len(ctx)
     q = torch.randn((hq, B, d), generator=gen).to(dt).to(device)
     pos = positions if positions is not None else [c - 1 for c in ctx]
-    got, plan = gpu_decode_slices(q, kp, vp, tables, pos, resident, kv_lens=kv_lens, scale=scale)
+    got, plan = gpu_decode_slices(q, kp, vp, tables, pos, cus, kv_lens=kv_lens, scale=scale)
     want = oatt.varlen_attention(to_np64(q), to_np64(kp), to_np64(vp), tables, list(range(B)), pos, bs,
                                  scale=scale)
     _check(to_np64(got), want, dt)
@@ -426,7 +426,7 @@ def test_decode_slices_against_the_oracle(device, dtype, hq, hkv, d):
     tile sequences) over GQA groups 1, 3, 5 and 16 and head_dim 32-128."""
     gen = torch.Generator().manual_seed(7 + d + hq)
     ctx = torch.randint(1, 700, (24,), generator=gen).tolist() + [1, 16, 17, 48]
-    plan = _slice_case(device, DT[dtype], ctx, hq, hkv, d, resident=6 * hkv, seed=11 + hq)
+    plan = _slice_case(device, DT[dtype], ctx, hq, hkv, d, cus=(6 * hkv + 3) // 4, seed=11 + hq)
     segs = plan.items_host[plan.n_narrow:]
     assert plan.n_narrow > 1 and plan.n_merges > 0            # several slices, split sequences
     assert (plan.items_host[: plan.n_narrow, 1] > 1).any()    # a slice holding several sequences
@@ -437,7 +437,7 @@ def test_decode_slices_against_the_oracle(device, dtype, hq, hkv, d):
 def test_decode_slices_head_dims(device, dtype, d):
     gen = torch.Generator().manual_seed(17 + d)
     ctx = torch.randint(1, 400, (12,), generator=gen).tolist()
-    _slice_case(device, DT[dtype], ctx, 8, 2, d, resident=12, seed=19 + d)
+    _slice_case(device, DT[dtype], ctx, 8, 2, d, cus=3, seed=19 + d)
 
 
 def test_decode_slices_segment_cap(device):
@@ -445,7 +445,7 @@ def test_decode_slices_segment_cap(device):
     (one record per lane) before they reach their share of tiles."""
     gen = torch.Generator().manual_seed(23)
     ctx = torch.randint(1, 33, (200,), generator=gen).tolist()
-    plan = _slice_case(device, torch.bfloat16, ctx, 40, 8, 128, resident=16, seed=29)
+    plan = _slice_case(device, torch.bfloat16, ctx, 40, 8, 128, cus=4, seed=29)
     assert int(plan.items_host[: plan.n_narrow, 1].max()) == 64
 
 
@@ -453,7 +453,7 @@ def test_decode_slices_segment_cap(device):
 def test_decode_slices_long_sequence_many_pieces(device, dtype):
     """One long sequence cut into more than twelve pieces (merge batches of
     four, more than three of them) beside short ones."""
-    plan = _slice_case(device, DT[dtype], [5000, 40, 3, 900], 40, 8, 128, resident=128, seed=31)
+    plan = _slice_case(device, DT[dtype], [5000, 40, 3, 900], 40, 8, 128, cus=32, seed=31)
     assert int(plan.merges_host[:, 3].max()) > 12
 
 
@@ -462,13 +462,13 @@ def test_decode_slices_mask_positions_below_kv_len(device):
     (kv_len > position + 1), inside a piece and at a piece's end."""
     ctx = [600, 333, 1200, 70]
     kv = [640, 400, 1300, 71]
-    _slice_case(device, torch.float32, ctx, 15, 5, 64, resident=20, seed=37,
+    _slice_case(device, torch.float32, ctx, 15, 5, 64, cus=5, seed=37,
                 positions=[c - 1 for c in ctx], kv_lens=kv)
 
 
 @pytest.mark.parametrize("scale", [-0.125, 0.0, 0.5])
 def test_decode_slices_scale_sign_and_zero(device, scale):
-    _slice_case(device, torch.bfloat16, [300, 17, 1000, 64], 15, 5, 64, resident=20, seed=41, scale=scale)
+    _slice_case(device, torch.bfloat16, [300, 17, 1000, 64], 15, 5, 64, cus=5, seed=41, scale=scale)
 
 
 def test_decode_slices_agree_with_the_per_range_plan_fp32(device):
@@ -483,7 +483,7 @@ def test_decode_slices_agree_with_the_per_range_plan_fp32(device):
     kp, vp = _pool(gen, max(max(t) for t in tables) + 1, 16, 8, 128, torch.float32, device)
     q = torch.randn((40, len(ctx), 128), generator=gen).to(device)
     pos = [c - 1 for c in ctx]
-    got, plan = gpu_decode_slices(q, kp, vp, tables, pos, resident_waves=128)
+    got, plan = gpu_decode_slices(q, kp, vp, tables, pos, num_cus=32)
     ref = gpu_varlen(q, kp, vp, tables, list(range(len(ctx))), pos)
     assert plan.sliced and plan.n_merges > 0
     assert float((got - ref).abs().max()) <= 2e-6
@@ -506,7 +506,7 @@ def test_operator_takes_slices_for_a_large_decode_batch(device, monkeypatch):
     monkeypatch.setattr(nat, "paged_attention_packed", spy)
     gen = torch.Generator().manual_seed(47)
     hq, hkv, d = 40, 8, 128
-    resident = nat.slice_resident_waves(torch.bfloat16, d, device)
+    resident = nat.device_cus(device) * nat.SLICE_WAVES_PER_CU
     per_seq = 4096
     B = (64 * resident // hkv + per_seq // 16 - 1) // (per_seq // 16)  # just past the slice threshold
     ctx = [per_seq] * B

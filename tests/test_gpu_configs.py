@@ -56,8 +56,8 @@ def test_c5_headline_plan_matches_the_oracle_on_sampled_rows(device, form):
                               torch.bfloat16, device, decode_slices=form == "slices")
     if form == "slices":
         # the plan the headline figure is measured on: one round of slices
-        resident = nat.slice_resident_waves(torch.bfloat16, bench.D, device)
-        assert plan.sliced and plan.n_narrow <= resident // bench.HKV and plan.n_merges > 0
+        per_round = nat.device_cus(device) * nat.SLICE_WAVES_PER_CU // bench.HKV
+        assert plan.sliced and plan.n_narrow <= per_round and plan.n_merges > 0
         assert int(plan.merges_host[:, 3].max()) > 4  # a merge of more than one batch
     else:
         assert not plan.sliced and plan.n_wide == 0 and plan.n_merges == 136, (plan.n_narrow, plan.n_merges)

@@ -28,6 +28,7 @@ def test_python_constants_match_the_header():
     assert nat.SLICE_MAX_TILES == _define("MF_SLICE_MAX_TILES")
     assert nat.SLICE_MAX_SEGMENTS == _define("MF_SLICE_MAX_SEGMENTS")
     assert nat.SLICE_MIN_TILES == _define("MF_SLICE_MIN_TILES")
+    assert nat.SLICE_WAVES_PER_CU == _define("MF_SLICE_WAVES_PER_CU")
 
 
 def _lognormal(n=256, seed=0):
@@ -36,7 +37,7 @@ def _lognormal(n=256, seed=0):
     return torch.clamp(torch.round(torch.exp(math.log(2048.0) + z)), 64, 32768).to(torch.int64).tolist()
 
 
-def _check_plan(kv, hkv, d, resident, made):
+def _check_plan(kv, hkv, d, cus, made):
     slices, merges, counts = made
     ns, nseg, nm, floats = (int(x) for x in counts)
     assert slices.shape == (ns + nseg, nat.SLICE_INTS)
@@ -74,59 +75,61 @@ def _check_plan(kv, hkv, d, resident, made):
         slots += range(slot0, slot0 + parts)
     assert sorted(slots) == list(range(len(slots)))
     assert floats == len(slots) * 16 * (max(d, 32) + 2)
-    # equal shares: every slice but the last carries the target, unless the
-    # segment cap or the padding closed it earlier
+    # equal shares: slice i carries total // n or one tile more (the first
+    # total % n of them), unless the segment cap closed it earlier
     real = np.add.reduceat(lens, hdr[:, 0]) if ns else np.zeros(0)
-    base = max(1, resident // hkv)
+    base = max(1, cus * nat.SLICE_WAVES_PER_CU // hkv)
     cap = nat.SLICE_MAX_TILES - 16 * (RING - 1)
     total = sum(T)
-    rounds = -(-total // (base * cap))
-    target = -(-total // (rounds * base))
-    full = hdr[:-1, 1] < nat.SLICE_MAX_SEGMENTS
-    assert (real <= target).all()
-    assert (real[:-1][full] >= target - RING).all() or not full.any()
+    n = base * -(-total // (base * cap))
+    share = total // n
+    assert (real <= share + 1).all()
+    capped = hdr[:, 1] == nat.SLICE_MAX_SEGMENTS
+    if not capped.any():
+        assert len(hdr) == min(n, len(hdr)) and (real >= share).all()
     return hdr, segs
 
 
-@pytest.mark.parametrize("hkv,d,resident", [(8, 128, 2048), (5, 64, 3072), (8, 128, 128), (2, 256, 40)])
-def test_lognormal_batches(hkv, d, resident):
+@pytest.mark.parametrize("hkv,d,cus", [(8, 128, 256), (5, 64, 256), (8, 128, 32), (2, 256, 10)])
+def test_lognormal_batches(hkv, d, cus):
     kv = _lognormal()
-    made = nat.plan_slices_host(list(range(len(kv) + 1)), kv, 5 * hkv, hkv, d, torch.bfloat16, resident,
+    made = nat.plan_slices_host(list(range(len(kv) + 1)), kv, 5 * hkv, hkv, d, torch.bfloat16, cus,
                                 min_tiles=0)
-    hdr, _ = _check_plan(kv, hkv, d, resident, made)
-    base = max(1, resident // hkv)
+    hdr, _ = _check_plan(kv, hkv, d, cus, made)
+    base = max(1, cus * nat.SLICE_WAVES_PER_CU // hkv)
     assert len(hdr) <= base * -(-sum((k + 15) // 16 for k in kv) // (base * (nat.SLICE_MAX_TILES - 32)))
 
 
 def test_the_c5_workload_runs_in_one_round():
-    """The bench's C5 batch on MI355X (256 CUs x 8 resident waves): one
-    slice per 8 kv heads' worth of waves, all within a single round."""
+    """The bench's C5 batch on MI355X (256 CUs, one workgroup of four waves
+    each): 128 slices of 8 kv heads, all in a single round."""
     kv = _lognormal()
-    made = nat.plan_slices_host(list(range(257)), kv, 40, 8, 128, torch.bfloat16, 2048)
+    made = nat.plan_slices_host(list(range(257)), kv, 40, 8, 128, torch.bfloat16, 256)
     assert made is not None
-    hdr, segs = _check_plan(kv, 8, 128, 2048, made)
-    assert len(hdr) <= 256 and int(hdr[:, 1].max()) <= 8
+    hdr, segs = _check_plan(kv, 8, 128, 256, made)
+    assert len(hdr) == 128 and int(hdr[:, 1].max()) <= 10
 
 
 def test_many_short_sequences_hit_the_segment_cap():
     kv = [1 + (i * 7) % 30 for i in range(500)]
-    made = nat.plan_slices_host(list(range(501)), kv, 40, 8, 128, torch.bfloat16, 16, min_tiles=0)
-    hdr, _ = _check_plan(kv, 8, 128, 16, made)
+    made = nat.plan_slices_host(list(range(501)), kv, 40, 8, 128, torch.bfloat16, 4, min_tiles=0)
+    hdr, _ = _check_plan(kv, 8, 128, 4, made)
     assert int(hdr[:, 1].max()) == nat.SLICE_MAX_SEGMENTS
 
 
 def test_whole_rounds_when_a_share_exceeds_one_slice():
-    """512 sequences of 2048 keys on 256 slices per round: two rounds of
+    """1,024 sequences of 2,048 keys on 128 slices per round: three rounds of
     equal slices, never a short extra round."""
-    kv = [2048] * 512
-    made = nat.plan_slices_host(list(range(513)), kv, 40, 8, 128, torch.bfloat16, 2048)
-    hdr, _ = _check_plan(kv, 8, 128, 2048, made)
-    assert len(hdr) == 512 and (hdr[:, 1] == 1).all() and (hdr[:, 2] == 129).all()
+    kv = [2048] * 1024
+    made = nat.plan_slices_host(list(range(1025)), kv, 40, 8, 128, torch.bfloat16, 256)
+    hdr, segs = _check_plan(kv, 8, 128, 256, made)
+    real = np.add.reduceat(segs[:, 2] - segs[:, 1], hdr[:, 0])
+    assert len(hdr) == 3 * 128 and real.max() - real.min() == 1 and real.sum() == 1024 * 128
 
 
 def test_small_launches_and_non_decode_steps_get_no_slice_plan():
     cu = list(range(65))
-    assert nat.plan_slices_host(cu, [300] * 64, 40, 8, 128, torch.bfloat16, 2048) is None  # fits one round
+    assert nat.plan_slices_host(cu, [300] * 64, 40, 8, 128, torch.bfloat16, 256) is None  # fits one round
     assert nat.plan_slices_host([0, 1, 5], [900, 900], 40, 8, 128, torch.bfloat16, 16, 0) is None  # prefill rows
     assert nat.plan_slices_host([0, 1], [900], 40, 8, 80, torch.bfloat16, 16, 0) is None  # head_dim 80
     assert nat.plan_slices_host([0, 1], [900], 68, 4, 128, torch.bfloat16, 16, 0) is None  # 17 heads per group
@@ -143,9 +146,9 @@ def test_capacity_and_argument_errors():
     kv = np.array([900, 40, 3, 5000], dtype=np.int32)
     counts = np.zeros(4, dtype=np.int64)
 
-    def call(resident=64, min_tiles=0, cap=0, mcap=0, buf=None, mbuf=None, hq=40, hkv=8):
+    def call(cus=16, min_tiles=0, cap=0, mcap=0, buf=None, mbuf=None, hq=40, hkv=8):
         return L.mf_attention_plan_slices(4, cu.ctypes.data, kv.ctypes.data, hq, hkv, 128, nat.MF_BF16,
-                                          resident, min_tiles, buf, cap, mbuf, mcap, counts.ctypes.data)
+                                          cus, min_tiles, buf, cap, mbuf, mcap, counts.ctypes.data)
 
     assert call() == -3  # sizes only: counts filled, capacities too small
     need, nm = int(counts[0] + counts[1]), int(counts[2])
@@ -154,4 +157,4 @@ def test_capacity_and_argument_errors():
     mg = np.zeros((nm, nat.PLAN_MERGE_INTS), np.int32)
     assert call(cap=need - 1, mcap=nm, buf=sl.ctypes.data, mbuf=mg.ctypes.data) == -3
     assert call(cap=need, mcap=nm, buf=sl.ctypes.data, mbuf=mg.ctypes.data) == 0
-    assert call(resident=0) == -1 and call(min_tiles=-1) == -1 and call(hq=41) == -1
+    assert call(cus=0) == -1 and call(min_tiles=-1) == -1 and call(hq=41) == -1
