@@ -71,6 +71,8 @@ def parse_args():
     ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end continuous-batching run")
     ap.add_argument("--e2e-requests", type=int, default=64)
     ap.add_argument("--e2e-tokens", type=int, default=128)
+    ap.add_argument("--e2e-unfused", action="store_true",
+                    help="engine with each layer's KV write as a launch of its own (fused_kv_write=False)")
     ap.add_argument("--e2e-eager", action="store_true",
                     help="run decode steps eagerly instead of replaying the captured decode graph")
     ap.add_argument("--no-mixed", action="store_true", help="skip the C2 mixed-step and C3 verify measurements")
@@ -374,7 +376,7 @@ def run_c1(dev, reps=50):
     }
 
 
-def run_c2(dev, layers=SM_LAYERS, reps=3):
+def run_c2(dev, layers=SM_LAYERS, reps=3, fused_leg=True, cpu_leg=True):
     """Mixed ragged step: 4 prefill chunks of 512 on priors U[0,2048] + 28
     decodes with contexts U[64,4096]; per layer the KV scatter of all 2076
     new tokens, then one varlen attention launch pair (decode items, prefill
@@ -455,6 +457,14 @@ def run_c2(dev, layers=SM_LAYERS, reps=3):
         nat.paged_attention(q, out, views[i], bt, cu_t, kv_t, pos_t, plan, scale, SM_HKV, partials=partials)
 
     graph_whole_us = _graph_us(layer_whole, layers)
+
+    def layer_fused(i):
+        # the engine's default form: the KV write rides in the attention launch
+        # (new keys read from the new rows), then the merge
+        nat.paged_attention_kv_write(q, out, views[i], bt, cu_t, kv_t, pos_t, plan, scale, SM_HKV,
+                                     knew[i], vnew[i], slot_t)
+
+    graph_fused_us = _graph_us(layer_fused, layers) if fused_leg else float("nan")
     kvb = SM_HKV * SM_D * 2 * 2  # K+V bytes per token per layer
     write_bytes = T * kvb * 2 + T * 8  # read new rows, write pool rows, read slots
     dec_bytes = sum(dctx) * kvb + 28 * SM_HQ * SM_D * 2 * 2
@@ -479,12 +489,15 @@ def run_c2(dev, layers=SM_LAYERS, reps=3):
         "graph_note": "one layer's KV write + decode items + prefill items + merge, replayed as a captured "
                       "graph of all layers (no host submission time)",
         "graph_step_layer_us": round(graph_whole_us, 2),
-        "graph_step_note": "the same layer as the engine runs it: KV write, then one attention call with the "
-                           "whole plan (decode and prefill items in one launch, then the merge)",
+        "graph_step_note": "KV write, then one attention call with the whole plan (decode and prefill items "
+                           "in one launch, then the merge)",
+        "graph_step_fused_layer_us": round(graph_fused_us, 2),
+        "graph_step_fused_note": "the layer as the engine runs it: one launch for the KV write and the decode "
+                                 "and prefill items (new keys read from the new rows), then the merge",
         "cpu_baseline": _c2_c3_cpu_leg(kp[0], vp[0], knew[0], vnew[0], slot_t, q, tables, cu, positions,
                                        "C2 layer: KV scatter of 2076 rows + the materialised varlen attention "
                                        "of 2076 rows (4 causal chunks of 512 + 28 decodes); beside "
-                                       "graph_step_layer_us"),
+                                       "graph_step_fused_layer_us") if cpu_leg else None,
     }
 
 
@@ -737,7 +750,8 @@ def run_e2e(args, dev):
     n_params = sum(p.numel() for p in model.parameters())
     engine = ContinuousBatchingEngine(model, _NullTokenizer(), block_size=BS, kv_budget_mb=E2E_KV_MB,
                                       max_num_seqs=64, max_model_len=2048, dtype=torch.bfloat16,
-                                      paged_cuda_graph=not args.e2e_eager)
+                                      paged_cuda_graph=not args.e2e_eager,
+                                      fused_kv_write=not args.e2e_unfused)
     params = SamplingParams(max_new_tokens=args.e2e_tokens, temperature=0.0, top_p=1.0, stop_on_eos=False)
     arrivals, prompts = e2e_workload(args.e2e_requests)
 
@@ -762,6 +776,7 @@ def run_e2e(args, dev):
                      f"U[32,1024], {args.e2e_tokens} greedy tokens, SmolLM2-360M-shaped Llama bf16 random "
                      f"init, KV {E2E_KV_MB} MB in 16-token blocks, max_num_seqs 64"),
         "decode_steps": "eager" if args.e2e_eager else "HIP graph replay (paged_cuda_graph)",
+        "kv_write": "separate launch" if args.e2e_unfused else "inside each layer's attention launch",
         "poisson_tok_s": round(tok_p / max(clock_p - arrivals[0], 1e-9), 1),
         "poisson_steps": steps_p,
         "poisson_virtual_s": round(clock_p - arrivals[0], 3),
@@ -782,7 +797,7 @@ def run_e2e(args, dev):
         },
         "telemetry": {k: v for k, v in engine.telemetry().items()
                       if k.startswith(("attention_", "kv_write_", "decode_graph_", "data_path_"))},
-        "cpu_baseline": _e2e_cpu_leg(cfg, prompts),
+        "cpu_baseline": None if args.no_cpu_baseline else _e2e_cpu_leg(cfg, prompts),
     }
 
 

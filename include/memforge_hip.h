@@ -240,6 +240,45 @@ int mf_paged_attention_counted(const void* q, int64_t q_stride_row, int64_t q_st
                                int64_t capacity_merges, const int32_t* device_counts,
                                float* partials, int64_t partials_floats, mf_stream_t stream);
 
+/* One packed step's KV write and its attention in one launch. Equivalent to
+ * mf_kv_write of new rows [0, num_new_rows) through slot_mapping (a slot < 0
+ * or >= num_slots is skipped) followed by mf_paged_attention with pool_lens
+ * set to kv_lens[s] - (cu_seqlens[s+1] - cu_seqlens[s]): the pool ends in the
+ * same state and the output is the same, bit for bit. Row cu_seqlens[s] + i
+ * of q, positions and new_k/new_v must be sequence s's new token at position
+ * kv_lens[s] - (cu_seqlens[s+1] - cu_seqlens[s]) + i (how the engine packs a
+ * step: every sequence's new tokens, in position order, end its context).
+ * The attention reads each sequence's new keys from new_k/new_v instead of
+ * the pool, so no workgroup waits on the copy, which runs in workgroups of
+ * the same launch. new_k/new_v are (rows, num_kv_heads, head_dim) in `dtype`
+ * with element strides new_stride_row / new_stride_head (16-byte aligned
+ * rows). With a block_size other than 16 or a head_dim the kernels pad, the
+ * call runs as the two launches it replaces. device_counts NULL: num_items_* and num_merges are the
+ * plan's counts, as in mf_paged_attention; non-NULL: they are capacities and
+ * device_counts holds the live counts, as in mf_paged_attention_counted (for
+ * graph capture; padding rows then carry slot -1). Split-K partitions are
+ * merged by the separate merge kernel.
+ * Replaces VarlenPackedCacheLayer.update's pool.write_flat
+ * (memforge_ml/runtime/varlen_cache.py:61-90, memforge_ml/runtime/kv_pool.py:181-192)
+ * together with the varlen binding of paged_attention_forward that follows it
+ * in every layer (memforge_ml/kernels/attention_backend.py:195-272).
+ */
+int mf_paged_attention_kv_write(const void* q, int64_t q_stride_row, int64_t q_stride_head,
+                                void* out, int64_t out_stride_row, int64_t out_stride_head,
+                                int dtype, void* k_pool, void* v_pool,
+                                int64_t pool_stride_block, int64_t pool_stride_slot,
+                                int64_t pool_stride_head, int block_size,
+                                const int32_t* block_tables, int64_t block_table_stride,
+                                const int32_t* cu_seqlens, const int32_t* kv_lens,
+                                const int64_t* positions, const void* new_k, const void* new_v,
+                                int64_t new_stride_row, int64_t new_stride_head,
+                                const int64_t* slot_mapping, int64_t num_new_rows, int64_t num_slots,
+                                int num_q_heads, int num_kv_heads, int head_dim, float scale,
+                                const int32_t* plan_items, int64_t num_items_narrow,
+                                int64_t num_items_wide, const int32_t* plan_merges,
+                                int64_t num_merges, const int32_t* device_counts,
+                                float* partials, int64_t partials_floats, mf_stream_t stream);
+
 /* mf_paged_attention without a partials buffer or merge counters, so that
  * the call allocates nothing. No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture,

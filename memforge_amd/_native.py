@@ -64,6 +64,10 @@ _SIGNATURES = {
         _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
         _c_int, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int,
         _c_int, _c_f32, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _vp]),
+    "mf_paged_attention_kv_write": (_c_int, [
+        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
+        _c_int, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64,
+        _c_int, _c_int, _c_int, _c_f32, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _vp]),
     "mf_paged_attention_noalloc": (_c_int, [
         _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _vp, _c_i64, _c_i64, _c_i64,
         _c_int, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int,
@@ -193,6 +197,12 @@ class PoolView:
         return PoolView(k, v, k.stride(0), k.stride(2), k.stride(1), bs, h, d)
 
 
+def _same_layout(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Same shape and the same strides on every axis longer than one (the
+    stride of a length-one axis is never used to address an element)."""
+    return a.shape == b.shape and all(x == y for x, y, n in zip(a.stride(), b.stride(), a.shape) if n > 1)
+
+
 def _rows_ok(t: torch.Tensor, name: str) -> None:
     if t.dim() != 3:
         raise ValueError(f"{name} must be a (tokens, heads, head_dim) view, got {tuple(t.shape)}")
@@ -206,7 +216,7 @@ def kv_write(k_rows: torch.Tensor, v_rows: torch.Tensor, slots: torch.Tensor, po
     """Scatter (T, H, D) rows into pool slots ``slots`` (int64, device)."""
     _rows_ok(k_rows, "k_rows")
     _rows_ok(v_rows, "v_rows")
-    if k_rows.stride() != v_rows.stride():
+    if not _same_layout(k_rows, v_rows):
         v_rows = v_rows.contiguous()
         k_rows = k_rows.contiguous()
     require_device(k_rows, v_rows, slots, pool.k)
@@ -230,7 +240,7 @@ def kv_gather(pool: PoolView, slots: torch.Tensor, k_rows: torch.Tensor, v_rows:
     """Copy pool slots ``slots`` into preallocated (T, H, D) rows."""
     _rows_ok(k_rows, "k_rows")
     _rows_ok(v_rows, "v_rows")
-    if k_rows.stride() != v_rows.stride():
+    if not _same_layout(k_rows, v_rows):
         raise ValueError("k_rows and v_rows must share strides")
     require_device(k_rows, v_rows, slots, pool.k)
     if slots.dtype != torch.int64 or not slots.is_contiguous():
@@ -598,7 +608,7 @@ def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView
         if nk is None or nv is None:
             raise ValueError("pool_lens needs the in-flight new_k_rows/new_v_rows")
         require_device(pool_lens, nk, nv)
-        if nk.stride() != nv.stride():
+        if not _same_layout(nk, nv):
             raise ValueError("in-flight K and V rows must share strides")
     bt_stride = block_tables.shape[1] if block_tables.dim() == 2 else 0
     _check(lib().mf_paged_attention(
@@ -613,6 +623,65 @@ def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView
         _ptr(plan.items), plan.n_narrow, plan.n_wide, _ptr(plan.merges), plan.n_merges,
         _ptr(partials), partials.numel() if partials is not None else 0, _ptr(counters), _stream(q_rows.device),
     ), "mf_paged_attention")
+
+
+def paged_attention_kv_write(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView,
+                             block_tables: torch.Tensor, cu_seqlens: torch.Tensor, kv_lens: torch.Tensor,
+                             positions: torch.Tensor, plan, scale: float, num_kv_heads: int,
+                             new_k_rows: torch.Tensor, new_v_rows: torch.Tensor,
+                             slot_mapping: torch.Tensor) -> None:
+    """One launch for a packed step's KV write and its attention
+    (mf_paged_attention_kv_write): rows ``new_k_rows``/``new_v_rows``
+    ((rows, Hkv, D) views in the pool's dtype) go to the pool through
+    ``slot_mapping`` (int64; slot -1 skips a row), and every sequence's keys
+    from ``kv_lens[s] - q_len[s]`` on are read from those rows instead of the
+    pool. Row cu_seqlens[s] + i must be sequence s's new token at position
+    kv_lens[s] - q_len[s] + i. ``plan`` is an AttentionPlan or a CountedPlan
+    (graph capture). Same pool contents and output as ``kv_write`` followed by
+    ``paged_attention``."""
+    _rows_ok(q_rows, "q_rows")
+    _rows_ok(out_rows, "out_rows")
+    _rows_ok(new_k_rows, "new_k_rows")
+    _rows_ok(new_v_rows, "new_v_rows")
+    require_device(q_rows, out_rows, pool.k, block_tables, cu_seqlens, kv_lens, positions, new_k_rows,
+                   new_v_rows, slot_mapping)
+    if q_rows.dtype != pool.k.dtype or out_rows.dtype != pool.k.dtype or new_k_rows.dtype != pool.k.dtype \
+            or new_v_rows.dtype != pool.k.dtype:
+        raise TypeError("query, output, new rows and pool must share a dtype")
+    if not _same_layout(new_k_rows, new_v_rows):
+        raise ValueError("new K and V rows must share shape and strides")
+    if slot_mapping.dtype != torch.int64 or not slot_mapping.is_contiguous():
+        raise TypeError("slot_mapping must be a contiguous int64 tensor")
+    T, H, D = new_k_rows.shape
+    if H != pool.num_heads or D != pool.head_dim or slot_mapping.numel() != T:
+        raise ValueError(f"new rows {tuple(new_k_rows.shape)} / {slot_mapping.numel()} slots do not match a "
+                         f"pool of {pool.num_heads} heads x {pool.head_dim}")
+    if getattr(plan, "sliced", False):
+        raise ValueError("a written-in-flight step takes per-range plans (mf_attention_plan)")
+    bt_stride = block_tables.shape[1] if block_tables.dim() == 2 else 0
+    if isinstance(plan, CountedPlan):
+        n_narrow, n_wide, n_merges = plan.cap_narrow, plan.cap_wide, plan.cap_merges
+        counts, partials = plan.counts, plan.partials
+    else:
+        n_narrow, n_wide, n_merges = plan.n_narrow, plan.n_wide, plan.n_merges
+        counts, partials = None, _WORKSPACE.partials(plan.partials_floats, q_rows.device)
+        # every item's rows (its sequence's first row and row count) must be
+        # rows of the new K/V the launch reads in flight
+        held = plan.items_host[: n_narrow + n_wide]
+        if held.shape[0] and int((held[:, 8] + held[:, 9]).max()) > T:
+            raise ValueError(f"the plan's sequences reach past the {T} new rows")
+    _check(lib().mf_paged_attention_kv_write(
+        _ptr(q_rows), q_rows.stride(0), q_rows.stride(1),
+        _ptr(out_rows), out_rows.stride(0), out_rows.stride(1),
+        dtype_code(q_rows.dtype), _ptr(pool.k), _ptr(pool.v),
+        pool.stride_block, pool.stride_slot, pool.stride_head, pool.block_size,
+        _ptr(block_tables), bt_stride, _ptr(cu_seqlens), _ptr(kv_lens), _ptr(positions),
+        _ptr(new_k_rows), _ptr(new_v_rows), new_k_rows.stride(0), new_k_rows.stride(1),
+        _ptr(slot_mapping), T, pool.num_slots,
+        q_rows.shape[1], num_kv_heads, q_rows.shape[2], float(scale),
+        _ptr(plan.items), n_narrow, n_wide, _ptr(plan.merges), n_merges, _ptr(counts),
+        _ptr(partials), partials.numel() if partials is not None else 0, _stream(q_rows.device),
+    ), "mf_paged_attention_kv_write")
 
 
 # fp32 partials the no-allocation entry point holds per GPU (32 MiB)
@@ -641,7 +710,7 @@ def paged_attention_noalloc(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: 
         if nk is None or nv is None:
             raise ValueError("pool_lens needs the in-flight new_k_rows/new_v_rows")
         require_device(pool_lens, nk, nv)
-        if nk.stride() != nv.stride():
+        if not _same_layout(nk, nv):
             raise ValueError("in-flight K and V rows must share strides")
     bt_stride = block_tables.shape[1] if block_tables.dim() == 2 else 0
     _check(lib().mf_paged_attention_noalloc(
@@ -684,7 +753,7 @@ def paged_attention_packed(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: P
         if nk is None or nv is None:
             raise ValueError("pool_lens needs the in-flight new_k_rows/new_v_rows")
         require_device(nk, nv)
-        if nk.stride() != nv.stride():
+        if not _same_layout(nk, nv):
             raise ValueError("in-flight K and V rows must share strides")
     dev = q_rows.device
     n_narrow, n_wide, n_merges, floats = (int(x) for x in counts)

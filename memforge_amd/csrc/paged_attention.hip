@@ -97,7 +97,47 @@ struct AttnArgs {
     int part_dstride;  // floats per column of a partial slot's output block
     const int32_t* merges;  // plan merge records (fused split-K merge)
     int32_t* counters;      // per-group arrival counters; null = separate merge kernel
+    // Written-in-flight launch (mf_paged_attention_kv_write; the kernels'
+    // TAIL instances): a sequence's keys at or above kv_len - rows are its own
+    // new rows, read from new_k/new_v (row cu_seqlens[s] + key - (kv_len -
+    // rows)), and the launch's first w_blocks workgroups copy new rows
+    // [0, w_rows) into the pool through w_slots (a slot < 0 or >= w_num_slots
+    // is skipped). No item reads a slot that this launch writes, so nothing
+    // waits on the copy.
+    int num_kv_heads;
+    const int64_t* w_slots;
+    int w_rows;
+    int w_blocks;
+    int64_t w_num_slots;
 };
+
+// The copy of a written-in-flight launch: workgroup `wblock` of the leading
+// w_blocks. Every new row's K and V, head by head, go to the pool slot of
+// w_slots in 16-byte pieces: consecutive lanes take consecutive pieces of one
+// row (its heads are adjacent), so loads and stores coalesce.
+template <int DT>
+__device__ __forceinline__ void write_new_rows(const AttnArgs& a, int wblock) {
+    constexpr int ES = DT == MF_F32 ? 4 : 2;
+    const int cpr = a.head_dim * ES / 16;  // 16-byte pieces of one head's row
+    const int per_row = 2 * a.num_kv_heads * cpr;
+    const int total = a.w_rows * per_row;
+    for (int u = wblock * 256 + (int)threadIdx.x; u < total; u += a.w_blocks * 256) {
+        const int row = u / per_row;
+        int rest = u - row * per_row;
+        const int isv = rest >= a.num_kv_heads * cpr;
+        rest -= isv * a.num_kv_heads * cpr;
+        const int head = rest / cpr;
+        const int piece = rest - head * cpr;
+        const int64_t slot = a.w_slots[row];
+        if (slot < 0 || slot >= a.w_num_slots) continue;
+        const int64_t blk = slot / a.block_size;
+        const int64_t off = slot - blk * a.block_size;
+        const char* src = (isv ? a.new_v : a.new_k) + ((int64_t)row * a.n_sr + (int64_t)head * a.n_sh) * ES + piece * 16;
+        char* dst = const_cast<char*>(isv ? a.v_pool : a.k_pool) +
+                    (blk * a.p_sb + off * a.p_ss + (int64_t)head * a.p_sh) * ES + piece * 16;
+        *(uint4*)dst = *(const uint4*)src;
+    }
+}
 
 // ------------------------------------------------------------- MFMA wrappers
 // S^T tile: 16 keys x 16 columns, contraction over one 16-byte chunk of
@@ -369,7 +409,9 @@ constexpr int attn_lds_bytes() {
 
 // The body of one workgroup of the attention kernel: `block` is its index
 // among the workgroups that run items of this column-tile width.
-template <int DT, int DP, int NT, bool FAST>
+// TAIL: a written-in-flight launch (compiled apart, so the other launches
+// keep their register budget).
+template <int DT, int DP, int NT, bool FAST, bool TAIL = false>
 __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     constexpr int ES = DT == MF_F32 ? 4 : 2;
     constexpr int EPL = 16 / ES;      // elements per 16-byte chunk
@@ -397,7 +439,11 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     const int row0 = it[8];
     const int ncols = it[9] * a.G;
     const int kv_len = it[10];
-    const int pool_len = a.pool_lens == nullptr ? kv_len : a.pool_lens[s];
+    // Keys below pool_len are in the pool; the rest are in-flight rows of the
+    // sequence's own new tokens (a verify pass: pool_lens; a written-in-flight
+    // step: everything past the keys before the sequence's rows).
+    const bool inflight = TAIL || a.pool_lens != nullptr;
+    const int pool_len = TAIL ? kv_len - it[9] : (a.pool_lens != nullptr ? a.pool_lens[s] : kv_len);
     const int D = a.head_dim;
 
     // The loads that need nothing but the item go out together -- block-table
@@ -410,8 +456,8 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // readlane. On a verify pass
     // that is every tile holding a pool key (the boundary tile included);
     // pool_end is the end of the tiles lying wholly in the pool.
-    const int tbl_end = a.pool_lens != nullptr ? max(kt0, min(kt1, (pool_len + 15) >> 4)) : kt1;
-    const int pool_end = a.pool_lens != nullptr ? max(kt0, min(kt1, pool_len >> 4)) : kt1;
+    const int tbl_end = inflight ? max(kt0, min(kt1, (pool_len + 15) >> 4)) : kt1;
+    const int pool_end = inflight ? max(kt0, min(kt1, pool_len >> 4)) : kt1;
     int tbl = 0, tbl_hi = 0;
     const int tbl_base = kt0;
     if constexpr (FAST) {
@@ -626,9 +672,28 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // with in-flight keys (a verify pass) that is only the tiles lying wholly
     // in the pool; the one or two tiles holding the boundary and the in-flight
     // candidates follow through the general per-key loads.
+    //
+    // Wide items whose workgroup shares one key range (the planner packs wide
+    // items that way, one column group per wave) stage each tile in LDS for
+    // all four waves (the workgroup-shared loop below). On a written-in-flight
+    // step that loop also takes the tiles holding new rows, reading each
+    // lane's key from the pool or from the new rows.
+    bool wg_shared = false;
+    if constexpr (FAST && DT != MF_F32 && NT > 1) {
+        if ((block + 1) * kWaves <= num_items) {
+            const int32_t* i0 = a.items + (int64_t)block * kWaves * MF_PLAN_ITEM_INTS;
+            wg_shared = true;
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) {
+                const int32_t* iw = i0 + w * MF_PLAN_ITEM_INTS;
+                wg_shared = wg_shared && iw[0] == i0[0] && iw[1] == i0[1] && iw[4] == i0[4] && iw[5] == i0[5];
+            }
+        }
+    }
+    const bool shared_inflight = TAIL && wg_shared;
     int fast_end = kt_end;
     if constexpr (FAST) {
-        if (a.pool_lens != nullptr) fast_end = max(kt0, min(kt_end, pool_len >> 4));
+        if (inflight && !shared_inflight) fast_end = max(kt0, min(kt_end, pool_len >> 4));
     }
     // Per-tile work is branch-free apart from wave-uniform decisions: every
     // column tile's MFMAs run (tiles past nct hold zero queries and are never
@@ -764,18 +829,6 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // chunks are stored xor-swizzled by key, so the fragment reads (16 keys x
     // one chunk) hit distinct banks; V rows are read 16 lanes to a row,
     // conflict-free. One barrier per stage.
-    bool wg_shared = false;
-    if constexpr (FAST && DT != MF_F32 && NT > 1) {
-        if ((block + 1) * kWaves <= num_items) {
-            const int32_t* i0 = a.items + (int64_t)block * kWaves * MF_PLAN_ITEM_INTS;
-            wg_shared = true;
-#pragma unroll
-            for (int w = 1; w < kWaves; ++w) {
-                const int32_t* iw = i0 + w * MF_PLAN_ITEM_INTS;
-                wg_shared = wg_shared && iw[0] == i0[0] && iw[1] == i0[1] && iw[4] == i0[4] && iw[5] == i0[5];
-            }
-        }
-    }
     if constexpr (FAST && DT != MF_F32 && NT > 1) {
         if (wg_shared) {
             constexpr int RB = DP * ES;             // bytes of one key row
@@ -802,7 +855,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
             // the block (vector types rather than arrays keep them in registers)
             typedef uint32_t offs_t __attribute__((ext_vector_type(NI)));
             typedef uint32_t regs_t __attribute__((ext_vector_type(4 * NI * TPS)));
-            offs_t src_off;
+            offs_t src_off, key_of, piece_of;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const int base = ((i * kWaves + wave) * 1024) % STAGE;
@@ -811,6 +864,18 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                 const int key = p2 / RB, slot = (p2 % RB) >> 4;
                 const int q = isv ? slot : (slot ^ (key & (NCH - 1)));
                 src_off[i] = (uint32_t)key * v_row_bytes + (uint32_t)q * 16;
+                key_of[i] = (uint32_t)key;
+                piece_of[i] = (uint32_t)q * 16;
+            }
+            // in-flight key k of this kv head: K row at ibase + k * irow_bytes,
+            // its V row iv_off bytes on (so the loop holds three numbers, not
+            // both tensors and their strides)
+            const char* ibase = a.new_k;
+            int64_t irow_bytes = 0, iv_off = 0;
+            if (shared_inflight) {
+                irow_bytes = a.n_sr * ES;
+                ibase = a.new_k + ((int64_t)(row0 - pool_len) * a.n_sr + (int64_t)h * a.n_sh) * ES;
+                iv_off = a.new_v - a.new_k;
             }
             // Loads are unconditional (a wave without a piece of a small tile
             // re-reads another wave's piece and does not store it; tiles past
@@ -819,12 +884,24 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
             auto fetch = [&](int t0, regs_t& r) __attribute__((always_inline)) {
 #pragma unroll
                 for (int u = 0; u < TPS; ++u) {
-                    const int phys = tbl_at(min(t0 + u, wg_end - 1) - kt0);
+                    const int t = min(t0 + u, wg_end - 1);
+                    const int phys = tbl_at(t - kt0);
                     const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
 #pragma unroll
                     for (int i = 0; i < NI; ++i) {
                         const int base = ((i * kWaves + wave) * 1024) % STAGE;
-                        const uint4 v = *(const uint4*)((base >= 16 * RB ? a.v_pool : a.k_pool) + boff + src_off[i]);
+                        const bool isv = base >= 16 * RB;
+                        const char* src = (isv ? a.v_pool : a.k_pool) + boff + src_off[i];
+                        if (shared_inflight) {
+                            // this lane's key is a new row of the sequence
+                            // (clamped to its last row past the context; those
+                            // keys are masked and their V cleared)
+                            const int key = t * 16 + (int)key_of[i];
+                            const char* isrc = ibase + (isv ? iv_off : 0) +
+                                               (int64_t)min(key, kv_len - 1) * irow_bytes + piece_of[i];
+                            src = key >= pool_len ? isrc : src;
+                        }
+                        const uint4 v = *(const uint4*)src;
                         const int w = 4 * (u * NI + i);
                         r[w] = v.x;
                         r[w + 1] = v.y;
@@ -1098,10 +1175,18 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     }
 }
 
-template <int DT, int DP, int NT, bool FAST>
+template <int DT, int DP, int NT, bool FAST, bool TAIL = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<DT, DP, NT>())))
 void attn_kernel(AttnArgs a) {
-    attn_body<DT, DP, NT, FAST>(a, blockIdx.x);
+    if constexpr (TAIL) {
+        // the copy workgroups first (measured on the C2 step: 53.7 us per
+        // layer against 55.7 with them last)
+        const int b = blockIdx.x;
+        if (b < a.w_blocks) write_new_rows<DT>(a, b);
+        else attn_body<DT, DP, NT, FAST, true>(a, b - a.w_blocks);
+    } else {
+        attn_body<DT, DP, NT, FAST>(a, blockIdx.x);
+    }
 }
 
 // Single-tile and wide items of one plan in one launch: the first
@@ -1135,6 +1220,28 @@ void attn_mixed_kernel(AttnArgs narrow, AttnArgs wide, int wide_blocks) {
     const int narrow_blocks = (int)gridDim.x - wide_blocks;
     if (b < narrow_blocks) attn_body<DT, DP, 1, true>(narrow, b);
     else attn_body<DT, DP, NTW, true>(wide, b - narrow_blocks);
+}
+
+// The written-in-flight form: the copy workgroups first, then the narrow and
+// wide ones. One argument block (the wide items differ only in their list):
+// the larger body needs the scalar registers a second block would take.
+template <int DT, int DP, int NTW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(mixed_waves_per_eu<DT, DP, NTW>())))
+void attn_mixed_tail_kernel(AttnArgs a, const int32_t* wide_items, int wide_num_items,
+                            const int32_t* wide_dev_count, int wide_blocks) {
+    const int b = blockIdx.x - a.w_blocks;
+    const int narrow_blocks = (int)gridDim.x - a.w_blocks - wide_blocks;
+    if (b < 0) {
+        write_new_rows<DT>(a, blockIdx.x);
+    } else if (b < narrow_blocks) {
+        attn_body<DT, DP, 1, true, true>(a, b);
+    } else {
+        AttnArgs w = a;
+        w.items = wide_items;
+        w.num_items = wide_num_items;
+        w.dev_count = wide_dev_count;
+        attn_body<DT, DP, NTW, true, true>(w, b - narrow_blocks);
+    }
 }
 
 // ------------------------------------------------------------ decode slices
@@ -1497,7 +1604,10 @@ int launch_merge(const AttnArgs& a, const int32_t* merges, int64_t n_merges, hip
     return check_launch();
 }
 
-template <int DT, int DP>
+// TAIL: a written-in-flight launch (16-token blocks and unpadded head_dim
+// only: `fast`); its copy workgroups ride in the first launch, or in a
+// copy-only launch when there are no items.
+template <int DT, int DP, bool TAIL = false>
 int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t n_wide,
                      const int32_t* merges, int64_t n_merges, bool fast, const int32_t* dev_counts,
                      hipStream_t stream) {
@@ -1505,6 +1615,20 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
     // a merges-only call (no items) still runs the separate merge kernel.
     const bool fused = a.counters != nullptr && (n_narrow + n_wide) > 0;
     constexpr int NTW = wide_tiles(DT, DP);
+    if constexpr (TAIL) {
+        if (!fast) return MF_ERR_UNSUPPORTED;
+        if (a.w_blocks > 0 && n_narrow + n_wide == 0) {
+            AttnArgs aw = a;
+            aw.items = items;
+            aw.num_items = 0;
+            aw.dev_count = nullptr;
+            hipLaunchKernelGGL((attn_kernel<DT, DP, 1, true, true>), dim3((unsigned)a.w_blocks), dim3(256),
+                               (attn_lds_bytes<DT, DP, 1, true>()), stream, aw);
+            if (int st = check_launch()) return st;
+        }
+    } else {
+        a.w_blocks = 0;
+    }
 #if MF_MIXED_LAUNCH
     if constexpr (NTW > 1 && DT != MF_F32) {
         if (fast && n_narrow > 0 && n_wide > 0) {
@@ -1516,13 +1640,18 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
             aw.num_items = (int)n_wide;
             aw.dev_count = dev_counts ? dev_counts + 1 : nullptr;
             const int64_t wide_blocks = (n_wide + kWaves - 1) / kWaves;
-            const dim3 grid((unsigned)(wide_blocks + (n_narrow + kWaves - 1) / kWaves));
+            const dim3 grid((unsigned)(a.w_blocks + wide_blocks + (n_narrow + kWaves - 1) / kWaves));
             constexpr int lds = attn_lds_bytes<DT, DP, 1, true>() > attn_lds_bytes<DT, DP, NTW, true>()
                                     ? attn_lds_bytes<DT, DP, 1, true>() : attn_lds_bytes<DT, DP, NTW, true>();
-            hipLaunchKernelGGL((attn_mixed_kernel<DT, DP, NTW>), grid, dim3(256), lds, stream, an, aw,
-                               (int)wide_blocks);
+            if constexpr (TAIL)
+                hipLaunchKernelGGL((attn_mixed_tail_kernel<DT, DP, NTW>), grid, dim3(256), lds, stream, an,
+                                   aw.items, aw.num_items, aw.dev_count, (int)wide_blocks);
+            else
+                hipLaunchKernelGGL((attn_mixed_kernel<DT, DP, NTW>), grid, dim3(256), lds, stream, an, aw,
+                                   (int)wide_blocks);
             if (int st = check_launch()) return st;
             n_narrow = n_wide = 0;
+            a.w_blocks = 0;
         }
     }
 #endif
@@ -1530,25 +1659,26 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
         a.items = items;
         a.num_items = (int)n_narrow;
         a.dev_count = dev_counts ? dev_counts + 0 : nullptr;
-        const dim3 grid((unsigned)((n_narrow + kWaves - 1) / kWaves));
+        const dim3 grid((unsigned)(a.w_blocks + (n_narrow + kWaves - 1) / kWaves));
         if (fast)
-            hipLaunchKernelGGL((attn_kernel<DT, DP, 1, true>), grid, dim3(256), (attn_lds_bytes<DT, DP, 1, true>()),
-                               stream, a);
-        else
+            hipLaunchKernelGGL((attn_kernel<DT, DP, 1, true, TAIL>), grid, dim3(256),
+                               (attn_lds_bytes<DT, DP, 1, true>()), stream, a);
+        else if constexpr (!TAIL)
             hipLaunchKernelGGL((attn_kernel<DT, DP, 1, false>), grid, dim3(256), (attn_lds_bytes<DT, DP, 1, false>()),
                                stream, a);
         if (int st = check_launch()) return st;
+        a.w_blocks = 0;
     }
     if constexpr (NTW > 1) {
         if (n_wide > 0) {
             a.items = items + n_narrow * MF_PLAN_ITEM_INTS;
             a.num_items = (int)n_wide;
             a.dev_count = dev_counts ? dev_counts + 1 : nullptr;
-            const dim3 grid((unsigned)((n_wide + kWaves - 1) / kWaves));
+            const dim3 grid((unsigned)(a.w_blocks + (n_wide + kWaves - 1) / kWaves));
             if (fast)
-                hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, true>), grid, dim3(256),
+                hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, true, TAIL>), grid, dim3(256),
                                    (attn_lds_bytes<DT, DP, NTW, true>()), stream, a);
-            else
+            else if constexpr (!TAIL)
                 hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, false>), grid, dim3(256),
                                    (attn_lds_bytes<DT, DP, NTW, false>()), stream, a);
             if (int st = check_launch()) return st;
@@ -2091,7 +2221,9 @@ int paged_attention_impl(
     int64_t new_stride_head, int num_q_heads, int num_kv_heads, int head_dim, float scale,
     const int32_t* plan_items, int64_t num_items_narrow, int64_t num_items_wide,
     const int32_t* plan_merges, int64_t num_merges, float* partials, int64_t partials_floats,
-    int32_t* merge_counters, const int32_t* device_counts, mf_stream_t stream, bool sliced = false) {
+    int32_t* merge_counters, const int32_t* device_counts, mf_stream_t stream, bool sliced = false,
+    const int64_t* write_slots = nullptr, int64_t write_rows = 0, int64_t write_num_slots = 0,
+    bool tail_inflight = false) {
     using namespace mf;
     if (!(std::fabs(scale) < INFINITY)) return MF_ERR_ARG;  // NaN or infinite
     if (!dtype_ok(dtype) || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
@@ -2101,7 +2233,7 @@ int paged_attention_impl(
     if (!DP) return MF_ERR_UNSUPPORTED;
     // A call may carry only items (partials left for a later merge-only call)
     // or only merges; both are how a caller times the two kernels apart.
-    if (num_items_narrow + num_items_wide == 0 && num_merges == 0) return MF_OK;
+    if (num_items_narrow + num_items_wide == 0 && num_merges == 0 && write_rows == 0) return MF_OK;
     if (!q || !out || !k_pool || !v_pool || !block_tables || !cu_seqlens || !kv_lens || !positions)
         return MF_ERR_ARG;
     if (num_items_narrow + num_items_wide > 0 && !plan_items) return MF_ERR_ARG;
@@ -2160,16 +2292,48 @@ int paged_attention_impl(
     a.part_dstride = part_dstride_for(head_dim);
     a.merges = plan_merges;
     a.counters = num_merges > 0 ? merge_counters : nullptr;
+    a.num_kv_heads = num_kv_heads;
     const bool fast = block_size == 16 && head_dim == DP;
     hipStream_t st = (hipStream_t)stream;
+    if (tail_inflight) {
+        if (!new_k || !new_v || row_map || pool_lens || write_rows < 0 || write_num_slots < 0) return MF_ERR_ARG;
+        if (write_rows > 0 && !write_slots) return MF_ERR_ARG;
+        if ((new_stride_row % epl) || (new_stride_head % epl) || (((uintptr_t)new_k | (uintptr_t)new_v) & 15))
+            return MF_ERR_ARG;
+        if (!fast) {
+            // other block sizes and padded head_dims: the write, then the
+            // attention reading every key from the pool (same result, two launches)
+            if (write_rows > 0) {
+                if (int sw = mf_kv_write(new_k, new_v, dtype, new_stride_row, new_stride_head, write_slots,
+                                         write_rows, const_cast<void*>(k_pool), const_cast<void*>(v_pool), dtype,
+                                         pool_stride_block, pool_stride_slot, pool_stride_head, block_size,
+                                         write_num_slots, num_kv_heads, head_dim, stream))
+                    return sw;
+            }
+            tail_inflight = false;
+        } else {
+            // the copy: 16-byte pieces of every new row's K and V, about four
+            // per thread of the copy workgroups
+            const int64_t pieces = write_rows * 2 * num_kv_heads * (head_dim * es / 16);
+            if (pieces > INT_MAX / 2) return MF_ERR_ARG;
+            a.w_slots = write_slots;
+            a.w_rows = (int)write_rows;
+            a.w_num_slots = write_num_slots;
+            a.w_blocks = pieces > 0 ? (int)std::min<int64_t>(1024, (pieces + 1023) / 1024) : 0;
+        }
+    }
 
-    if (sliced && (!fast || row_map || pool_lens || merge_counters || device_counts)) return MF_ERR_UNSUPPORTED;
+    if (sliced && (!fast || row_map || pool_lens || merge_counters || device_counts || tail_inflight))
+        return MF_ERR_UNSUPPORTED;
 #define MF_ATTN_CASE(DT, DPV)                                                                  \
     if (dtype == DT && DP == DPV)                                                              \
         return sliced ? launch_slices<DT, DPV>(a, plan_items, num_items_narrow, num_kv_heads,  \
                                                plan_merges, num_merges, st)                    \
-                      : launch_attention<DT, DPV>(a, plan_items, num_items_narrow, num_items_wide, \
-                                                  plan_merges, num_merges, fast, device_counts, st);
+                      : (tail_inflight ? launch_attention<DT, DPV, true>(a, plan_items, num_items_narrow, \
+                                                                         num_items_wide, plan_merges, num_merges, \
+                                                                         fast, device_counts, st) \
+                                       : launch_attention<DT, DPV>(a, plan_items, num_items_narrow, num_items_wide, \
+                                                                   plan_merges, num_merges, fast, device_counts, st));
     MF_ATTN_CASE(MF_F32, 16)
     MF_ATTN_CASE(MF_F32, 32)
     MF_ATTN_CASE(MF_F32, 64)
@@ -2243,6 +2407,26 @@ extern "C" int mf_paged_attention_counted(
                                 num_kv_heads, head_dim, scale, plan_items, capacity_narrow, capacity_wide,
                                 plan_merges, capacity_merges, partials, partials_floats, nullptr,
                                 device_counts, stream);
+}
+
+extern "C" int mf_paged_attention_kv_write(
+    const void* q, int64_t q_stride_row, int64_t q_stride_head, void* out, int64_t out_stride_row,
+    int64_t out_stride_head, int dtype, void* k_pool, void* v_pool, int64_t pool_stride_block,
+    int64_t pool_stride_slot, int64_t pool_stride_head, int block_size, const int32_t* block_tables,
+    int64_t block_table_stride, const int32_t* cu_seqlens, const int32_t* kv_lens, const int64_t* positions,
+    const void* new_k, const void* new_v, int64_t new_stride_row, int64_t new_stride_head,
+    const int64_t* slot_mapping, int64_t num_new_rows, int64_t num_slots, int num_q_heads, int num_kv_heads,
+    int head_dim, float scale, const int32_t* plan_items, int64_t num_items_narrow, int64_t num_items_wide,
+    const int32_t* plan_merges, int64_t num_merges, const int32_t* device_counts, float* partials,
+    int64_t partials_floats, mf_stream_t stream) {
+    return paged_attention_impl(q, q_stride_row, q_stride_head, out, out_stride_row, out_stride_head, dtype,
+                                k_pool, v_pool, pool_stride_block, pool_stride_slot, pool_stride_head,
+                                block_size, block_tables, block_table_stride, cu_seqlens, kv_lens, positions,
+                                nullptr, nullptr, new_k, new_v, new_stride_row, new_stride_head, num_q_heads,
+                                num_kv_heads, head_dim, scale, plan_items, num_items_narrow, num_items_wide,
+                                plan_merges, num_merges, partials, partials_floats, nullptr, device_counts,
+                                stream, /*sliced=*/false, slot_mapping, num_new_rows, num_slots,
+                                /*tail_inflight=*/true);
 }
 
 // ------------------------------------------------------- no-allocation entry

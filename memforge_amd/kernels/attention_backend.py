@@ -75,7 +75,7 @@ class _VarlenBinding:
     """
 
     __slots__ = ("pool", "block_tables", "seq_ids", "positions", "block_wise", "used", "_meta",
-                 "pool_lens", "num_rows", "timer")
+                 "pool_lens", "num_rows", "timer", "write_slots")
 
     def __init__(self, pool, block_tables, seq_ids, positions, block_wise=False, pool_lens=None):
         self.pool = pool
@@ -88,9 +88,17 @@ class _VarlenBinding:
         self.pool_lens = pool_lens
         self.num_rows = len(self.seq_ids)
         self.timer = None  # a sampled pass's event record (engine telemetry)
+        self.write_slots = None
 
     @classmethod
-    def from_packed(cls, pool, meta: dict, num_rows: int, pool_lens: Optional[torch.Tensor] = None):
+    def from_packed(cls, pool, meta: dict, num_rows: int, pool_lens: Optional[torch.Tensor] = None,
+                    write_slots: Optional[torch.Tensor] = None):
+        """A prepared binding. ``write_slots`` (the step's slot_mapping, with a
+        cache made by ``VarlenPackedCache.from_slot_mapping(...,
+        write_in_attention=True)``): every layer's attention launch also writes
+        the new K/V rows it is handed into the pool and reads each sequence's
+        new keys from those rows (the step's rows are every sequence's new
+        tokens, ending its context)."""
         b = cls.__new__(cls)
         b.pool = pool
         b.block_tables = []
@@ -102,6 +110,7 @@ class _VarlenBinding:
         b.pool_lens = pool_lens
         b.num_rows = num_rows
         b.timer = None
+        b.write_slots = write_slots
         return b
 
     def meta(self, num_q_heads: int, head_dim: int, dtype: torch.dtype, device) -> dict:
@@ -225,6 +234,16 @@ def _varlen_forward(module, query, key, value, scaling, binding: _VarlenBinding)
         nv = value[0].to(dtype).permute(1, 0, 2)
     timer = binding.timer
     began = timer.start(layer) if timer is not None else None
+    if binding.write_slots is not None:
+        nat.paged_attention_kv_write(
+            q_rows, out[0], pool.layer_view(layer), meta["block_tables"], meta["cu_seqlens"],
+            meta["kv_lens"], meta["positions"], meta["plan"],
+            scaling if scaling is not None else 1.0 / math.sqrt(d), pool.spec.num_kv_heads,
+            key[0].to(dtype).permute(1, 0, 2), value[0].to(dtype).permute(1, 0, 2), binding.write_slots,
+        )
+        if timer is not None:
+            timer.stop("attention_kv_write", began)
+        return out.to(query.dtype)
     nat.paged_attention(
         q_rows, out[0], pool.layer_view(layer), meta["block_tables"], meta["cu_seqlens"],
         meta["kv_lens"], meta["positions"], meta["plan"],

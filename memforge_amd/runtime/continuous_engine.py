@@ -235,13 +235,16 @@ class ContinuousBatchingEngine:
                  block_attention: bool = False, max_prefill_tokens_per_step: int = 0,
                  draft_model=None, lookahead_k: int = 0, fused_prefill: bool = False,
                  paged_attn_kernel: str = "gather", draft_cuda_graph=False, paged_cuda_graph=False,
-                 telemetry_sample_every: int = 16):
+                 telemetry_sample_every: int = 16, fused_kv_write: bool = True):
         if not HAS_CPP_ENGINE:
             raise RuntimeError("The native memforge_c extension is required; build it with "
                                "`python -m memforge_amd._build`")
         if decode_view_cache:
             raise NotImplementedError("the contiguous decode mirror is not part of memforge_amd")
         self.model = model
+        # each layer's KV write rides in its attention launch (one launch per
+        # layer instead of two); needs the pool in the model's dtype
+        self._fused_kv_write = bool(fused_kv_write)
         self.tokenizer = tokenizer
         self.device = device or str(next(model.parameters()).device)
         if torch.device(self.device).type != "cuda":
@@ -280,7 +283,8 @@ class ContinuousBatchingEngine:
         if paged_cuda_graph:
             if paged_cuda_graph != "auto" or self._graph_heads_ok(model):
                 self._paged_graph = GraphedPagedDecoder(model, self.pool, max_batch=max_num_seqs,
-                                                        max_model_len=max_model_len)
+                                                        max_model_len=max_model_len,
+                                                        fuse_kv_write=fused_kv_write)
 
         # Draft proposals (False | "batched" | "batched-unrolled" | "auto" |
         # True, as the reference's draft_cuda_graph): the batched forms draft
@@ -376,7 +380,9 @@ class ContinuousBatchingEngine:
             "data_path": {
                 "library": nat.LIB_PATH.name,
                 "arch": "gfx950",
-                "step": "one packed varlen pass (ragged pack, per-layer KV write and paged attention)",
+                "step": "one packed varlen pass (ragged pack, then per layer "
+                        + ("one launch for the KV write and the paged attention)" if self._fused_kv_write
+                           else "the KV write and the paged attention)"),
                 "speculative_resolve": "one mf_spec_verify launch per round" if self._batched_resolve
                                        else "one row at a time",
                 "telemetry_sample_every": self._meter.every,
@@ -572,7 +578,8 @@ class ContinuousBatchingEngine:
         try:
             res = packed_forward(self.model, self.pool, [e["tokens"] for e in plan],
                                  [e["start"] for e in plan], [e["table"] for e in plan],
-                                 [int(cu[i + 1]) - 1 for i in emit], timer=timer)
+                                 [int(cu[i + 1]) - 1 for i in emit], timer=timer,
+                                 fuse_kv_write=self._fused_kv_write)
         except IndexError as exc:
             raise IndexError(f"{exc} (sequences {[e['rt'].seq_id for e in plan]})") from None
         self.total_forward_passes += 1

@@ -6,8 +6,9 @@ keys, so they keep their names. On top, ``DataPathMeter`` measures the
 bandwidth the data-path kernels reach inside the engine, without a profiler:
 
 * every ``every``-th forward pass is sampled;
-* on a sampled eager pass, one layer's KV write and attention launch are
-  timed with HIP events on the stream the kernels run on. An eager pass is
+* on a sampled eager pass, one layer's KV write and attention launch (or
+  the one launch doing both, family ``attention_kv_write``) are timed with
+  HIP events on the stream the kernels run on. An eager pass is
   usually host-bound -- the GPU waits for each launch -- so an event recorded
   just before a launch would time the host's enqueue latency too. The timed
   launch is therefore preceded by a short GPU spin (about 40 us, recalibrated
@@ -127,8 +128,9 @@ class DataPathMeter:
         """Algorithmic bytes of one layer's attention and KV write."""
         kv = sum(int(n) for n in kv_lens)
         tables = sum((int(n) + self.block_size - 1) // self.block_size for n in kv_lens) * 4
-        return {"attention": 2 * kv * self.kv_row + tables + 2 * rows * self.q_row,
-                "kv_write": 2 * 2 * rows * self.kv_row + 8 * rows}
+        attention = 2 * kv * self.kv_row + tables + 2 * rows * self.q_row
+        kv_write = 2 * 2 * rows * self.kv_row + 8 * rows
+        return {"attention": attention, "kv_write": kv_write, "attention_kv_write": attention + kv_write}
 
     def step_bytes(self, kv_lens: List[int], rows: int) -> int:
         """Bytes roofline of a whole pass: weights once, every layer's data path."""
@@ -166,7 +168,7 @@ class DataPathMeter:
         """The measured figures, one group of keys per kernel family."""
         self.poll()
         out: Dict[str, Any] = {"data_path_sample_every": self.every, "hbm_peak_gbps": HBM_PEAK_GBPS}
-        for family in ("attention", "kv_write", "decode_graph"):
+        for family in ("attention", "kv_write", "attention_kv_write", "decode_graph"):
             t = self._totals.get(family)
             if t is None or t[2] <= 0:
                 out.update({f"{family}_samples": 0, f"{family}_gbps": None, f"{family}_hbm_frac": None,

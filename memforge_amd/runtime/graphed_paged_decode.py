@@ -6,9 +6,9 @@ each of B sequences against the paged pool as one graph replay, with
 everything that varies between steps held in device buffers that the graph
 reads. The reference graphs a gather of every context plus the model's sdpa
 attention; here the graph holds the packed varlen pass itself -- the ragged
-pack, every layer's KV write through slot_mapping and the varlen attention
-kernel reading the pool in place -- so nothing is gathered or padded by
-context length.
+pack and, per layer, one attention launch that writes the layer's new K/V
+through slot_mapping and attends with the pool read in place -- so nothing is
+gathered or padded by context length.
 
 What makes the attention capturable is mf_paged_attention_counted: its grids
 are sized by a capacity fixed at capture time, and the live item and merge
@@ -81,9 +81,11 @@ class _Bucket:
         meta = {"block_tables": self.packed.block_tables, "cu_seqlens": self.packed.cu_seqlens,
                 "kv_lens": self.packed.kv_lens, "positions": self.packed.positions, "row_map": None,
                 "plan": self.plan}
-        self.binding = attention_backend._VarlenBinding.from_packed(owner.pool, meta, b)
+        fuse = owner.fuse_kv_write
+        self.binding = attention_backend._VarlenBinding.from_packed(
+            owner.pool, meta, b, write_slots=self.packed.slot_mapping if fuse else None)
         self.cache = VarlenPackedCache.from_slot_mapping(owner.pool, owner.pool.spec.num_layers,
-                                                         self.packed.slot_mapping)
+                                                         self.packed.slot_mapping, write_in_attention=fuse)
         self.graph = None
         self.logits = None
         self.copied = None
@@ -93,10 +95,11 @@ class GraphedPagedDecoder:
     """Decode one token for each of B sequences against the paged pool, as a graph."""
 
     def __init__(self, model, pool, max_batch: int, max_model_len: int, ctx_bucket: int = 32,
-                 attn_kernel: str = "gather", num_splits: int = 8):
+                 attn_kernel: str = "gather", num_splits: int = 8, fuse_kv_write: bool = True):
         # ctx_bucket / attn_kernel / num_splits are accepted for the
         # reference's signature: nothing here is padded to a context bucket and
-        # there is one attention kernel.
+        # there is one attention kernel. fuse_kv_write: every layer's KV write
+        # rides in its attention launch (mf_paged_attention_kv_write).
         if not str(pool.spec.device).startswith("cuda"):
             raise ValueError("graphed paged decode needs a GPU device")
         hq = model.config.num_attention_heads
@@ -106,6 +109,7 @@ class GraphedPagedDecoder:
         if not attention_backend.register():
             raise RuntimeError("the transformers attention registry is required")
         self.model, self.pool = model, pool
+        self.fuse_kv_write = bool(fuse_kv_write) and pool.key_pool.dtype == model.dtype
         self.device = pool.spec.device
         self.bs = pool.block_size
         self.max_batch = max(1, int(max_batch))

@@ -4,9 +4,11 @@ Every contributing sequence adds a run of query tokens at consecutive
 positions ``start .. start + len - 1`` whose K/V are written through its block
 table. The descriptors, tables, token ids and attention plan are staged in
 pinned memory and cross PCIe in one copy; the ragged-pack kernel builds token ids, positions,
-slot_mapping, cu_seqlens and padded tables on the device; each layer's cache
-update is the KV-write kernel and its attention the varlen kernel reading the
-pool in place. This is the reference's fused varlen step
+slot_mapping, cu_seqlens and padded tables on the device; each layer's
+attention is one launch that writes the layer's new K/V through slot_mapping
+and attends with the pool read in place (the new keys read from the rows
+themselves) -- or, unfused, the KV-write kernel in the cache update followed
+by the attention launch. This is the reference's fused varlen step
 (memforge_ml/runtime/continuous_engine.py:782-905) with the gather, the padding
 and the Python list building moved onto the GPU.
 """
@@ -35,13 +37,16 @@ class PackedPassResult:
 
 @torch.no_grad()
 def packed_forward(model, pool, tokens: Sequence[Sequence[int]], starts: Sequence[int],
-                   tables: Sequence[Sequence[int]], keep_rows: Sequence[int], timer=None) -> PackedPassResult:
+                   tables: Sequence[Sequence[int]], keep_rows: Sequence[int], timer=None,
+                   fuse_kv_write: bool = True) -> PackedPassResult:
     """Run ``model`` once over every sequence's ``tokens`` (written at
     ``starts[i]`` onward through ``tables[i]``) and return the logits of the
     packed rows ``keep_rows``. Raises IndexError when a run does not fit its
     table, and RuntimeError when a layer did not use the varlen kernel. With
     ``timer`` (a sampled pass's event record) every layer's KV write and
-    attention launch is bracketed by HIP events."""
+    attention launch is bracketed by HIP events. With ``fuse_kv_write`` each
+    layer's KV write rides in its attention launch (mf_paged_attention_kv_write)
+    instead of running as a launch of its own."""
     bs = pool.block_size
     spec = pool.spec
     B = len(tokens)
@@ -79,8 +84,10 @@ def packed_forward(model, pool, tokens: Sequence[Sequence[int]], starts: Sequenc
     meta = {"block_tables": packed.block_tables, "cu_seqlens": packed.cu_seqlens,
             "kv_lens": packed.kv_lens, "positions": packed.positions, "row_map": None,
             "plan": attn_plan}
-    binding = attention_backend._VarlenBinding.from_packed(pool, meta, T)
-    cache = VarlenPackedCache.from_slot_mapping(pool, spec.num_layers, packed.slot_mapping)
+    fuse = fuse_kv_write and pool.key_pool.dtype == model.dtype
+    binding = attention_backend._VarlenBinding.from_packed(pool, meta, T,
+                                                           write_slots=packed.slot_mapping if fuse else None)
+    cache = VarlenPackedCache.from_slot_mapping(pool, spec.num_layers, packed.slot_mapping, write_in_attention=fuse)
     binding.timer = cache.timer = timer
     with attention_backend.backend_enabled_on(model) as routed:
         if not routed:

@@ -50,6 +50,10 @@ class VarlenPackedCacheLayer(CacheLayerMixin):
             raise ValueError(f"{key_states.shape[-2]} key states for {self.owner.num_tokens} packed tokens")
         if self.owner.hold_new_kv:
             self.owner.new_kv[self.layer_idx] = (key_states, value_states)
+        elif self.owner.write_in_attention:
+            # the layer's attention launch writes these rows itself
+            # (mf_paged_attention_kv_write), reading them in flight meanwhile
+            pass
         else:
             timer = self.owner.timer
             began = timer.start(self.layer_idx) if timer is not None else None
@@ -144,6 +148,8 @@ class VarlenPackedCache(Cache):
 
     # a sampled pass's event record (engine telemetry); None: nothing is timed
     timer = None
+    # the pass's attention writes each layer's new rows (see from_slot_mapping)
+    write_in_attention = False
 
     def __init__(self, pool, num_layers: int, block_tables: Sequence[torch.Tensor], seq_ids: Sequence[int],
                  positions: Sequence[int]):
@@ -162,13 +168,19 @@ class VarlenPackedCache(Cache):
         super().__init__(layers=[VarlenPackedCacheLayer(self, i) for i in range(num_layers)])
 
     @classmethod
-    def from_slot_mapping(cls, pool, num_layers: int, slot_mapping: torch.Tensor) -> "VarlenPackedCache":
-        """Wrap a slot_mapping already built on the device by the ragged pack."""
+    def from_slot_mapping(cls, pool, num_layers: int, slot_mapping: torch.Tensor,
+                          write_in_attention: bool = False) -> "VarlenPackedCache":
+        """Wrap a slot_mapping already built on the device by the ragged pack.
+        With ``write_in_attention`` ``update`` writes nothing: the pass's
+        attention binding carries the slot_mapping and every layer's
+        attention launch writes the rows it is handed (one launch instead of
+        a write and an attention per layer); only valid under such a binding."""
         self = cls.__new__(cls)
         self.pool = pool
         self.block_tables, self.seq_ids, self.positions = [], [], []
         self.num_tokens = int(slot_mapping.numel())
         self.hold_new_kv = False
+        self.write_in_attention = bool(write_in_attention)
         self.new_kv = [None] * num_layers
         self.write_index = slot_mapping
         Cache.__init__(self, layers=[VarlenPackedCacheLayer(self, i) for i in range(num_layers)])

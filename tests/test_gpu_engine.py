@@ -614,15 +614,21 @@ def test_batched_speculative_resolve_keeps_seeded_output(model, draft, tok, draf
     assert runs[0][4] > 0 and runs[0][3] < runs[0][2]
 
 
-def test_telemetry_reports_measured_data_path_bandwidth(model, tok):
+@pytest.mark.parametrize("fused", [True, False])
+def test_telemetry_reports_measured_data_path_bandwidth(model, tok, fused):
     """telemetry() carries the data path's measured figures (HIP events on
     sampled passes): attention and KV-write GB/s and fraction of the HBM peak
-    on eager passes, and the bytes-roofline fraction of graph-replayed decode
-    steps; describe() names the pool layout."""
-    engine = make_engine(model, tok, paged_cuda_graph=True, telemetry_sample_every=1)
+    on eager passes (one family for the launch doing both when the write rides
+    in the attention launch), and the bytes-roofline fraction of
+    graph-replayed decode steps; describe() names the pool layout."""
+    engine = make_engine(model, tok, paged_cuda_graph=True, telemetry_sample_every=1, fused_kv_write=fused)
     engine.generate(PROMPTS, greedy(6, stop_on_eos=False))
     t = engine.telemetry()
-    for family in ("attention", "kv_write", "decode_graph"):
+    timed = ("attention_kv_write",) if fused else ("attention", "kv_write")
+    idle = ("attention", "kv_write") if fused else ("attention_kv_write",)
+    for family in idle:
+        assert t[f"{family}_samples"] == 0 and t[f"{family}_gbps"] is None, family
+    for family in (*timed, "decode_graph"):
         assert t[f"{family}_samples"] > 0, family
         assert t[f"{family}_gbps"] > 0 and 0 < t[f"{family}_hbm_frac"] < 1, (family, t[f"{family}_gbps"])
         assert t[f"{family}_us_per_launch"] > 0 and t[f"{family}_bytes_per_launch"] > 0
@@ -631,7 +637,7 @@ def test_telemetry_reports_measured_data_path_bandwidth(model, tok):
     assert pool["layout"] == "(layers, blocks, block_size, kv_heads, head_dim)" and pool["dtype"] == "torch.float32"
     off = make_engine(model, tok, telemetry_sample_every=0)
     off.generate(PROMPTS[:1], greedy(3))
-    assert off.telemetry()["attention_samples"] == 0 and off.telemetry()["attention_gbps"] is None
+    assert off.telemetry()["attention_kv_write_samples"] == 0 and off.telemetry()["attention_gbps"] is None
 
 
 def test_streamed_text_adds_up_to_the_final_text(model, tok):
