@@ -197,7 +197,7 @@ class PoolView:
         return PoolView(k, v, k.stride(0), k.stride(2), k.stride(1), bs, h, d)
 
 
-def _same_layout(a: torch.Tensor, b: torch.Tensor) -> bool:
+def same_layout(a: torch.Tensor, b: torch.Tensor) -> bool:
     """Same shape and the same strides on every axis longer than one (the
     stride of a length-one axis is never used to address an element)."""
     return a.shape == b.shape and all(x == y for x, y, n in zip(a.stride(), b.stride(), a.shape) if n > 1)
@@ -216,7 +216,7 @@ def kv_write(k_rows: torch.Tensor, v_rows: torch.Tensor, slots: torch.Tensor, po
     """Scatter (T, H, D) rows into pool slots ``slots`` (int64, device)."""
     _rows_ok(k_rows, "k_rows")
     _rows_ok(v_rows, "v_rows")
-    if not _same_layout(k_rows, v_rows):
+    if not same_layout(k_rows, v_rows):
         v_rows = v_rows.contiguous()
         k_rows = k_rows.contiguous()
     require_device(k_rows, v_rows, slots, pool.k)
@@ -240,7 +240,7 @@ def kv_gather(pool: PoolView, slots: torch.Tensor, k_rows: torch.Tensor, v_rows:
     """Copy pool slots ``slots`` into preallocated (T, H, D) rows."""
     _rows_ok(k_rows, "k_rows")
     _rows_ok(v_rows, "v_rows")
-    if not _same_layout(k_rows, v_rows):
+    if not same_layout(k_rows, v_rows):
         raise ValueError("k_rows and v_rows must share strides")
     require_device(k_rows, v_rows, slots, pool.k)
     if slots.dtype != torch.int64 or not slots.is_contiguous():
@@ -608,7 +608,7 @@ def paged_attention(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView
         if nk is None or nv is None:
             raise ValueError("pool_lens needs the in-flight new_k_rows/new_v_rows")
         require_device(pool_lens, nk, nv)
-        if not _same_layout(nk, nv):
+        if not same_layout(nk, nv):
             raise ValueError("in-flight K and V rows must share strides")
     bt_stride = block_tables.shape[1] if block_tables.dim() == 2 else 0
     _check(lib().mf_paged_attention(
@@ -648,7 +648,7 @@ def paged_attention_kv_write(q_rows: torch.Tensor, out_rows: torch.Tensor, pool:
     if q_rows.dtype != pool.k.dtype or out_rows.dtype != pool.k.dtype or new_k_rows.dtype != pool.k.dtype \
             or new_v_rows.dtype != pool.k.dtype:
         raise TypeError("query, output, new rows and pool must share a dtype")
-    if not _same_layout(new_k_rows, new_v_rows):
+    if not same_layout(new_k_rows, new_v_rows):
         raise ValueError("new K and V rows must share shape and strides")
     if slot_mapping.dtype != torch.int64 or not slot_mapping.is_contiguous():
         raise TypeError("slot_mapping must be a contiguous int64 tensor")
@@ -710,7 +710,7 @@ def paged_attention_noalloc(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: 
         if nk is None or nv is None:
             raise ValueError("pool_lens needs the in-flight new_k_rows/new_v_rows")
         require_device(pool_lens, nk, nv)
-        if not _same_layout(nk, nv):
+        if not same_layout(nk, nv):
             raise ValueError("in-flight K and V rows must share strides")
     bt_stride = block_tables.shape[1] if block_tables.dim() == 2 else 0
     _check(lib().mf_paged_attention_noalloc(
@@ -753,7 +753,7 @@ def paged_attention_packed(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: P
         if nk is None or nv is None:
             raise ValueError("pool_lens needs the in-flight new_k_rows/new_v_rows")
         require_device(nk, nv)
-        if not _same_layout(nk, nv):
+        if not same_layout(nk, nv):
             raise ValueError("in-flight K and V rows must share strides")
     dev = q_rows.device
     n_narrow, n_wide, n_merges, floats = (int(x) for x in counts)

@@ -235,11 +235,15 @@ def _varlen_forward(module, query, key, value, scaling, binding: _VarlenBinding)
     timer = binding.timer
     began = timer.start(layer) if timer is not None else None
     if binding.write_slots is not None:
+        # the launch reads K and V rows with one pair of strides
+        wk, wv = key[0].to(dtype).permute(1, 0, 2), value[0].to(dtype).permute(1, 0, 2)
+        if not nat.same_layout(wk, wv):
+            wk, wv = wk.contiguous(), wv.contiguous()
         nat.paged_attention_kv_write(
             q_rows, out[0], pool.layer_view(layer), meta["block_tables"], meta["cu_seqlens"],
             meta["kv_lens"], meta["positions"], meta["plan"],
-            scaling if scaling is not None else 1.0 / math.sqrt(d), pool.spec.num_kv_heads,
-            key[0].to(dtype).permute(1, 0, 2), value[0].to(dtype).permute(1, 0, 2), binding.write_slots,
+            scaling if scaling is not None else 1.0 / math.sqrt(d), pool.spec.num_kv_heads, wk, wv,
+            binding.write_slots,
         )
         if timer is not None:
             timer.stop("attention_kv_write", began)
