@@ -639,6 +639,112 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
             load_tile(max(kt0, min(kt0 + i, pool_end - 1)), kR[i], vR[i], kt0 + i > pool_end - 1, none);
     }
 
+    // ---- workgroup-shared key loop, first part. Wide items whose workgroup
+    // shares one key range (the planner packs wide items that way, one column
+    // group per wave) stage each 16-key K/V tile in LDS for all four waves
+    // (the loop itself follows below). Its first stage needs only the item and
+    // the block table, so it is fetched here, before the row positions are
+    // waited for: the setup then costs the block table's round trip and the
+    // stage's, overlapped with the positions', instead of three in a row
+    // (the positions only trim how far the range is read; the first stage is
+    // bounded by the item's range instead). On a written-in-flight step the
+    // loop also takes the tiles holding new rows, reading each lane's key from
+    // the pool or from the new rows.
+    constexpr int RB = DP * ES;             // bytes of one key row
+    constexpr int NCH = RB / 16;            // 16-byte chunks per row
+    constexpr int STAGE = 32 * RB;          // K tile, then V tile
+    constexpr int NI = (STAGE + kWaves * 1024 - 1) / (kWaves * 1024);  // 16-byte loads per lane per tile
+    // Tiles per LDS stage: each barrier and each refill covers TPS
+    // tiles, so a refill has TPS tiles of compute to arrive in.
+    // Measured on the C2 prefill items (bf16, D 64): 1 tile 42.0 us,
+    // 2 tiles 40.3 us, 4 tiles 39.2 us. Four would take the D 32
+    // kernel past 128 registers (three waves per SIMD), so other row
+    // sizes use two.
+    constexpr int TPS = RB == 128 ? 4 : 2;
+    // this lane's 16 bytes of each tile: LDS byte base + lane*16 of
+    // piece (i*4 + wave) mod STAGE, and the matching pool offset inside
+    // the block (vector types rather than arrays keep them in registers)
+    typedef uint32_t offs_t __attribute__((ext_vector_type(NI)));
+    typedef uint32_t regs_t __attribute__((ext_vector_type(4 * NI * TPS)));
+    bool wg_shared = false;
+    if constexpr (FAST && DT != MF_F32 && NT > 1) {
+        if ((block + 1) * kWaves <= num_items) {
+            const int32_t* i0 = a.items + (int64_t)block * kWaves * MF_PLAN_ITEM_INTS;
+            wg_shared = true;
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) {
+                const int32_t* iw = i0 + w * MF_PLAN_ITEM_INTS;
+                wg_shared = wg_shared && iw[0] == i0[0] && iw[1] == i0[1] && iw[4] == i0[4] && iw[5] == i0[5];
+            }
+        }
+    }
+    const bool shared_inflight = TAIL && wg_shared;
+    offs_t src_off, key_of, piece_of;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int base = ((i * kWaves + wave) * 1024) % STAGE;
+        const bool isv = base >= 16 * RB;
+        const int p2 = (isv ? base - 16 * RB : base) + lane * 16;
+        const int key = p2 / RB, slot = (p2 % RB) >> 4;
+        const int q = isv ? slot : (slot ^ (key & (NCH - 1)));
+        src_off[i] = (uint32_t)key * v_row_bytes + (uint32_t)q * 16;
+        key_of[i] = (uint32_t)key;
+        piece_of[i] = (uint32_t)q * 16;
+    }
+    // in-flight key k of this kv head: K row at ibase + k * irow_bytes,
+    // its V row iv_off bytes on (so the loop holds three numbers, not
+    // both tensors and their strides)
+    const char* ibase = a.new_k;
+    int64_t irow_bytes = 0, iv_off = 0;
+    if (shared_inflight) {
+        irow_bytes = a.n_sr * ES;
+        ibase = a.new_k + ((int64_t)(row0 - pool_len) * a.n_sr + (int64_t)h * a.n_sh) * ES;
+        iv_off = a.new_v - a.new_k;
+    }
+    // Tiles the fetches clamp to: the item's range for the first stage, the
+    // workgroup's last read tile once the positions are in.
+    int fetch_end = kt1;
+    // Loads are unconditional (a wave without a piece of a small tile
+    // re-reads another wave's piece and does not store it; tiles past
+    // the range re-read the last one): a conditional load would make
+    // every later wait drain all loads.
+    auto fetch = [&](int t0, regs_t& r) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < TPS; ++u) {
+            const int t = min(t0 + u, fetch_end - 1);
+            const int phys = tbl_at(t - kt0);
+            const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int base = ((i * kWaves + wave) * 1024) % STAGE;
+                const bool isv = base >= 16 * RB;
+                const char* src = (isv ? a.v_pool : a.k_pool) + boff + src_off[i];
+                if (shared_inflight) {
+                    // this lane's key is a new row of the sequence
+                    // (clamped to its last row past the context; those
+                    // keys are masked and their V cleared)
+                    const int key = t * 16 + (int)key_of[i];
+                    const char* isrc = ibase + (isv ? iv_off : 0) +
+                                       (int64_t)min(key, kv_len - 1) * irow_bytes + piece_of[i];
+                    src = key >= pool_len ? isrc : src;
+                }
+                const uint4 v = *(const uint4*)src;
+                const int w = 4 * (u * NI + i);
+                r[w] = v.x;
+                r[w + 1] = v.y;
+                r[w + 2] = v.z;
+                r[w + 3] = v.w;
+            }
+        }
+    };
+    regs_t rs;
+    if constexpr (FAST && DT != MF_F32 && NT > 1) {
+        if (wg_shared) {
+            if constexpr (MF_WIDE_PRIO > 0) __builtin_amdgcn_s_setprio(MF_WIDE_PRIO);
+            if (kt1 > kt0) fetch(kt0, rs);
+        }
+    }
+
     int maxpos = -1;
     int minpos = INT_MAX;  // over the item's real columns
 #pragma unroll
@@ -683,25 +789,6 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // with in-flight keys (a verify pass) that is only the tiles lying wholly
     // in the pool; the one or two tiles holding the boundary and the in-flight
     // candidates follow through the general per-key loads.
-    //
-    // Wide items whose workgroup shares one key range (the planner packs wide
-    // items that way, one column group per wave) stage each tile in LDS for
-    // all four waves (the workgroup-shared loop below). On a written-in-flight
-    // step that loop also takes the tiles holding new rows, reading each
-    // lane's key from the pool or from the new rows.
-    bool wg_shared = false;
-    if constexpr (FAST && DT != MF_F32 && NT > 1) {
-        if ((block + 1) * kWaves <= num_items) {
-            const int32_t* i0 = a.items + (int64_t)block * kWaves * MF_PLAN_ITEM_INTS;
-            wg_shared = true;
-#pragma unroll
-            for (int w = 1; w < kWaves; ++w) {
-                const int32_t* iw = i0 + w * MF_PLAN_ITEM_INTS;
-                wg_shared = wg_shared && iw[0] == i0[0] && iw[1] == i0[1] && iw[4] == i0[4] && iw[5] == i0[5];
-            }
-        }
-    }
-    const bool shared_inflight = TAIL && wg_shared;
     int fast_end = kt_end;
     if constexpr (FAST) {
         if (inflight && !shared_inflight) fast_end = max(kt0, min(kt_end, pool_len >> 4));
@@ -709,11 +796,13 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // Per-tile work is branch-free apart from wave-uniform decisions: every
     // column tile's MFMAs run (tiles past nct hold zero queries and are never
     // stored), and masking is a select, so the scheduler sees one straight
-    // block per tile.
-    auto process = [&](int kt, const uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
+    // block per tile, in four parts: scores, the lazy rescale, exponentials
+    // and the PV product.
+    //
+    // Slots past the context in the last block may hold anything, NaN
+    // included; p = 0 there, but 0 * NaN is NaN, so clear them.
+    auto clear_v_tail = [&](int kt, uint32_t (&vf)[4][VWD]) {
         if constexpr (FAST) {
-            // Slots past the context in the last block may hold anything,
-            // NaN included; p = 0 there, but 0 * NaN is NaN, so clear them.
             if ((kt + 1) * 16 > kv_len) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -723,10 +812,11 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                 }
             }
         }
-        // QK MFMAs of all column tiles first, then the rescale decision, then
-        // exponentials, so one tile's MFMAs overlap another tile's vector work.
-        // Scores stay raw; the scale is applied inside the exponent,
-        // p = 2^(s * scale - m), one fma.
+    };
+    // S^T = K Q^T for every column tile (lane (g, j): keys 4g..4g+3 of
+    // column j), masked. Scores stay raw; the scale is applied inside the
+    // exponent, p = 2^(s * scale - m), one fma.
+    auto scores = [&](int kt, const uint4 (&kf)[NL], float (&sv)[NT][4]) {
         f32x4 st[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
@@ -734,8 +824,6 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
 #pragma unroll
             for (int c = 0; c < NL; ++c) st[nt] = mfma_qk<DT>(kf[c], qf[nt][c], st[nt]);
         }
-        // lane (g, j) holds S^T[keys 4g..4g+3][column j] of every tile
-        float sv[NT][4];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -749,33 +837,37 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                 for (int r = 0; r < 4; ++r)
                     sv[nt][r] = kt * 16 + 4 * g + r <= lim[nt] ? sv[nt][r] : kNegInf;
         }
-        // Lazy rescaling: a column's running max m moves (and l, acc are
-        // rescaled) only when one of its scores exceeds m by more than
-        // kLazyLog2, so p = 2^(s - m) stays below 2^kLazyLog2; l and acc always
-        // share the m they were built with, so the result is the same softmax.
-        // Each lane tests its own four scores; the max across the column's
-        // four lane groups is only formed when some lane asks for a move.
-        float lmax[NT];
+    };
+    // Lazy rescaling: a column's running max m moves (and l, acc are
+    // rescaled) only when one of its scores exceeds m by more than
+    // kLazyLog2, so p = 2^(s - m) stays below 2^kLazyLog2; l and acc always
+    // share the m they were built with, so the result is the same softmax.
+    // Each lane tests its own four scores; the max across the column's
+    // four lane groups is only formed when some lane asks for a move.
+    auto needs_rescale = [&](const float (&sv)[NT][4], float (&lmax)[NT]) -> bool {
         bool grow = false;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             lmax[nt] = fmax_prop(fmax_prop(sv[nt][0], sv[nt][1]), fmax_prop(sv[nt][2], sv[nt][3]));
             grow |= lmax[nt] > thr[nt];
         }
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        return __builtin_amdgcn_ballot_w64(grow) != 0;
+    };
+    auto rescale = [&](const float (&lmax)[NT]) {
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const float mn = fmaxf(m[nt], group_max4(lmax[nt]) * a.scale_log2);
-                const float alpha = __builtin_amdgcn_exp2f(m[nt] - mn);
-                l[nt] *= alpha;
+        for (int nt = 0; nt < NT; ++nt) {
+            const float mn = fmaxf(m[nt], group_max4(lmax[nt]) * a.scale_log2);
+            const float alpha = __builtin_amdgcn_exp2f(m[nt] - mn);
+            l[nt] *= alpha;
 #pragma unroll
-                for (int c = 0; c < VCH; ++c) acc[nt][c] *= alpha;
-                m[nt] = mn;
-                thr[nt] = (mn + kLazyLog2) * a.inv_scale_log2;
-            }
+            for (int c = 0; c < VCH; ++c) acc[nt][c] *= alpha;
+            m[nt] = mn;
+            thr[nt] = (mn + kLazyLog2) * a.inv_scale_log2;
         }
-        uint2 p16[NT];
-        float p32[NT][4];
+    };
+    // p = 2^(s * scale - m) against the current running max, l += row sums;
+    // packed to the 16-bit dtype for the PV MFMA (fp32 kept as is).
+    auto exps = [&](const float (&sv)[NT][4], uint2 (&p16)[NT], float (&p32)[NT][4]) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             float p[4];
@@ -795,8 +887,18 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                                      f32_to_bits<DT>(p[2]) | (f32_to_bits<DT>(p[3]) << 16));
             }
         }
-        // O^T += V^T P^T, one MFMA per 16-row head_dim tile c: row i of tile c
-        // is head_dim element i*VCH + c.
+    };
+    // MFMA A operand (16-bit) of head_dim tile c: element c of keys
+    // 4g..4g+3, the low (c even) or high halves of word c/2, paired by byte
+    // permutes. Row i of tile c is head_dim element i*VCH + c.
+    auto va16 = [&](const uint32_t (&vf)[4][VWD], int c) -> uint2 {
+        const int wd = c >> 1;
+        const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+        return make_uint2(__builtin_amdgcn_perm(vf[1][wd], vf[0][wd], sel),
+                          __builtin_amdgcn_perm(vf[3][wd], vf[2][wd], sel));
+    };
+    // O^T += V^T P^T for one tile, one MFMA per 16-row head_dim tile c.
+    auto pv = [&](const uint32_t (&vf)[4][VWD], const uint2 (&p16)[NT], const float (&p32)[NT][4]) {
 #pragma unroll
         for (int c = 0; c < VCH; ++c) {
             if constexpr (DT == MF_F32) {
@@ -808,16 +910,22 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                         acc[nt][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, p32[nt][r], acc[nt][c], 0, 0, 0);
                 }
             } else {
-                // element c of keys 4g..4g+3: the low (c even) or high
-                // halves of word c/2, paired by byte permutes
-                const int wd = c >> 1;
-                const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-                const uint2 va = make_uint2(__builtin_amdgcn_perm(vf[1][wd], vf[0][wd], sel),
-                                            __builtin_amdgcn_perm(vf[3][wd], vf[2][wd], sel));
+                const uint2 va = va16(vf, c);
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) acc[nt][c] = mfma_pv16<DT>(va, p16[nt], acc[nt][c]);
             }
         }
+    };
+    auto process = [&](int kt, const uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
+        clear_v_tail(kt, vf);
+        float sv[NT][4];
+        scores(kt, kf, sv);
+        float lmax[NT];
+        if (needs_rescale(sv, lmax)) rescale(lmax);
+        uint2 p16[NT];
+        float p32[NT][4];
+        exps(sv, p16, p32);
+        pv(vf, p16, p32);
     };
 
     // ---- key loops. Single-column-tile items (decode, verify) stream their
@@ -842,18 +950,6 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // conflict-free. One barrier per stage.
     if constexpr (FAST && DT != MF_F32 && NT > 1) {
         if (wg_shared) {
-            if constexpr (MF_WIDE_PRIO > 0) __builtin_amdgcn_s_setprio(MF_WIDE_PRIO);
-            constexpr int RB = DP * ES;             // bytes of one key row
-            constexpr int NCH = RB / 16;            // 16-byte chunks per row
-            constexpr int STAGE = 32 * RB;          // K tile, then V tile
-            constexpr int NI = (STAGE + kWaves * 1024 - 1) / (kWaves * 1024);  // 16-byte loads per lane per tile
-            // Tiles per LDS stage: each barrier and each refill covers TPS
-            // tiles, so a refill has TPS tiles of compute to arrive in.
-            // Measured on the C2 prefill items (bf16, D 64): 1 tile 42.0 us,
-            // 2 tiles 40.3 us, 4 tiles 39.2 us. Four would take the D 32
-            // kernel past 128 registers (three waves per SIMD), so other row
-            // sizes use two.
-            constexpr int TPS = RB == 128 ? 4 : 2;
             static_assert(wide_lds_bytes<DT, DP>() == 2 * TPS * STAGE + 16, "LDS arena layout");
             char* smem = attn_lds;
             int* s_end = reinterpret_cast<int*>(attn_lds + 2 * TPS * STAGE);
@@ -862,66 +958,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
             const int wg_end = __builtin_amdgcn_readfirstlane(
                 max(max(s_end[0], s_end[1]), max(s_end[2], s_end[3])));
             const int n = wg_end - kt0;
-            // this lane's 16 bytes of each tile: LDS byte base + lane*16 of
-            // piece (i*4 + wave) mod STAGE, and the matching pool offset inside
-            // the block (vector types rather than arrays keep them in registers)
-            typedef uint32_t offs_t __attribute__((ext_vector_type(NI)));
-            typedef uint32_t regs_t __attribute__((ext_vector_type(4 * NI * TPS)));
-            offs_t src_off, key_of, piece_of;
-#pragma unroll
-            for (int i = 0; i < NI; ++i) {
-                const int base = ((i * kWaves + wave) * 1024) % STAGE;
-                const bool isv = base >= 16 * RB;
-                const int p2 = (isv ? base - 16 * RB : base) + lane * 16;
-                const int key = p2 / RB, slot = (p2 % RB) >> 4;
-                const int q = isv ? slot : (slot ^ (key & (NCH - 1)));
-                src_off[i] = (uint32_t)key * v_row_bytes + (uint32_t)q * 16;
-                key_of[i] = (uint32_t)key;
-                piece_of[i] = (uint32_t)q * 16;
-            }
-            // in-flight key k of this kv head: K row at ibase + k * irow_bytes,
-            // its V row iv_off bytes on (so the loop holds three numbers, not
-            // both tensors and their strides)
-            const char* ibase = a.new_k;
-            int64_t irow_bytes = 0, iv_off = 0;
-            if (shared_inflight) {
-                irow_bytes = a.n_sr * ES;
-                ibase = a.new_k + ((int64_t)(row0 - pool_len) * a.n_sr + (int64_t)h * a.n_sh) * ES;
-                iv_off = a.new_v - a.new_k;
-            }
-            // Loads are unconditional (a wave without a piece of a small tile
-            // re-reads another wave's piece and does not store it; tiles past
-            // the range re-read the last one): a conditional load would make
-            // every later wait drain all loads.
-            auto fetch = [&](int t0, regs_t& r) __attribute__((always_inline)) {
-#pragma unroll
-                for (int u = 0; u < TPS; ++u) {
-                    const int t = min(t0 + u, wg_end - 1);
-                    const int phys = tbl_at(t - kt0);
-                    const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
-#pragma unroll
-                    for (int i = 0; i < NI; ++i) {
-                        const int base = ((i * kWaves + wave) * 1024) % STAGE;
-                        const bool isv = base >= 16 * RB;
-                        const char* src = (isv ? a.v_pool : a.k_pool) + boff + src_off[i];
-                        if (shared_inflight) {
-                            // this lane's key is a new row of the sequence
-                            // (clamped to its last row past the context; those
-                            // keys are masked and their V cleared)
-                            const int key = t * 16 + (int)key_of[i];
-                            const char* isrc = ibase + (isv ? iv_off : 0) +
-                                               (int64_t)min(key, kv_len - 1) * irow_bytes + piece_of[i];
-                            src = key >= pool_len ? isrc : src;
-                        }
-                        const uint4 v = *(const uint4*)src;
-                        const int w = 4 * (u * NI + i);
-                        r[w] = v.x;
-                        r[w + 1] = v.y;
-                        r[w + 2] = v.z;
-                        r[w + 3] = v.w;
-                    }
-                }
-            };
+            fetch_end = wg_end;
             auto stash = [&](const regs_t& r, int buf) __attribute__((always_inline)) {
 #pragma unroll
                 for (int u = 0; u < TPS; ++u) {
@@ -947,9 +984,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
             // is refilled with stage u+2.
             if (n > 0) {
                 const int nst = (n + TPS - 1) / TPS;
-                regs_t rs;
-                fetch(kt0, rs);
-                stash(rs, 0);
+                stash(rs, 0);  // the first stage, fetched with the setup loads
                 fetch(kt0 + TPS, rs);
                 sync();
                 for (int u = 0; u < nst; ++u) {
