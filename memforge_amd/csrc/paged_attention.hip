@@ -58,6 +58,11 @@ constexpr int kMaxItemTiles = MF_MAX_ITEM_TILES;  // key tiles per work item (tw
 // Raised, the wide waves issue first and the decode waves take the slots they
 // leave while they wait on memory. Measured on the C2 engine layer: 53.7 us at
 // equal priority, 49.3-49.8 us at 1, 49.4-49.8 at 2.
+// Stages of the workgroup-shared prefill loop move global -> LDS directly
+// (1) or through registers (0).
+#ifndef MF_WIDE_DIRECT_LDS
+#define MF_WIDE_DIRECT_LDS 1
+#endif
 #ifndef MF_WIDE_PRIO
 #define MF_WIDE_PRIO 1
 #endif
@@ -210,6 +215,16 @@ __device__ __forceinline__ uint4 ld_nt16(const char* p) {
     const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+// 16 bytes per lane from global memory straight into LDS (gfx950's
+// global_load_lds_dwordx4): lane i's bytes land at lds_addr + 16 i, lds_addr
+// being the same for the whole wave. Written as inline assembly because the
+// builtin makes the compiler wait for the transfer before every later LDS
+// read; the caller waits for it (vmcnt) before the barrier that publishes it.
+__device__ __forceinline__ void ld_lds16(const void* gsrc, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(gsrc)
+                 : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void ld_words_nt(const char* p, uint32_t* w) {
     if constexpr (N == 4) {
@@ -737,11 +752,40 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
             }
         }
     };
+    // The same stage straight into LDS buffer `buf` (direct form): each wave
+    // writes its 1 KB pieces of each tile; a wave without a piece of a small
+    // tile loads nothing.
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)attn_lds;
+    auto dfetch = [&](int t0, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < TPS; ++u) {
+            const int t = min(t0 + u, fetch_end - 1);
+            const int phys = tbl_at(t - kt0);
+            const int64_t boff = ((int64_t)phys * a.p_sb + (int64_t)h * a.p_sh) * ES;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int base = (i * kWaves + wave) * 1024;
+                if (base >= STAGE) continue;
+                const bool isv = base >= 16 * RB;
+                const char* src = (isv ? a.v_pool : a.k_pool) + boff + src_off[i];
+                if (shared_inflight) {
+                    const int key = t * 16 + (int)key_of[i];
+                    const char* isrc = ibase + (isv ? iv_off : 0) +
+                                       (int64_t)min(key, kv_len - 1) * irow_bytes + piece_of[i];
+                    src = key >= pool_len ? isrc : src;
+                }
+                ld_lds16(src, lds_base + (uint32_t)((buf * TPS + u) * STAGE + base));
+            }
+        }
+    };
     regs_t rs;
     if constexpr (FAST && DT != MF_F32 && NT > 1) {
         if (wg_shared) {
             if constexpr (MF_WIDE_PRIO > 0) __builtin_amdgcn_s_setprio(MF_WIDE_PRIO);
-            if (kt1 > kt0) fetch(kt0, rs);
+            if (kt1 > kt0) {
+                if constexpr (MF_WIDE_DIRECT_LDS) dfetch(kt0, 0);
+                else fetch(kt0, rs);
+            }
         }
     }
 
@@ -982,7 +1026,45 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
             // One register set in flight: stage u+1 (TPS tiles) arrives during
             // stage u's compute, is stored to the other LDS buffer, and the set
             // is refilled with stage u+2.
-            if (n > 0) {
+            // Direct form: two LDS buffers. Stage u+1 arrives while stage u is
+            // computed; after the barrier that ends stage u (every wave is
+            // done reading its buffer, and has waited for its own pieces of
+            // stage u+1), stage u+2 is issued into the buffer stage u held.
+            auto wait_stage = [&](int pending) {
+                // this wave's direct loads, all but the `pending` last ones
+                if (pending == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(TPS * NI) : "memory");
+            };
+            if (n > 0 && MF_WIDE_DIRECT_LDS) {
+                const int nst = (n + TPS - 1) / TPS;
+                dfetch(kt0 + TPS, 1);  // the first stage went out with the setup loads
+                wait_stage(1);
+                sync();
+                for (int u = 0; u < nst; ++u) {
+                    // fragments of staged tile v (K rows swizzled, V rows plain)
+                    auto frags = [&](int v, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
+                        const char* stg = smem + ((u & 1) * TPS + v) * STAGE;
+#pragma unroll
+                        for (int c = 0; c < NL; ++c)
+                            kf[c] = *(const uint4*)(stg + j * RB + (((c * 4 + g) ^ (j & (NCH - 1))) << 4));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) ld_words<VB>(stg + 16 * RB + (4 * g + r) * RB + j * VB, vf[r]);
+                    };
+#pragma unroll
+                    for (int v = 0; v < TPS; ++v) {
+                        const int t = kt0 + u * TPS + v;
+                        if (t < fast_end) {
+                            uint4 kf[NL];
+                            uint32_t vf[4][VWD];
+                            frags(v, kf, vf);
+                            process(t, kf, vf);
+                        }
+                    }
+                    wait_stage(0);
+                    sync();
+                    if (u + 2 < nst) dfetch(kt0 + (u + 2) * TPS, u & 1);
+                }
+            } else if (n > 0) {
                 const int nst = (n + TPS - 1) / TPS;
                 stash(rs, 0);  // the first stage, fetched with the setup loads
                 fetch(kt0 + TPS, rs);
