@@ -417,8 +417,18 @@ def run_c2(dev, layers=SM_LAYERS, reps=3, fused_leg=True, cpu_leg=True):
     partials = torch.empty(max(plan.partials_floats, 1), dtype=torch.float32, device=dev)
     narrow = nat.AttentionPlan(plan.items, plan.merges, plan.n_narrow, 0, 0, plan.partials_floats,
                                plan.items_host, plan.merges_host)
-    wide = nat.AttentionPlan(plan.items[plan.n_narrow:], plan.merges, 0, plan.n_wide, 0, plan.partials_floats,
-                             plan.items_host, plan.merges_host)
+    # The prefill items alone, as a prefill-only step plans them (decodes with
+    # no rows): the same items, partial slots and merge records as the mixed
+    # plan's wide part, in the order the planner gives a launch of wide items
+    # only (each key range's workgroups on one XCD). The merge leg then reads
+    # the same partials either way.
+    plan_pre = nat.plan_attention(cu[:5] + [cu[4]] * 28, kv, SM_HQ, SM_HKV, SM_D, torch.bfloat16, dev)
+    mixed_wide = plan.items_host[plan.n_narrow:plan.n_narrow + plan.n_wide]
+    assert plan_pre.n_narrow == 0 and plan_pre.n_wide == plan.n_wide, "prefill-only plan differs"
+    assert sorted(map(tuple, mixed_wide.tolist())) == sorted(map(tuple, plan_pre.items_host.tolist())), \
+        "prefill-only plan holds other items"
+    wide = nat.AttentionPlan(plan_pre.items, plan_pre.merges, 0, plan_pre.n_wide, 0, plan_pre.partials_floats,
+                             plan_pre.items_host, plan_pre.merges_host)
     merges = nat.AttentionPlan(plan.items, plan.merges, 0, 0, plan.n_merges, plan.partials_floats,
                                plan.items_host, plan.merges_host)
     scale = 1.0 / math.sqrt(SM_D)

@@ -50,6 +50,11 @@ constexpr int kMaxItemTiles = MF_MAX_ITEM_TILES;  // key tiles per work item (tw
 #ifndef MF_NARROW_ITEMS
 #define MF_NARROW_ITEMS 4096  // planner: target item count that sets the narrow key partition
 #endif
+// Stages of the workgroup-shared prefill loop move global -> LDS directly
+// (1) or through registers (0).
+#ifndef MF_WIDE_DIRECT_LDS
+#define MF_WIDE_DIRECT_LDS 1
+#endif
 // Wave priority (s_setprio) of the workgroup-shared wide loop. In a mixed
 // launch a CU holds single-tile (decode) waves beside the wide (prefill) ones;
 // at equal priority the decode waves' issue slowed the wide workgroups sharing
@@ -58,13 +63,24 @@ constexpr int kMaxItemTiles = MF_MAX_ITEM_TILES;  // key tiles per work item (tw
 // Raised, the wide waves issue first and the decode waves take the slots they
 // leave while they wait on memory. Measured on the C2 engine layer: 53.7 us at
 // equal priority, 49.3-49.8 us at 1, 49.4-49.8 at 2.
-// Stages of the workgroup-shared prefill loop move global -> LDS directly
-// (1) or through registers (0).
-#ifndef MF_WIDE_DIRECT_LDS
-#define MF_WIDE_DIRECT_LDS 1
-#endif
 #ifndef MF_WIDE_PRIO
 #define MF_WIDE_PRIO 1
+#endif
+// XCD-local order of the wide workgroups in plans without single-tile items
+// (1). The dispatcher sends workgroup b of a launch to XCD b mod 8, so the
+// consecutive wide workgroups of one key range (the column groups of one
+// sequence, kv head and key partition, which read the same K/V tiles) land on
+// eight XCDs whose L2s each fetch the tiles. The planner instead deals whole
+// ranges to eight queues (least causal work first) and interleaves them, so
+// workgroup 8k + x comes from queue x and a range stays on one XCD; each
+// queue runs its workgroups most causal work first. Measured on the C2
+// prefill items alone: 38.2-38.8 us -> 35.1-35.5 us between events, PMC
+// FETCH 74 MB -> 24 MB (1.4x the K/V and query bytes). Beside single-tile
+// items (one mixed launch) the same order was slower (C2 engine layer 49.2
+// -> 50.2 us; the causal-work order alone 51.2 us), so mixed plans keep the
+// range-length order.
+#ifndef MF_WIDE_XCD
+#define MF_WIDE_XCD 1
 #endif
 #ifndef MF_WIDE_ITEMS
 #define MF_WIDE_ITEMS 4096  // planner: most wide items before partitions grow
@@ -2180,7 +2196,81 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     for (size_t i = 0; i < shared_items.size(); i += U) wunits.push_back(&shared_items[i]);
     for (size_t i = 0; i < loose_items.size(); i += U) wunits.push_back(&loose_items[i]);
     emit(nunits, 0);
-    emit(wunits, n_narrow);
+    // A wide item's work: its tiles up to the last one its last column sees
+    // (causal), a workgroup's the most of its four.
+    auto item_work = [&](const Item& o) -> int64_t {
+        const int ncols = o[9] * G;
+        const int last_col = std::min((o[2] + o[3]) * 16, ncols) - 1;
+        if (o[3] <= 0 || last_col < 0) return 0;
+        const int last_pos = o[10] - o[9] + last_col / G;
+        return std::max(0, std::min(o[5], last_pos / 16 + 1) - o[4]);
+    };
+    auto unit_work = [&](const Item* u) {
+        int64_t l = 0;
+        for (int w = 0; w < U; ++w) l = std::max(l, item_work(u[w]));
+        return l;
+    };
+    if (MF_WIDE_XCD && n_narrow == 0) {
+        // Runs of workgroups on one key range, most work first, are dealt
+        // to the queue with the least work so far; each queue then runs its
+        // workgroups most work first, and the queues are interleaved.
+        constexpr int X = 8;
+        auto same_range = [](const Item* x, const Item* y) {
+            return x[0][0] == y[0][0] && x[0][1] == y[0][1] && x[0][4] == y[0][4] && x[0][5] == y[0][5];
+        };
+        std::vector<std::vector<const Item*>> runs;
+        std::vector<int64_t> run_work;
+        for (size_t i = 0; i < wunits.size(); ++i) {
+            if (i >= shared_items.size() / U || runs.empty() || !same_range(runs.back().back(), wunits[i])) {
+                runs.emplace_back();
+                run_work.push_back(0);
+            }
+            runs.back().push_back(wunits[i]);
+            run_work.back() += unit_work(wunits[i]);
+        }
+        std::vector<size_t> order(runs.size());
+        for (size_t i = 0; i < order.size(); ++i) order[i] = i;
+        std::stable_sort(order.begin(), order.end(), [&](size_t x, size_t y) { return run_work[x] > run_work[y]; });
+        // queue x holds exactly the workgroups at wide positions x mod 8; a
+        // run that no queue has room for is split over the roomiest ones
+        std::vector<const Item*> queue[X];
+        int64_t load[X] = {};
+        const int64_t nunits = (int64_t)wunits.size();
+        auto room = [&](int x) { return nunits / X + (x < nunits % X ? 1 : 0) - (int64_t)queue[x].size(); };
+        for (size_t ri : order) {
+            size_t i = 0;
+            const size_t n = runs[ri].size();
+            while (i < n) {
+                int best = -1;
+                for (int x = 0; x < X; ++x)
+                    if (room(x) >= (int64_t)(n - i) && (best < 0 || load[x] < load[best])) best = x;
+                if (best < 0) {
+                    for (int x = 0; x < X; ++x)
+                        if (best < 0 || room(x) > room(best)) best = x;
+                }
+                const size_t take = std::min<size_t>(n - i, (size_t)room(best));
+                for (size_t t = 0; t < take; ++t, ++i) {
+                    queue[best].push_back(runs[ri][i]);
+                    load[best] += unit_work(runs[ri][i]);
+                }
+            }
+        }
+        for (auto& q : queue)
+            std::stable_sort(q.begin(), q.end(), [&](const Item* x, const Item* y) { return unit_work(x) > unit_work(y); });
+        int64_t wi = n_narrow;
+        for (size_t k = 0;; ++k) {
+            bool any = false;
+            for (int x = 0; x < X; ++x) {
+                if (k >= queue[x].size()) continue;
+                any = true;
+                for (int w = 0; w < U; ++w, ++wi)
+                    std::copy(queue[x][k][w].begin(), queue[x][k][w].end(), items + wi * MF_PLAN_ITEM_INTS);
+            }
+            if (!any) break;
+        }
+    } else {
+        emit(wunits, n_narrow);
+    }
     return MF_OK;
 }
 

@@ -53,8 +53,11 @@ def test_plan_covers_every_tile_exactly_once_and_merges_line_up(dtype, d, pt):
     kv = [int(x) for x in rng.integers(1, 3000, len(q_lens))]
     kv[4] = 0
     kv[2] = 7
+    _check_plan_cover(q_lens, kv, 8, 2, d, dtype, pt)
+
+
+def _check_plan_cover(q_lens, kv, hq, hkv, d, dtype, pt):
     cu = np.concatenate([[0], np.cumsum(q_lens)]).tolist()
-    hq, hkv = 8, 2
     G = hq // hkv
     p = _plan(cu, kv, hq, hkv, d, dtype, pt)
     items = p.items_host
@@ -127,6 +130,49 @@ def test_plan_covers_every_tile_exactly_once_and_merges_line_up(dtype, d, pt):
         seen.add((s, h, c))
     assert len(seen) == merges.shape[0]
     assert p.partials_floats >= len(slots) * 16 * (max(d, 32) + 2)
+    return p
+
+
+def _wide_work(it, G):
+    """Key tiles a wide item runs: up to the last one its last column sees."""
+    s, h, c0, nct, kt0, kt1 = (int(x) for x in it[:6])
+    nrows, kvl = int(it[9]), int(it[10])
+    last_col = min((c0 + nct) * 16, nrows * G) - 1
+    if nct <= 0 or last_col < 0:
+        return 0
+    last_pos = kvl - nrows + last_col // G
+    return max(0, min(kt1, last_pos // 16 + 1) - kt0)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(15, 5, 64), (8, 2, 128), (16, 4, 32)])
+def test_prefill_only_plan_keeps_each_key_range_on_one_xcd(hq, hkv, d):
+    """Without single-tile items the wide workgroups of one key range sit at
+    wide positions of one residue mod 8 (the XCD the dispatcher sends them
+    to), the eight residue classes carry near-equal causal work, and each
+    class runs its workgroups most work first."""
+    rng = np.random.default_rng(d)
+    q_lens = [512, 512, 384, 512, 200]
+    kv = [q + int(x) for q, x in zip(q_lens, rng.integers(0, 2049, len(q_lens)))]
+    p = _check_plan_cover(q_lens, kv, hq, hkv, d, torch.bfloat16, 0)
+    assert p.n_narrow == 0 and p.n_wide >= 64
+    G = hq // hkv
+    wide = p.items_host
+    units = [wide[u:u + 4] for u in range(0, p.n_wide, 4)]
+    work = [max(_wide_work(it, G) for it in u) for u in units]
+    ranges = {}
+    for w, u in enumerate(units):
+        keys = {(int(it[0]), int(it[1]), int(it[4]), int(it[5])) for it in u}
+        if len(keys) == 1:
+            ranges.setdefault(keys.pop(), set()).add(w % 8)
+    # a run split between two queues (at most one per queue but the last)
+    spilled = sum(len(r) > 1 for r in ranges.values())
+    assert spilled <= 7, f"{spilled} of {len(ranges)} key ranges span XCDs"
+    load = [sum(work[w] for w in range(c, len(units), 8)) for c in range(8)]
+    assert max(load) <= 1.1 * min(load), load
+    full = (len(units) // 8) * 8  # whole rounds of the interleave
+    for c in range(8):
+        seq = [work[w] for w in range(c, full, 8)]
+        assert seq == sorted(seq, reverse=True)
 
 
 def test_plan_capacity_and_argument_errors():
