@@ -433,11 +433,26 @@ constexpr int attn_waves_per_eu() {
 // workgroup (attn_mixed_kernel) sizes the arena for the larger, not for both.
 extern __shared__ __attribute__((aligned(16))) char attn_lds[];
 
+// Workgroup-shared prefill loop: tiles per LDS stage, and stage buffers (the
+// stage being computed plus the ones in flight) for 128-byte rows. Measured
+// on the C2 engine layer (and the prefill items alone, between events):
+// 2 x 4 tiles 48.8-49.0 us (35.4-35.8), 4 x 2 50.3 (36.3-36.5), 3 x 3
+// 49.1-49.4 (36.2-36.4), 3 x 2 49.6-50.1 (36.2-36.5), 3 x 4 55.4-55.6 (48 KB
+// of LDS: three workgroups per CU). More tiles in flight do not help: the
+// loop does not wait on memory.
+#ifndef MF_WIDE_TPS128
+#define MF_WIDE_TPS128 4
+#endif
+#ifndef MF_WIDE_NBUF128
+#define MF_WIDE_NBUF128 2
+#endif
+constexpr int wide_tps(int rb) { return rb == 128 ? MF_WIDE_TPS128 : 2; }
+constexpr int wide_nbuf(int rb) { return rb == 128 ? MF_WIDE_NBUF128 : 2; }
 template <int DT, int DP>
 constexpr int wide_lds_bytes() {
     constexpr int rb = DP * (DT == MF_F32 ? 4 : 2);
     if constexpr (DT == MF_F32) return 0;  // the workgroup-shared loop is 16-bit only
-    else return 2 * (rb == 128 ? 4 : 2) * 32 * rb + 16;
+    else return wide_nbuf(rb) * wide_tps(rb) * 32 * rb + 16;
 }
 template <int DP>
 constexpr int coop_lds_bytes() {
@@ -691,7 +706,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // 2 tiles 40.3 us, 4 tiles 39.2 us. Four would take the D 32
     // kernel past 128 registers (three waves per SIMD), so other row
     // sizes use two.
-    constexpr int TPS = RB == 128 ? 4 : 2;
+    constexpr int TPS = wide_tps(RB);
+    constexpr int NBUF = wide_nbuf(RB);
+    static_assert(NBUF >= 2 && NBUF <= 5 && (MF_WIDE_DIRECT_LDS || NBUF == 2), "stage buffers");
     // this lane's 16 bytes of each tile: LDS byte base + lane*16 of
     // piece (i*4 + wave) mod STAGE, and the matching pool offset inside
     // the block (vector types rather than arrays keep them in registers)
@@ -1010,9 +1027,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // conflict-free. One barrier per stage.
     if constexpr (FAST && DT != MF_F32 && NT > 1) {
         if (wg_shared) {
-            static_assert(wide_lds_bytes<DT, DP>() == 2 * TPS * STAGE + 16, "LDS arena layout");
+            static_assert(wide_lds_bytes<DT, DP>() == NBUF * TPS * STAGE + 16, "LDS arena layout");
             char* smem = attn_lds;
-            int* s_end = reinterpret_cast<int*>(attn_lds + 2 * TPS * STAGE);
+            int* s_end = reinterpret_cast<int*>(attn_lds + NBUF * TPS * STAGE);
             if (lane == 0) s_end[wave] = fast_end;
             __syncthreads();
             const int wg_end = __builtin_amdgcn_readfirstlane(
@@ -1046,20 +1063,29 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
             // computed; after the barrier that ends stage u (every wave is
             // done reading its buffer, and has waited for its own pieces of
             // stage u+1), stage u+2 is issued into the buffer stage u held.
-            auto wait_stage = [&](int pending) {
-                // this wave's direct loads, all but the `pending` last ones
-                if (pending == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(TPS * NI) : "memory");
+            auto wait_stages = [&](int pending) {
+                // this wave's direct loads done, but for the last `pending` stages
+                if (pending <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                else if (pending == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(TPS * NI) : "memory");
+                else if (pending == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * TPS * NI) : "memory");
+                else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * TPS * NI) : "memory");
             };
             if (n > 0 && MF_WIDE_DIRECT_LDS) {
+                // NBUF buffers: stage u is computed while stages u+1 ..
+                // u+NBUF-1 arrive; after the barrier that ends stage u (every
+                // wave is done reading its buffer, and has waited for its own
+                // pieces of stage u+1), stage u+NBUF is issued into it.
                 const int nst = (n + TPS - 1) / TPS;
-                dfetch(kt0 + TPS, 1);  // the first stage went out with the setup loads
-                wait_stage(1);
+                // the first stage went out with the setup loads
+                for (int s = 1; s < NBUF; ++s)
+                    if (s < nst) dfetch(kt0 + s * TPS, s);
+                wait_stages(min(NBUF - 1, nst - 1));
                 sync();
+                int buf = 0;
                 for (int u = 0; u < nst; ++u) {
                     // fragments of staged tile v (K rows swizzled, V rows plain)
                     auto frags = [&](int v, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
-                        const char* stg = smem + ((u & 1) * TPS + v) * STAGE;
+                        const char* stg = smem + (buf * TPS + v) * STAGE;
 #pragma unroll
                         for (int c = 0; c < NL; ++c)
                             kf[c] = *(const uint4*)(stg + j * RB + (((c * 4 + g) ^ (j & (NCH - 1))) << 4));
@@ -1076,9 +1102,10 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                             process(t, kf, vf);
                         }
                     }
-                    wait_stage(0);
+                    wait_stages(min(NBUF - 2, nst - 2 - u));
                     sync();
-                    if (u + 2 < nst) dfetch(kt0 + (u + 2) * TPS, u & 1);
+                    if (u + NBUF < nst) dfetch(kt0 + (u + NBUF) * TPS, buf);
+                    buf = buf + 1 == NBUF ? 0 : buf + 1;
                 }
             } else if (n > 0) {
                 const int nst = (n + TPS - 1) / TPS;
