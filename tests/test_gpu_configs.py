@@ -114,13 +114,16 @@ def test_long_waves_use_both_table_registers_fp32_d128(device):
     assert err <= 1e-5, f"fp32 max-abs {err:.3e}"
 
 
-def test_c2_mixed_step_at_full_size(device):
+@pytest.mark.parametrize("prefill_only", [False, True])
+def test_c2_mixed_step_at_full_size(device, prefill_only):
     """C2: 4 chunks of 512 on priors U[0,2048] + 28 decodes of U[64,4096],
     bf16, 15q/5kv, D 64. The KV scatter of all 2,076 new tokens, then one
     attention call with the whole plan (decode and prefill items in one
     launch, split-K merge) -- the engine's form of the step. The scatter is
     checked bit-exactly; the attention of every decode row and of 48 rows per
-    prefill chunk against the oracle."""
+    prefill chunk against the oracle. prefill_only: the same step planned with
+    the decodes given no rows (a plan of wide items only, in the planner's
+    XCD order), the prefill rows checked."""
     gen = torch.Generator().manual_seed(0)
     bs, hq, hkv, d = 16, 15, 5, 64
     prior = torch.randint(0, 2049, (4,), generator=gen).tolist()
@@ -144,8 +147,13 @@ def test_c2_mixed_step_at_full_size(device):
     slot_t = torch.tensor(slots, dtype=torch.int64, device=device)
     nat.kv_write(knew, vnew, slot_t, pool)
     assert torch.equal(kp.view(-1, hkv, d)[slot_t], knew) and torch.equal(vp.view(-1, hkv, d)[slot_t], vnew)
+    if prefill_only:
+        cu = cu[:5] + [cu[4]] * 28
     plan = nat.plan_attention(cu, kv, hq, hkv, d, torch.bfloat16, device)
-    assert plan.n_narrow and plan.n_wide and plan.n_merges  # one mixed launch, then the merge
+    if prefill_only:
+        assert plan.n_narrow == 0 and plan.n_wide == 3600 and plan.n_merges
+    else:
+        assert plan.n_narrow and plan.n_wide and plan.n_merges  # one mixed launch, then the merge
     bt = torch.zeros((32, max(len(t) for t in tables)), dtype=torch.int32)
     for i, t in enumerate(tables):
         bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
@@ -158,7 +166,8 @@ def test_c2_mixed_step_at_full_size(device):
     for e in range(4):
         pick = {0, 511, 255} | set(rng.choice(512, 45, replace=False).tolist())
         rows += [cu[e] + i for i in sorted(pick)]
-    rows += list(range(cu[4], T))
+    if not prefill_only:
+        rows += list(range(cu[4], T))
     seq_of = [e for e, n in enumerate(q_lens) for _ in range(n)]
     kp_h, vp_h = kp.float().cpu().numpy(), vp.float().cpu().numpy()
     want = oatt.varlen_attention(q[rows].permute(1, 0, 2).float().cpu().numpy(), kp_h, vp_h, tables,
