@@ -144,6 +144,21 @@ def _wide_work(it, G):
     return max(0, min(kt1, last_pos // 16 + 1) - kt0)
 
 
+@pytest.mark.parametrize("q_lens,kv", [
+    ([40], [40]),                      # one short run: fewer workgroups than XCDs
+    ([20, 33, 70], [20, 900, 3000]),   # pooled (loose) wide items beside shared runs
+    ([512, 7, 300], [700, 2000, 300]),
+    ([2048], [4096]),                  # one long sequence, many partitions
+])
+def test_prefill_only_plans_of_any_shape_cover_every_tile_once(q_lens, kv):
+    """The XCD order of plans without single-tile items only permutes
+    workgroups: every tile is still planned once and every partial slot and
+    merge record lines up, down to plans smaller than one round of XCDs."""
+    for hq, hkv, d in ((8, 2, 128), (15, 5, 64)):
+        p = _check_plan_cover(q_lens, kv, hq, hkv, d, torch.bfloat16, 0)
+        assert p.n_narrow == 0
+
+
 @pytest.mark.parametrize("hq,hkv,d", [(15, 5, 64), (8, 2, 128), (16, 4, 32)])
 def test_prefill_only_plan_keeps_each_key_range_on_one_xcd(hq, hkv, d):
     """Without single-tile items the wide workgroups of one key range sit at
