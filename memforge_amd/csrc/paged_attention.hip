@@ -2021,7 +2021,9 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
             // wave's key range is hidden behind the wide waves; longer
             // narrow partitions then only save items and merges. Measured
             // on the C2 step (PW 32): narrow P 16 (the estimate's pick)
-            // 58.1-58.9 us per layer, P 32 56.6-56.8, P 64 60.3-60.5.
+            // 58.1-58.9 us per layer, P 32 56.6-56.8, P 64 60.3-60.5;
+            // again with the KV write in the launch and the raised prefill
+            // priority: P 16 57.0-57.3, P 32 48.9-49.3, P 64 58.1-58.3.
             // The planner does not see the pool's block size: the shared
             // launch needs 16-key blocks, and with other block sizes the two
             // classes run as separate launches, where the raised partition
