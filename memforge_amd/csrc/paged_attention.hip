@@ -1056,13 +1056,6 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
             };
-            // One register set in flight: stage u+1 (TPS tiles) arrives during
-            // stage u's compute, is stored to the other LDS buffer, and the set
-            // is refilled with stage u+2.
-            // Direct form: two LDS buffers. Stage u+1 arrives while stage u is
-            // computed; after the barrier that ends stage u (every wave is
-            // done reading its buffer, and has waited for its own pieces of
-            // stage u+1), stage u+2 is issued into the buffer stage u held.
             auto wait_stages = [&](int pending) {
                 // this wave's direct loads done, but for the last `pending` stages
                 if (pending <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1108,6 +1101,10 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                     buf = buf + 1 == NBUF ? 0 : buf + 1;
                 }
             } else if (n > 0) {
+                // Register form (two LDS buffers): one register set in
+                // flight; stage u+1 (TPS tiles) arrives during stage u's
+                // compute, is stored to the other LDS buffer, and the set is
+                // refilled with stage u+2.
                 const int nst = (n + TPS - 1) / TPS;
                 stash(rs, 0);  // the first stage, fetched with the setup loads
                 fetch(kt0 + TPS, rs);
