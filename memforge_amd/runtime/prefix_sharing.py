@@ -1,6 +1,6 @@
 """Pool-side half of prefix sharing: the copy-on-write block copy and the
 sharing figures (same functions as the reference, memforge_ml/runtime/
-prefix_sharing.py:27-140). Which blocks are shared is decided by the C++
+prefix_sharing.py:28-98). Which blocks are shared is decided by the C++
 ``PrefixCache`` and ``BlockAllocator``; this file only moves K/V and reports.
 """
 
