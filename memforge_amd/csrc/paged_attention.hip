@@ -2241,56 +2241,63 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
         // to the queue with the least work so far; each queue then runs its
         // workgroups most work first, and the queues are interleaved.
         constexpr int X = 8;
-        auto same_range = [](const Item* x, const Item* y) {
-            return x[0][0] == y[0][0] && x[0][1] == y[0][1] && x[0][4] == y[0][4] && x[0][5] == y[0][5];
+        const size_t nu = wunits.size();
+        std::vector<int64_t> work(nu);
+        for (size_t i = 0; i < nu; ++i) work[i] = unit_work(wunits[i]);
+        auto same_range = [&](size_t x, size_t y) {
+            const Item& a = wunits[x][0];
+            const Item& b = wunits[y][0];
+            return a[0] == b[0] && a[1] == b[1] && a[4] == b[4] && a[5] == b[5];
         };
-        std::vector<std::vector<const Item*>> runs;
+        // run r holds units [run_begin[r], run_begin[r + 1])
+        std::vector<size_t> run_begin;
         std::vector<int64_t> run_work;
-        for (size_t i = 0; i < wunits.size(); ++i) {
-            if (i >= shared_items.size() / U || runs.empty() || !same_range(runs.back().back(), wunits[i])) {
-                runs.emplace_back();
+        for (size_t i = 0; i < nu; ++i) {
+            if (i >= shared_items.size() / U || run_begin.empty() || !same_range(i - 1, i)) {
+                run_begin.push_back(i);
                 run_work.push_back(0);
             }
-            runs.back().push_back(wunits[i]);
-            run_work.back() += unit_work(wunits[i]);
+            run_work.back() += work[i];
         }
-        std::vector<size_t> order(runs.size());
-        for (size_t i = 0; i < order.size(); ++i) order[i] = i;
+        const size_t nruns = run_begin.size();
+        run_begin.push_back(nu);
+        std::vector<size_t> order(nruns);
+        for (size_t i = 0; i < nruns; ++i) order[i] = i;
         std::stable_sort(order.begin(), order.end(), [&](size_t x, size_t y) { return run_work[x] > run_work[y]; });
         // queue x holds exactly the workgroups at wide positions x mod 8; a
         // run that no queue has room for is split over the roomiest ones
-        std::vector<const Item*> queue[X];
+        std::vector<size_t> queue[X];
         int64_t load[X] = {};
-        const int64_t nunits = (int64_t)wunits.size();
-        auto room = [&](int x) { return nunits / X + (x < nunits % X ? 1 : 0) - (int64_t)queue[x].size(); };
+        for (auto& q : queue) q.reserve(nu / X + 1);
+        auto room = [&](int x) { return (int64_t)(nu / X + (x < (int)(nu % X) ? 1 : 0)) - (int64_t)queue[x].size(); };
         for (size_t ri : order) {
-            size_t i = 0;
-            const size_t n = runs[ri].size();
-            while (i < n) {
+            size_t i = run_begin[ri];
+            const size_t end = run_begin[ri + 1];
+            while (i < end) {
                 int best = -1;
                 for (int x = 0; x < X; ++x)
-                    if (room(x) >= (int64_t)(n - i) && (best < 0 || load[x] < load[best])) best = x;
+                    if (room(x) >= (int64_t)(end - i) && (best < 0 || load[x] < load[best])) best = x;
                 if (best < 0) {
                     for (int x = 0; x < X; ++x)
                         if (best < 0 || room(x) > room(best)) best = x;
                 }
-                const size_t take = std::min<size_t>(n - i, (size_t)room(best));
+                const size_t take = std::min<size_t>(end - i, (size_t)room(best));
                 for (size_t t = 0; t < take; ++t, ++i) {
-                    queue[best].push_back(runs[ri][i]);
-                    load[best] += unit_work(runs[ri][i]);
+                    queue[best].push_back(i);
+                    load[best] += work[i];
                 }
             }
         }
         for (auto& q : queue)
-            std::stable_sort(q.begin(), q.end(), [&](const Item* x, const Item* y) { return unit_work(x) > unit_work(y); });
+            std::stable_sort(q.begin(), q.end(), [&](size_t x, size_t y) { return work[x] > work[y]; });
         int64_t wi = n_narrow;
         for (size_t k = 0;; ++k) {
             bool any = false;
             for (int x = 0; x < X; ++x) {
                 if (k >= queue[x].size()) continue;
                 any = true;
-                for (int w = 0; w < U; ++w, ++wi)
-                    std::copy(queue[x][k][w].begin(), queue[x][k][w].end(), items + wi * MF_PLAN_ITEM_INTS);
+                const Item* u = wunits[queue[x][k]];
+                for (int w = 0; w < U; ++w, ++wi) std::copy(u[w].begin(), u[w].end(), items + wi * MF_PLAN_ITEM_INTS);
             }
             if (!any) break;
         }
