@@ -287,7 +287,11 @@ int mf_paged_attention_kv_write(const void* q, int64_t q_stride_row, int64_t q_s
  * (32 MiB) per GPU, held from the first call on that GPU until the process
  * ends; partitions are merged by the separate merge kernel. partials_floats
  * is what the plan needs (counts[3] from mf_attention_plan): a plan needing
- * more is MF_ERR_WORKSPACE, returned before anything touches the device. The
+ * more is MF_ERR_WORKSPACE, returned before anything touches the device.
+ * partials_floats must cover every partial slot the plan's items and merge
+ * records name (a planner-made plan's counts[3] does): the kernels do not
+ * bound slots, so a hand-edited plan naming slots past the array would write
+ * past it. The Python binding checks this against the host copy of the plan. The
  * stream must belong to the current device. Every call on one GPU uses the
  * same array, which keeps the last call's contents (no kernel here needs it
  * cleared), so calls that overlap on one GPU race. Everything else is as in

@@ -688,6 +688,27 @@ def paged_attention_kv_write(q_rows: torch.Tensor, out_rows: torch.Tensor, pool:
 NOALLOC_PARTIALS_FLOATS = 8 * 1024 * 1024
 
 
+def plan_partials_reach(plan: AttentionPlan, head_dim: int) -> int:
+    """fp32 partial floats up to the end of the highest partial slot a
+    per-range plan's items or merge records name. The kernels take the slot
+    numbers as given, so this (not a declared size) is what a buffer must
+    hold."""
+    stride = 16 * (max(32, head_dim) + 2)
+    top = 0
+    n_items = plan.n_narrow + plan.n_wide
+    if n_items:
+        it = np.asarray(plan.items_host[:n_items], dtype=np.int64)
+        named = it[:, 6] >= 0
+        if named.any():
+            # an item writes slots pslot .. pslot + column tiles - 1
+            top = max(top, int((it[named, 6] + np.maximum(it[named, 3], 1)).max()))
+    if plan.n_merges:
+        mg = np.asarray(plan.merges_host[:plan.n_merges], dtype=np.int64)
+        # record: partitions mg[3] at slot mg[4] + p * mg[5]
+        top = max(top, int((mg[:, 4] + (np.maximum(mg[:, 3], 1) - 1) * mg[:, 5] + 1).max()))
+    return top * stride
+
+
 def paged_attention_noalloc(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: PoolView,
                             block_tables: torch.Tensor, cu_seqlens: torch.Tensor, kv_lens: torch.Tensor,
                             positions: torch.Tensor, plan: AttentionPlan, scale: float, num_kv_heads: int,
@@ -700,6 +721,14 @@ def paged_attention_noalloc(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: 
     NOALLOC_PARTIALS_FLOATS partial floats are refused."""
     if getattr(plan, "sliced", False):
         raise ValueError("the no-allocation entry point takes per-range plans (mf_attention_plan)")
+    # The slots the plan's items and merge records name must lie inside the
+    # library's array, whatever partials_floats declares: no kernel bounds a
+    # slot against it.
+    reach = max(plan_partials_reach(plan, q_rows.shape[2]), plan.partials_floats)
+    if reach > NOALLOC_PARTIALS_FLOATS:
+        raise MemforgeHipError(
+            f"mf_paged_attention_noalloc: the plan's partial slots need {reach} floats, past the "
+            f"{NOALLOC_PARTIALS_FLOATS} of the library's array (workspace too small)")
     _rows_ok(q_rows, "q_rows")
     _rows_ok(out_rows, "out_rows")
     require_device(q_rows, out_rows, pool.k, block_tables, cu_seqlens, kv_lens, positions)

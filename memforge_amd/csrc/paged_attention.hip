@@ -236,9 +236,11 @@ __device__ __forceinline__ uint4 ld_nt16(const char* p) {
 // being the same for the whole wave. Written as inline assembly because the
 // builtin makes the compiler wait for the transfer before every later LDS
 // read; the caller waits for it (vmcnt) before the barrier that publishes it.
+// m0 is declared clobbered, so nothing the compiler keeps in it survives
+// across the statement unsaved.
 __device__ __forceinline__ void ld_lds16(const void* gsrc, uint32_t lds_addr) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(gsrc)
-                 : "memory");
+                 : "memory", "m0");
 }
 
 template <int N>

@@ -14,10 +14,15 @@
 // draws E, where w is the residual max(p - q, 0) normalised twice (by its sum,
 // then again in sample_from_probs) when the round rejected and the residual
 // has mass, else the target row p normalised, or uniform when p has no mass.
-// Each normalisation divides every candidate by the same positive number, which
-// leaves the argmax where it is, so the pass keeps the three first-index
-// argmaxes -- of max(p - q, 0) / E, of max(p, 0) / E and of 1 / E -- and
-// whether any residual or target value is positive. Launch 3 picks the family
+// In exact arithmetic each normalisation divides every candidate by the same
+// positive number and leaves the argmax where it is, so the pass keeps the
+// three first-index argmaxes -- of max(p - q, 0) / E, of max(p, 0) / E and of
+// 1 / E -- and whether any residual or target value is positive. In fp32 the
+// reference's keys fl(fl(fl(d / S1) / S2) / E) carry two more roundings than
+// fl(d / E) (and S1, S2 come from torch's own reduction order), so two
+// candidates within about an ulp of each other can be ordered differently:
+// the draw equals the reference's up to such near-ties (none in 1.28M seeded
+// CPU draws at vocabularies 256 to 49,152). Launch 3 picks the family
 // the reference's branches would take and combines the chunk winners.
 // At this size the three launches are bound by dependent memory round trips,
 // not bytes: the accept walk takes two (tokens with statistics, then the

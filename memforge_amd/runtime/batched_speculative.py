@@ -438,7 +438,10 @@ def resolve_rounds_global_rng(seq_ids: Sequence[int], candidates: Sequence[Seque
                               temperatures: Sequence[float]) -> List[SpeculativeRound]:
     """Every row of a speculative step resolved by ONE mf_spec_verify launch,
     with the same outcome, row for row, as ``resolve_round`` applied to the
-    rows in order -- including what each consumes of torch's global
+    rows in order, up to fp32 near-ties in the final draw (the kernel ranks
+    the candidates by fl(w / E) where the reference's ``multinomial`` sees w
+    normalised twice first, two more roundings; accept decisions are exact)
+    -- including what each consumes of torch's global
     generators (memforge_ml/runtime/continuous_engine.py:1295-1311,
     memforge_ml/speculative/rejection_sampler.py:28-83):
 

@@ -197,8 +197,11 @@ class _AbortRequests:
 
 class _ThroughputWindow:
     """Tokens emitted over the last ``seconds`` of activity, kept as one
-    (time, count) mark per commit instead of one timestamp per token. The rate
-    is tokens over the span from the oldest to the newest mark in the window."""
+    (first token time, last token time, count) mark per commit instead of one
+    timestamp per token. The rate is tokens over the span from the oldest
+    mark's first token to the newest mark's last, so a window holding one
+    multi-token commit still has a span, as the reference's per-token stamps
+    do (memforge_ml/runtime/continuous_engine.py:1422-1430)."""
 
     __slots__ = ("seconds", "_marks", "_count")
 
@@ -207,18 +210,18 @@ class _ThroughputWindow:
         self._marks: Deque = deque()
         self._count = 0
 
-    def mark(self, when: float, count: int) -> None:
+    def mark(self, first: float, last: float, count: int) -> None:
         if count:
-            self._marks.append((when, count))
+            self._marks.append((first, last, count))
             self._count += count
 
     def rate(self, now: float) -> float:
         horizon = now - self.seconds
-        while self._marks and self._marks[0][0] < horizon:
-            self._count -= self._marks.popleft()[1]
+        while self._marks and self._marks[0][1] < horizon:
+            self._count -= self._marks.popleft()[2]
         if self._count < 2:
             return 0.0
-        span = self._marks[-1][0] - self._marks[0][0]
+        span = self._marks[-1][1] - self._marks[0][0]
         return round(self._count / span, 2) if span > 0 else 0.0
 
 
@@ -784,7 +787,9 @@ class ContinuousBatchingEngine:
                 break
         rt.events.extend(produced)
         self.total_tokens_generated += len(produced)
-        self._throughput.mark(now, len(produced))
+        # the run's first token counts from the step's clock reading, its
+        # last from now
+        self._throughput.mark(now, time.perf_counter(), len(produced))
         if reason:
             self._finish(rt, reason)
         return produced

@@ -26,18 +26,31 @@ def test_abort_requests_are_taken_once_from_any_thread():
 def test_throughput_window_counts_tokens_over_the_span_of_the_window():
     w = _ThroughputWindow(5.0)
     assert w.rate(0.0) == 0.0
-    w.mark(10.0, 1)
+    w.mark(10.0, 10.0, 1)
     assert w.rate(10.0) == 0.0            # fewer than two tokens
-    w.mark(10.0, 3)
+    w.mark(10.0, 10.0, 3)
     assert w.rate(10.0) == 0.0            # no span yet
-    w.mark(12.0, 4)
+    w.mark(12.0, 12.0, 4)
     assert w.rate(12.0) == 4.0            # 8 tokens over 2 s
-    w.mark(13.0, 0)                       # empty commits leave no mark
+    w.mark(13.0, 13.0, 0)                 # empty commits leave no mark
     # at 16.5 the marks at 10.0 have left the window: the 4 tokens at 12.0
     # remain, with no span to divide by
     assert w.rate(16.5) == 0.0 and w._count == 4
-    w.mark(17.0, 6)
+    w.mark(17.0, 17.0, 6)
     assert w.rate(17.0) == 2.0            # 10 tokens over 5 s
+
+
+def test_throughput_window_one_multi_token_commit_has_a_span():
+    """A window holding a single commit of several tokens spans from its first
+    token to its last, as per-token timestamps would (the reference stamps
+    each token, memforge_ml/runtime/continuous_engine.py:1342-1352, 1422-1430)."""
+    w = _ThroughputWindow(5.0)
+    w.mark(20.0, 20.5, 5)
+    assert w.rate(20.5) == 10.0           # 5 tokens over 0.5 s
+    # a mark stays while its last token is inside the window
+    w.mark(24.0, 26.0, 3)
+    assert w.rate(25.2) == round(8 / 6.0, 2)
+    assert w.rate(25.6) == 1.5 and w._count == 3   # the 20.0-20.5 mark left: 3 over 2 s
 
 
 class _SpaceTokenizer:

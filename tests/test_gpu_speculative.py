@@ -225,6 +225,56 @@ def test_global_rng_batched_resolve_equals_row_by_row(device, seed, temps):
     assert torch.equal(torch.cuda.get_rng_state(), gpu_after)
 
 
+# torch.manual_seed(0), then torch.rand(ZERO_OFFSET): the next torch.rand(1)
+# on the CPU generator is exactly 0.0 (pinned in tests/test_oracle.py)
+ZERO_SEED, ZERO_OFFSET = 0, 41102971
+
+
+@pytest.mark.parametrize("temperature", [1.0, 0.0])
+def test_global_rng_resolve_accepts_a_zero_probability_candidate_at_u_zero(device, temperature):
+    """The reference accepts a candidate when r <= min(1, p / (q + 1e-9))
+    (rejection_sampler.py:55-57), so a draw of exactly 0.0 accepts a candidate
+    with p = 0. Row 0's first candidate gets no target mass (a -inf logit, so
+    softmax gives exactly 0, or a one-hot argmax elsewhere at temperature 0)
+    and the global CPU generator is placed so that its next uniform is 0.0:
+    the engine's batched resolve keeps the candidate, as the row-by-row
+    resolve and the reference algorithm on the global generators do, and all
+    three leave the generators in the same state."""
+    from memforge_amd.runtime.batched_speculative import (_probs_from_logits, resolve_round,
+                                                          resolve_rounds_global_rng)
+
+    g = torch.Generator().manual_seed(11)
+    B, K, V = 3, 4, 500
+    target = torch.randn((B, K + 1, V), generator=g) * 2
+    dprobs = torch.softmax(torch.randn((B, K, V), generator=g) * 2, dim=-1)
+    cand = [[int(torch.multinomial(dprobs[b, i], 1, generator=g)) for i in range(K)] for b in range(B)]
+    target[0, 0, cand[0][0]] = float("-inf")
+    target, dprobs = target.to(device), dprobs.to(device)
+    t_rows = [temperature] * B
+
+    def seeded():
+        torch.manual_seed(ZERO_SEED)
+        torch.rand(ZERO_OFFSET)
+        torch.cuda.manual_seed(5)
+
+    seeded()
+    want = [resolve_round(b, cand[b], list(dprobs[b]), list(target[b]), t_rows[b]) for b in range(B)]
+    cpu_after, gpu_after = torch.get_rng_state(), torch.cuda.get_rng_state()
+    seeded()
+    got = resolve_rounds_global_rng(list(range(B)), cand, dprobs, target, t_rows)
+    assert [(r.accepted, r.is_draft, r.num_accepted_draft) for r in got] == \
+           [(r.accepted, r.is_draft, r.num_accepted_draft) for r in want]
+    assert torch.equal(torch.get_rng_state(), cpu_after)
+    assert torch.equal(torch.cuda.get_rng_state(), gpu_after)
+    assert got[0].accepted[0] == cand[0][0] and got[0].is_draft[0]
+    # the reference algorithm itself, row 0, from the same generator state
+    seeded()
+    probs0 = [_probs_from_logits(target[0, i], temperature) for i in range(K + 1)]
+    assert float(probs0[0][cand[0][0]]) == 0.0
+    acc, flags, n = orj.verify_tokens_global_rng(cand[0], list(dprobs[0]), probs0)
+    assert (acc, flags, n) == (got[0].accepted, got[0].is_draft, got[0].num_accepted_draft)
+
+
 def test_confirmed_prefix_scatter_writes_only_confirmed_rows(device):
     """One KV write per layer for every row's confirmed prefix: the pool
     holds exactly the rows scatter_accepted_kv would write one sequence at a

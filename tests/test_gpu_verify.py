@@ -129,3 +129,54 @@ def test_draw_families_residual_target_uniform(device):
         assert tok[b, :cnt[b]].tolist() == want, f"row {b}"
     assert cnt.tolist() == [1, 1, 3]
     assert int(tok[2, 2]) == int(torch.argmin(noise[2]))
+
+
+def test_zero_uniform_accepts_zero_probability_candidates(device):
+    """The accept test is r <= min(1, p / (q + 1e-9)) (rejection_sampler.py:55-57),
+    so r = 0.0 accepts even a candidate the target gives no mass: p = 0 gives
+    a ratio of exactly 0, and 0 <= 0. Row 0 draws u = 0 at every candidate,
+    each with p = 0, and keeps all of them plus the bonus; row 1 draws the
+    smallest positive uniform at its second candidate, which then fails.
+    Checked against the oracle and against the closed form."""
+    B, K, V = 2, 3, 1000
+    gen = torch.Generator().manual_seed(9)
+    draft = torch.softmax(torch.randn((B, K, V), generator=gen) * 2.0, dim=-1)
+    target = torch.softmax(torch.randn((B, K + 1, V), generator=gen) * 2.0, dim=-1)
+    tokens = torch.stack([torch.multinomial(draft[b], 1, generator=gen).view(-1) for b in range(B)]).to(torch.int32)
+    for b in range(B):
+        for i in range(K):
+            target[b, i, int(tokens[b, i])] = 0.0
+    u = torch.zeros((B, K))
+    u[1, 1] = float(np.float32(2.0 ** -24))
+    noise = torch.empty((B, V)).exponential_(1.0, generator=gen)
+    res = nat.spec_verify(tokens.to(device), draft.to(device), target.to(device), 1.0, u.to(device),
+                          noise.to(device), target_is_probs=True)
+    tok, cnt, nacc = res.tokens.cpu().numpy(), res.count.cpu().numpy(), res.num_accepted.cpu().numpy()
+    for b in range(B):
+        want, flags, n = orj.verify_tokens(tokens[b].tolist(), [draft[b, i].numpy() for i in range(K)],
+                                           [target[b, i].numpy() for i in range(K + 1)], u[b].tolist(),
+                                           noise[b].numpy())
+        assert tok[b, :cnt[b]].tolist() == want and int(nacc[b]) == n, f"row {b}"
+    assert nacc.tolist() == [K, 1] and cnt.tolist() == [K + 1, 2]
+    assert tok[0, :K].tolist() == tokens[0].tolist()
+
+
+def test_greedy_zero_uniform_accepts_a_mismatching_candidate(device):
+    """At temperature 0 the target is a one-hot on its argmax, so a candidate
+    that differs from it has p = 0 and q = 1 (a one-hot draft); u = 0 still
+    accepts it (0 <= 0), where any positive uniform replaces it by the
+    argmax (test_greedy_known_answers)."""
+    B, K, V = 2, 4, 64
+    gen = torch.Generator().manual_seed(12)
+    target = torch.randn((B, K + 1, V), generator=gen)
+    greedy = target.argmax(-1)
+    tokens = ((greedy[:, :K] + 3) % V).to(torch.int32)  # every candidate differs from the argmax
+    draft = torch.full((B, K, V), -1e4)
+    for b in range(B):
+        for i in range(K):
+            draft[b, i, int(tokens[b, i])] = 0.0
+    u = torch.zeros((B, K))
+    u[1, 2] = 0.25
+    noise = torch.empty((B, V)).exponential_(1.0, generator=gen)
+    count, nacc = _run_both(device, draft, target, tokens, u, noise, 0.0)
+    assert nacc.tolist() == [4, 2] and count.tolist() == [5, 3]

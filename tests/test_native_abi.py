@@ -451,3 +451,43 @@ def test_noalloc_attention_refuses_oversized_plans_before_touching_the_device():
     assert call(-1) == -1
     m = re.search(r"#define MF_NOALLOC_PARTIALS_FLOATS \((\d+) \* 1024 \* 1024\)", HEADER.read_text())
     assert m and nat.NOALLOC_PARTIALS_FLOATS == int(m.group(1)) << 20
+
+
+@pytest.mark.parametrize("dtype,hq,hkv,d", [(torch.bfloat16, 40, 8, 128), (torch.float32, 15, 5, 64),
+                                            (torch.bfloat16, 15, 5, 64), (torch.float16, 8, 8, 16)])
+def test_plan_partials_reach_is_what_the_planner_counts(dtype, hq, hkv, d):
+    """The highest partial slot a planner-made plan names ends exactly at the
+    partials the planner reports: every slot it counts is used, no more."""
+    rng = np.random.default_rng(d + hq)
+    q_lens = [1, 512, 1, 5, 1, 300, 1]
+    kv = [int(x) for x in rng.integers(600, 9000, len(q_lens))]
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).tolist()
+    for pt in (0, 4, 16):
+        plan = nat.plan_attention(cu, kv, hq, hkv, d, dtype, "cpu", partition_tiles=pt)
+        assert plan.n_merges > 0
+        assert nat.plan_partials_reach(plan, d) == plan.partials_floats
+
+
+def test_noalloc_refuses_a_plan_whose_slots_reach_past_its_array():
+    """A plan whose items or merge records name partial slots past the
+    library's array is refused before any device call, even when its declared
+    partials_floats is small (the slots, not the declaration, are what the
+    kernels write)."""
+    cu, kv = [0, 1, 2], [30000, 20000]
+    plan = nat.plan_attention(cu, kv, 40, 8, 128, torch.bfloat16, "cpu", partition_tiles=4)
+    assert plan.n_merges > 0 and 0 < plan.partials_floats <= nat.NOALLOC_PARTIALS_FLOATS
+    stride = 16 * (128 + 2)
+    far = nat.NOALLOC_PARTIALS_FLOATS // stride + 1
+    for field in ("item", "merge"):
+        items, merges = plan.items_host.copy(), plan.merges_host.copy()
+        if field == "item":
+            k = int(np.nonzero(items[:plan.n_narrow + plan.n_wide, 6] >= 0)[0][0])
+            items[k, 6] = far
+        else:
+            merges[0, 4] = far
+        bad = nat.AttentionPlan(plan.items, plan.merges, plan.n_narrow, plan.n_wide, plan.n_merges,
+                                plan.partials_floats, items, merges)
+        assert nat.plan_partials_reach(bad, 128) > nat.NOALLOC_PARTIALS_FLOATS
+        q = torch.zeros((2, 40, 128), dtype=torch.bfloat16)
+        with pytest.raises(nat.MemforgeHipError, match="workspace"):
+            nat.paged_attention_noalloc(q, q.clone(), None, None, None, None, None, bad, 0.1, 8)

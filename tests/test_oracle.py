@@ -348,3 +348,29 @@ def test_speculative_sampling_preserves_the_target_distribution():
     expected = p * n
     chi2 = float(((counts - expected) ** 2 / expected).sum())
     assert chi2 < 20.5, (counts, expected)  # 4 dof, p ~ 4e-4
+
+
+def test_accept_rule_zero_uniform_accepts_zero_target_mass():
+    """Closed form of the accept test r <= min(1, p / (q + 1e-9))
+    (rejection_sampler.py:55-57): a uniform of exactly 0.0 accepts a
+    candidate whose target probability is 0 (ratio 0, and 0 <= 0), and any
+    positive uniform rejects it. The explicit-noise oracle and the global-RNG
+    restatement both follow it; the generator position that yields an exact
+    0.0 draw is the one the GPU tests use."""
+    V = 8
+    q = np.full(V, 1.0 / V, dtype=np.float32)
+    p = np.zeros(V, dtype=np.float32)
+    p[3] = 1.0
+    noise = np.ones(V, dtype=np.float32)
+    acc, flags, n = orj.verify_tokens([5, 6], [q, q], [p, p, p], [0.0, 0.0], noise)
+    assert acc == [5, 6, 3] and flags == [True, True, False] and n == 2
+    acc, flags, n = orj.verify_tokens([5, 6], [q, q], [p, p, p], [0.0, 2.0 ** -24], noise)
+    assert acc == [5, 3] and flags == [True, False] and n == 1
+    # torch.rand's CPU stream at seed 0 holds an exact 0.0 at this position
+    torch.manual_seed(0)
+    torch.rand(41102971)
+    assert torch.rand(1).item() == 0.0
+    torch.manual_seed(0)
+    torch.rand(41102971)
+    acc, flags, n = orj.verify_tokens_global_rng([5], [torch.from_numpy(q)], [torch.from_numpy(p)] * 2)
+    assert acc[0] == 5 and flags[0] is True
