@@ -236,11 +236,12 @@ __device__ __forceinline__ uint4 ld_nt16(const char* p) {
 // being the same for the whole wave. Written as inline assembly because the
 // builtin makes the compiler wait for the transfer before every later LDS
 // read; the caller waits for it (vmcnt) before the barrier that publishes it.
-// m0 is declared clobbered, so nothing the compiler keeps in it survives
-// across the statement unsaved.
+// The LDS address is bound to m0 by the operand constraint, so the compiler
+// writes m0 itself and knows what it holds (a clobber of the reserved m0
+// would not be honoured); the s_nop gives the write its one wait state before
+// the load reads it.
 __device__ __forceinline__ void ld_lds16(const void* gsrc, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(gsrc)
-                 : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"{m0}"(lds_addr), "v"(gsrc) : "memory");
 }
 
 template <int N>
