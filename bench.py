@@ -477,6 +477,17 @@ def run_c2(dev, layers=SM_LAYERS, reps=3, fused_leg=True, cpu_leg=True):
     graph_fused_us = _graph_us(layer_fused, layers) if fused_leg else float("nan")
     kvb = SM_HKV * SM_D * 2 * 2  # K+V bytes per token per layer
     write_bytes = T * kvb * 2 + T * 8  # read new rows, write pool rows, read slots
+    # The engine's layer (one launch for the KV write and every item, then the
+    # merge): every attended K/V row read once (a chunk's own new rows among
+    # them), the new rows written to the pool once, their slots, Q read and
+    # the output written once, one block-table entry per key tile; FLOPs
+    # 4 Hq D per (row, visible key), decode rows included.
+    eng_bytes = (sum(kv) * kvb + T * kvb + T * 8 + T * SM_HQ * SM_D * 2 * 2
+                 + sum((c + BS - 1) // BS for c in kv) * 4)
+    eng_flops = (sum(4 * SM_HQ * SM_D * (p + i + 1) for p in prior for i in range(512))
+                 + sum(4 * SM_HQ * SM_D * c for c in dctx))
+    t_hbm = eng_bytes / (HBM_PEAK_GBPS * 1e3)
+    t_mfma = eng_flops / (BF16_PEAK_TFLOPS * 1e6)
     dec_bytes = sum(dctx) * kvb + 28 * SM_HQ * SM_D * 2 * 2
     pre_bytes = sum(p + 512 for p in prior) * kvb + 4 * 512 * SM_HQ * SM_D * 2 * 2
     pre_flops = sum(4 * SM_HQ * SM_D * (p + i + 1) for p in prior for i in range(512))
@@ -493,7 +504,28 @@ def run_c2(dev, layers=SM_LAYERS, reps=3, fused_leg=True, cpu_leg=True):
         "prefill_mfma_frac": round(pre_flops / pre_us / 1e6 / BF16_PEAK_TFLOPS, 4),
         "prefill_attn_gbps": round(pre_bytes / pre_us / 1e3, 1),
         "merge_us": round(mrg_us, 2),
+        "timing_note": "kv_write/decode/prefill/merge figures are the layer's parts timed apart between "
+                       "events; prefill_* is the prefill items alone as a prefill-only step plans them "
+                       "(a side figure: the engine runs them inside the mixed launch, see engine_layer)",
         "plan": {"narrow": plan.n_narrow, "wide": plan.n_wide, "merges": plan.n_merges},
+        "engine_layer": {
+            "us": round(graph_fused_us, 2),
+            "form": "graph_step_fused_layer_us: one launch for the KV write, decode and prefill items, "
+                    "then the merge",
+            "bytes": eng_bytes,
+            "flops": eng_flops,
+            "gbps": round(eng_bytes / graph_fused_us / 1e3, 1),
+            "tflops": round(eng_flops / graph_fused_us / 1e6, 1),
+            "hbm_us_at_peak": round(t_hbm, 2),
+            "mfma_us_at_peak": round(t_mfma, 2),
+            "bound": "hbm" if t_hbm >= t_mfma else "mfma",
+            "bound_us": round(max(t_hbm, t_mfma), 2),
+            "frac": round(max(t_hbm, t_mfma) / graph_fused_us, 4),
+            "serial_bound_us": round(t_hbm + t_mfma, 2),
+            "serial_frac": round((t_hbm + t_mfma) / graph_fused_us, 4),
+            "note": "bound: the larger of the bytes at 8 TB/s and the FLOPs at the 2.5 PFLOP/s bf16 dense "
+                    "peak (both overlapped); serial: their sum",
+        } if fused_leg else None,
         "step_attn_us": round(dec_us + pre_us + mrg_us, 2),
         "graph_layer_us": round(graph_layer_us, 2),
         "graph_note": "one layer's KV write + decode items + prefill items + merge, replayed as a captured "
@@ -531,40 +563,33 @@ def _c2_c3_cpu_leg(kp, vp, knew, vnew, slots, q, tables, cu, positions, what: st
     return _cpu_leg(round(secs * 1e6, 1), "us per layer", f"{what}; fp32, {reps} timed layers")
 
 
-def run_kv_write_large(dev, tokens=33792, reps=20):
+def run_kv_write_large(dev, tokens=33792, sets=6, reps=10):
     """KV write of a C4-sized prefill step (33,792 tokens of the SmolLM2
-    shape, bf16) into a shuffled pool: the streaming case of the same kernel."""
+    shape, bf16) into a shuffled pool: the streaming case of the same kernel.
+    Timed as graph replays of back-to-back launches (a single ~15 us launch
+    between two events carries several us of submission gap), cycling through
+    ``sets`` independent sources and pools (6 x 130 MB, more than the 256 MB
+    Infinity Cache holds) so no launch reads what the previous one left in a
+    cache."""
     from memforge_amd import _native as nat
 
     gen = torch.Generator().manual_seed(1)
     nblocks = (tokens + BS - 1) // BS + 64
-    perm = torch.randperm(nblocks * BS, generator=gen)[:tokens].to(dev)
-    kp = torch.zeros((nblocks, BS, SM_HKV, SM_D), device=dev, dtype=torch.bfloat16)
-    vp = torch.zeros_like(kp)
-    k = torch.randn((tokens, SM_HKV, SM_D), device=dev, dtype=torch.bfloat16)
-    v = torch.randn_like(k)
-    view = nat.PoolView.from_bshd(kp, vp)
-    nat.kv_write(k, v, perm, view)
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for a, b in evs:
-        a.record()
-        nat.kv_write(k, v, perm, view)
-        b.record()
-    torch.cuda.synchronize()
-    us = _event_us(evs)
+    bufs = []
+    for _ in range(sets):
+        perm = torch.randperm(nblocks * BS, generator=gen)[:tokens].to(dev)
+        kp = torch.zeros((nblocks, BS, SM_HKV, SM_D), device=dev, dtype=torch.bfloat16)
+        vp = torch.zeros_like(kp)
+        k = torch.randn((tokens, SM_HKV, SM_D), device=dev, dtype=torch.bfloat16)
+        bufs.append((k, torch.randn_like(k), perm, nat.PoolView.from_bshd(kp, vp),
+                     torch.empty_like(k), torch.empty_like(k)))
+    us = _graph_us(lambda i: nat.kv_write(bufs[i][0], bufs[i][1], bufs[i][2], bufs[i][3]), sets, reps)
+    gus = _graph_us(lambda i: nat.kv_gather(bufs[i][3], bufs[i][2], bufs[i][4], bufs[i][5]), sets, reps)
     nbytes = tokens * SM_HKV * SM_D * 2 * 2 * 2 + tokens * 8
-    kg, vg = torch.empty_like(k), torch.empty_like(v)
-    gevs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for a, b in gevs:
-        a.record()
-        nat.kv_gather(view, perm, kg, vg)
-        b.record()
-    torch.cuda.synchronize()
-    gus = _event_us(gevs)
     return {"tokens": tokens, "us": round(us, 2), "gbps": round(nbytes / us / 1e3, 1),
             "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4),
-            "gather_us": round(gus, 2), "gather_gbps": round(nbytes / gus / 1e3, 1)}
+            "gather_us": round(gus, 2), "gather_gbps": round(nbytes / gus / 1e3, 1),
+            "timing": f"graph replays of back-to-back launches over {sets} rotating buffer sets"}
 
 
 def run_c3(dev, layers=SM_LAYERS, reps=3):
@@ -811,25 +836,31 @@ def run_e2e(args, dev):
     }
 
 
-def _e2e_cpu_leg(cfg, prompts, n_requests: int = 2, new_tokens: int = 8) -> dict:
-    """CPU baseline of C4: the same model shape in fp32 on the host cores,
-    greedy, requests one after another with their own transformers cache (the
-    forward the reference engine runs, on its CPU device), on the first
-    requests of the same workload."""
+def _e2e_cpu_leg(cfg, prompts, n_requests: int = 8, new_tokens: int = 64) -> dict:
+    """CPU baseline of C4: the reference engine's CPU path (the host
+    scheduler, a forward per prefill, one left-padded batched forward per
+    decode step over contexts gathered from the pool; oracle.cpu_engine) with
+    the same model shape in fp32 on the host cores, the first requests of the
+    same workload all submitted at once."""
     from transformers import LlamaForCausalLM
 
-    from oracle.cpu_baseline import greedy_cpu
+    from oracle.cpu_engine import CpuBatchedEngine
 
     torch.set_num_threads(os.cpu_count() or 1)
     torch.manual_seed(0)
     model = LlamaForCausalLM(cfg).float().eval()
     sample = prompts[:n_requests]
+    need = sum((len(p) + new_tokens + BS - 1) // BS for p in sample)
+    eng = CpuBatchedEngine(model, num_blocks=need + n_requests, block_size=BS, max_num_seqs=n_requests)
     t0 = time.perf_counter()
-    greedy_cpu(model, sample, new_tokens)
+    out = eng.generate(sample, new_tokens)
     dt = time.perf_counter() - t0
+    assert all(len(o) == new_tokens for o in out)
     return _cpu_leg(round(n_requests * new_tokens / dt, 2), "output tok/s",
-                    f"{n_requests} requests (prompts of {[len(p) for p in sample]} tokens) x {new_tokens} greedy "
-                    f"tokens, SmolLM2-360M shape, fp32, {dt:.1f} s; beside saturated_tok_s")
+                    f"{n_requests} concurrent requests (prompts of {[len(p) for p in sample]} tokens) x "
+                    f"{new_tokens} greedy tokens through the reference's batched CPU path (host scheduler, "
+                    f"{eng.forward_passes} forward passes, left-padded batched decode), SmolLM2-360M shape, "
+                    f"fp32, {dt:.1f} s incl. prefill; beside saturated_tok_s")
 
 
 # --------------------------------------------------- draft proposals (C3 shape)
@@ -1091,6 +1122,10 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
+            "traffic_source": ("PMC FETCH_SIZE x2.0 + WRITE_SIZE x1.0 of this plan form's launch, from "
+                               + ("profiles/attn_slice_kernel_c5_decode_14b.md" if plan.sliced else
+                                  "profiles/attn_kernel_c5_decode_14b.md")
+                               + " (rocprofv3 --pmc; bench.py cannot read counters itself)") if traffic else None,
             "kernel": ("attn_slice_kernel<bf16,128>" if plan.sliced else
                        "attn_kernel<bf16,128,1,fast>" + (" (split-K merge fused)" if args.fused else "")),
             "kernel_avg_us": round(attn_avg_s * 1e6, 2),
