@@ -592,7 +592,7 @@ def run_kv_write_large(dev, tokens=33792, sets=6, reps=10):
             "timing": f"graph replays of back-to-back launches over {sets} rotating buffer sets"}
 
 
-def run_c3(dev, layers=SM_LAYERS, reps=3):
+def run_c3(dev, layers=SM_LAYERS, reps=3, cpu_leg=True):
     """Speculative verify step: 16 sequences, ctx U[128,2048], lookahead 4,
     so 5 query rows per sequence attend to the pool plus their own in-flight
     candidates; then rejection sampling over (16,5,49152) target and
@@ -668,6 +668,7 @@ def run_c3(dev, layers=SM_LAYERS, reps=3):
         vevs.append((a, b))
     torch.cuda.synchronize()
     ver_us = _event_us(vevs)
+    graph_ver_us = _graph_us(lambda i: nat.spec_verify(dt_d, dp_d, tl_d, 1.0, u_d, n_d), 10)
     ver_bytes = (B * (K + 1) * V + B * K * V) * 4
     return {
         "workload": "C3: 16 sequences, ctx U[128,2048], lookahead 4 (5 query rows each, candidates attended "
@@ -681,14 +682,16 @@ def run_c3(dev, layers=SM_LAYERS, reps=3):
         "graph_verify_attn_gbps": round(attn_bytes / graph_attn_us / 1e3, 1),
         "rejection_us": round(ver_us, 2),
         "rejection_gbps": round(ver_bytes / ver_us / 1e3, 1),
+        "graph_rejection_us": round(graph_ver_us, 2),
+        "graph_rejection_note": "per call, ten calls captured in one graph and replayed (kernels only, no host submission)",
         "accepted_per_row": res.num_accepted.cpu().tolist(),
         # the candidates' K/V go through the same scatter the CPU path would
         # do before attending them (the reference writes them to the pool)
         "cpu_baseline": _c2_c3_cpu_leg(kp[0], vp[0], nk[0], nv[0], torch.tensor(
             [tables[b][p // BS] * BS + p % BS for b, c in enumerate(ctx) for p in range(c, c + K + 1)]),
             q, tables, cu, positions, "C3 layer: scatter of the 80 verify rows + the materialised varlen "
-            "attention of 16 x 5 rows; beside graph_verify_attn_us"),
-        "rejection_cpu_baseline": _rejection_cpu_leg(dtok, dprobs, tl, u, noise),
+            "attention of 16 x 5 rows; beside graph_verify_attn_us") if cpu_leg else None,
+        "rejection_cpu_baseline": _rejection_cpu_leg(dtok, dprobs, tl, u, noise) if cpu_leg else None,
     }
 
 

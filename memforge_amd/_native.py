@@ -518,13 +518,14 @@ class CountedPlan:
 
 
 class Workspace:
-    """Grow-only scratch for split-K partials (fp32) and merge arrival
-    counters (int32, kept all-zero between calls by the kernels), one per
-    (device, stream) so concurrent streams never share it."""
+    """Grow-only scratch for split-K partials (fp32), merge arrival counters
+    (int32, kept all-zero between calls by the kernels) and the rejection
+    verify, one per (device, stream) so concurrent streams never share it."""
 
     def __init__(self) -> None:
         self._partials = {}
         self._counters = {}
+        self._verify = {}
 
     def partials(self, floats: int, device) -> Optional[torch.Tensor]:
         if floats <= 0:
@@ -535,6 +536,16 @@ class Workspace:
         if buf is None or buf.numel() < floats:
             buf = torch.empty(max(floats, 1 << 16), dtype=torch.float32, device=device)
             self._partials[key] = buf
+        return buf
+
+    def verify(self, nbytes: int, device) -> torch.Tensor:
+        """mf_spec_verify's scratch, kept between calls."""
+        dev = torch.device(device)
+        key = (dev.index, _stream(dev))
+        buf = self._verify.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            self._verify[key] = buf
         return buf
 
     def counters(self, n: int, device) -> Optional[torch.Tensor]:
@@ -939,6 +950,9 @@ class VerifyResult:
     num_accepted: torch.Tensor  # int32 [B]
 
 
+_VERIFY_WS_BYTES = {}  # (rows, candidates) -> mf_spec_verify_workspace_size
+
+
 def spec_verify(draft_tokens: torch.Tensor, draft_probs: torch.Tensor, target_logits: torch.Tensor,
                 temperature: float, u_accept: torch.Tensor, exp_noise: torch.Tensor,
                 target_is_probs: bool = False) -> VerifyResult:
@@ -956,16 +970,21 @@ def spec_verify(draft_tokens: torch.Tensor, draft_probs: torch.Tensor, target_lo
     draft_tokens = draft_tokens.to(torch.int32).contiguous()
     u_accept = u_accept.to(torch.float32).contiguous()
     dev = target_logits.device
-    # only the first count[b] entries of each row are written
+    # one allocation for the four outputs (only the first count[b] entries of
+    # each row are written); is_draft is bytes of its int32 tail
+    n = B * (K + 1)
+    out = torch.empty(n + 2 * B + (n + 3) // 4, dtype=torch.int32, device=dev)
     res = VerifyResult(
-        tokens=torch.empty((B, K + 1), dtype=torch.int32, device=dev),
-        is_draft=torch.empty((B, K + 1), dtype=torch.uint8, device=dev),
-        count=torch.empty(B, dtype=torch.int32, device=dev),
-        num_accepted=torch.empty(B, dtype=torch.int32, device=dev),
+        tokens=out[:n].view(B, K + 1),
+        is_draft=out[n + 2 * B:].view(torch.uint8)[:n].view(B, K + 1),
+        count=out[n:n + B],
+        num_accepted=out[n + B:n + 2 * B],
     )
     L = lib()
-    ws_bytes = int(L.mf_spec_verify_workspace_size(B, K))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ws_bytes = _VERIFY_WS_BYTES.get((B, K))
+    if ws_bytes is None:
+        ws_bytes = _VERIFY_WS_BYTES[(B, K)] = int(L.mf_spec_verify_workspace_size(B, K))
+    ws = _WORKSPACE.verify(ws_bytes, dev)
     _check(L.mf_spec_verify(
         B, K, V, _ptr(draft_tokens), _ptr(draft_probs),
         draft_probs.stride(0) if K > 0 else 0, draft_probs.stride(1) if K > 0 else 0,

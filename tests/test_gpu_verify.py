@@ -180,3 +180,18 @@ def test_greedy_zero_uniform_accepts_a_mismatching_candidate(device):
     noise = torch.empty((B, V)).exponential_(1.0, generator=gen)
     count, nacc = _run_both(device, draft, target, tokens, u, noise, 0.0)
     assert nacc.tolist() == [4, 2] and count.tolist() == [5, 3]
+
+
+
+def test_repeated_calls_on_one_workspace_and_a_large_batch(device):
+    """The binding keeps its scratch between calls: repeated calls give the
+    oracle's tokens every time, and a batch of 1,100 rows (over a small
+    vocabulary) resolves like a small one."""
+    draft, target, tokens, u, noise = _inputs(21, 16, 4, 49152, agree=0.5)
+    first = None
+    for _ in range(3):
+        count, nacc = _run_both(device, draft, target, tokens, u, noise, 1.0)
+        first = (count, nacc) if first is None else first
+        assert (count == first[0]).all() and (nacc == first[1]).all()
+    draft, target, tokens, u, noise = _inputs(22, 1100, 2, 96, agree=0.5)
+    _run_both(device, draft, target, tokens, u, noise, 0.9)
