@@ -415,22 +415,25 @@ def run_c2(dev, layers=SM_LAYERS, reps=3, fused_leg=True, cpu_leg=True):
     pos_t = torch.tensor(positions, dtype=torch.int64, device=dev)
     plan = nat.plan_attention(cu, kv, SM_HQ, SM_HKV, SM_D, torch.bfloat16, dev)
     partials = torch.empty(max(plan.partials_floats, 1), dtype=torch.float32, device=dev)
-    narrow = nat.AttentionPlan(plan.items, plan.merges, plan.n_narrow, 0, 0, plan.partials_floats,
+    # The mixed plan's three parts, each launched alone: its decode items,
+    # its prefill items (the same items, partial slots and order as in the
+    # mixed launch) and its merge, so the parts read and write the same
+    # partials as the engine's launch.
+    nn = plan.n_narrow
+    narrow = nat.AttentionPlan(plan.items, plan.merges, nn, 0, 0, plan.partials_floats,
                                plan.items_host, plan.merges_host)
-    # The prefill items alone, as a prefill-only step plans them (decodes with
-    # no rows): the same items, partial slots and merge records as the mixed
-    # plan's wide part, in the order the planner gives a launch of wide items
-    # only (each key range's workgroups on one XCD). The merge leg then reads
-    # the same partials either way.
-    plan_pre = nat.plan_attention(cu[:5] + [cu[4]] * 28, kv, SM_HQ, SM_HKV, SM_D, torch.bfloat16, dev)
-    mixed_wide = plan.items_host[plan.n_narrow:plan.n_narrow + plan.n_wide]
-    assert plan_pre.n_narrow == 0 and plan_pre.n_wide == plan.n_wide, "prefill-only plan differs"
-    assert sorted(map(tuple, mixed_wide.tolist())) == sorted(map(tuple, plan_pre.items_host.tolist())), \
-        "prefill-only plan holds other items"
-    wide = nat.AttentionPlan(plan_pre.items, plan_pre.merges, 0, plan_pre.n_wide, 0, plan_pre.partials_floats,
-                             plan_pre.items_host, plan_pre.merges_host)
+    wide = nat.AttentionPlan(plan.items[nn:], plan.merges, 0, plan.n_wide, 0, plan.partials_floats,
+                             plan.items_host[nn:], plan.merges_host)
     merges = nat.AttentionPlan(plan.items, plan.merges, 0, 0, plan.n_merges, plan.partials_floats,
                                plan.items_host, plan.merges_host)
+    # A prefill-only step (the decodes given no rows) plans the same chunks
+    # as wide items only: the planner's XCD order and the single-class
+    # partition. Its items are timed as a side figure.
+    plan_pre = nat.plan_attention(cu[:5] + [cu[4]] * 28, kv, SM_HQ, SM_HKV, SM_D, torch.bfloat16, dev)
+    assert plan_pre.n_narrow == 0 and plan_pre.n_wide > 0, "prefill-only plan holds decode items"
+    wide_pre = nat.AttentionPlan(plan_pre.items, plan_pre.merges, 0, plan_pre.n_wide, 0, plan_pre.partials_floats,
+                                 plan_pre.items_host, plan_pre.merges_host)
+    partials_pre = torch.empty(max(plan_pre.partials_floats, 1), dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(SM_D)
     views = [nat.PoolView.from_bshd(kp[i], vp[i]) for i in range(layers)]
 
@@ -459,6 +462,17 @@ def run_c2(dev, layers=SM_LAYERS, reps=3, fused_leg=True, cpu_leg=True):
     pre_us = _event_us([(e[2], e[3]) for e in evs])
     mrg_us = _event_us([(e[3], e[4]) for e in evs])
     graph_layer_us = _graph_us(layer, layers)
+    pre_evs = []
+    for r in range(reps):
+        for i in range(layers):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            nat.paged_attention(q, out, views[i], bt, cu_t, kv_t, pos_t, wide_pre, scale, SM_HKV,
+                                partials=partials_pre)
+            b.record()
+            pre_evs.append((a, b))
+    torch.cuda.synchronize()
+    pre_only_us = _event_us(pre_evs)
 
     def layer_whole(i):
         # the engine's form: one call with the whole plan (decode and prefill
@@ -504,9 +518,17 @@ def run_c2(dev, layers=SM_LAYERS, reps=3, fused_leg=True, cpu_leg=True):
         "prefill_mfma_frac": round(pre_flops / pre_us / 1e6 / BF16_PEAK_TFLOPS, 4),
         "prefill_attn_gbps": round(pre_bytes / pre_us / 1e3, 1),
         "merge_us": round(mrg_us, 2),
-        "timing_note": "kv_write/decode/prefill/merge figures are the layer's parts timed apart between "
-                       "events; prefill_* is the prefill items alone as a prefill-only step plans them "
-                       "(a side figure: the engine runs them inside the mixed launch, see engine_layer)",
+        "prefill_only_plan": {
+            "us": round(pre_only_us, 2),
+            "tflops": round(pre_flops / pre_only_us / 1e6, 1),
+            "mfma_frac": round(pre_flops / pre_only_us / 1e6 / BF16_PEAK_TFLOPS, 4),
+            "wide_items": plan_pre.n_wide,
+            "note": "side figure: the same chunks planned as a prefill-only step (no decodes), its prefill "
+                    "items alone between events",
+        },
+        "timing_note": "kv_write/decode/prefill/merge figures are the mixed plan's parts timed apart between "
+                       "events (side figures: the engine runs decode and prefill items in one launch, see "
+                       "engine_layer)",
         "plan": {"narrow": plan.n_narrow, "wide": plan.n_wide, "merges": plan.n_merges},
         "engine_layer": {
             "us": round(graph_fused_us, 2),

@@ -1980,7 +1980,7 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
         }
         return best_q;
     };
-    int64_t work = 0, wide_units = 0;
+    int64_t work = 0, wide_units = 0, narrow_units = 0;
     int wide_max_tiles = 0;
     for (int s = 0; s < num_seqs; ++s) {
         const int nct = col_tiles(s);
@@ -1989,6 +1989,7 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
         const int groups = narrow ? nct : (nct + WT - 1) / WT;
         const int tiles = (kv_lens[s] + 15) / 16;
         work += (int64_t)Hkv * groups * tiles;
+        if (narrow) narrow_units += (int64_t)Hkv * groups;
         if (!narrow) {
             wide_units += (int64_t)Hkv * groups;
             wide_max_tiles = std::max(wide_max_tiles, tiles);
@@ -2029,7 +2030,17 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
             // classes run as separate launches, where the raised partition
             // only lengthens the narrow launch's chains (no effect on
             // results, which do not depend on the partition).
-            if (MF_MIXED_LAUNCH && WT > 1 && dtype != MF_F32 && head_dim == DP) P = std::max(P, PW);
+            // The wide partition is then doubled: in the shared launch the
+            // wide chains run beside the narrow ones, and half the partitions
+            // halve the split-K partials and the merge's reads. C2 step,
+            // graph replays: PW 32 49.0-49.1 us per layer, PW 64 47.1-47.2
+            // (merge 12.2 -> 9.7 us), PW 128 64.6. A plan of wide items only
+            // keeps PW (there the prefill items alone take 35.5 us at PW 32
+            // against 41 at 64).
+            if (MF_MIXED_LAUNCH && WT > 1 && dtype != MF_F32 && head_dim == DP && narrow_units > 0) {
+                P = std::max(P, PW);
+                PW = std::min(2 * PW, (int)mf::kMaxItemTiles);
+            }
         }
     }
 

@@ -358,9 +358,9 @@ def test_planner_partition_picks_on_the_config_shapes():
 
 def test_planner_mixed_step_partitions_on_the_c2_shape():
     """The C2 mixed step (4 chunks of 512 on priors U[0,2048] + 28 decodes of
-    U[64,4096], bf16 D 64): the wide partition is the smallest power of two
-    that keeps wide items within the target (32 tiles), and the narrow
-    partition is raised to it because both classes share one launch."""
+    U[64,4096], bf16 D 64): the narrow partition is raised to the smallest
+    power of two that keeps wide items within the target (32 tiles), because
+    both classes share one launch, and the wide partition is twice that."""
     g = torch.Generator().manual_seed(0)
     prior = torch.randint(0, 2049, (4,), generator=g).tolist()
     dctx = torch.randint(64, 4097, (28,), generator=g).tolist()
@@ -370,8 +370,12 @@ def test_planner_mixed_step_partitions_on_the_c2_shape():
     p = _plan(cu, kv, hq=15, hkv=5, d=64)
     wide = p.items_host[p.n_narrow:]
     live = wide[wide[:, 3] > 0]
-    assert int((live[:, 5] - live[:, 4]).max()) == 32
+    assert int((live[:, 5] - live[:, 4]).max()) == 64
     assert _partition_of(p.items_host[: p.n_narrow]) == 32
+    # the same chunks with no decodes: one class, the wide partition kept
+    pre = _plan(cu[:5], kv[:4], hq=15, hkv=5, d=64)
+    live = pre.items_host[pre.items_host[:, 3] > 0]
+    assert pre.n_narrow == 0 and int((live[:, 5] - live[:, 4]).max()) == 32
     # decode rows alone keep the estimate's own pick
     alone = _plan(list(range(29)), dctx, hq=15, hkv=5, d=64)
     assert _partition_of(alone.items_host[: alone.n_narrow]) == 16
