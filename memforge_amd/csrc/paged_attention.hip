@@ -2061,11 +2061,19 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     const int U = mf::kWaves;
     auto round_up = [&](int64_t n) { return (n + U - 1) / U * U; };
     // key partitions of sequence s: count, and the start of partition p
-    // (narrow cooperative ranges are balanced; the rest are Q-tile strides)
+    // (narrow cooperative ranges are balanced; the rest are Q-tile strides).
+    // A wide range takes as many partitions as PW-tile strides would give,
+    // in strides of equal length: on the C2 step 46.0-46.9 us per layer
+    // against 47.1-47.6 with PW strides (a short last partition), and the
+    // same chunks planned prefill-only 34.9-35.3 against 36.3-36.6 us.
     auto partitions = [&](int s, bool narrow, int& Q, bool& coop) {
         const int tiles = (kv_lens[s] + 15) / 16;
         coop = narrow && tiles > P;
         Q = narrow ? (coop ? U * P : P) : PW;
+        if (!narrow && tiles > PW) {
+            const int np = (tiles + PW - 1) / PW;
+            Q = (tiles + np - 1) / np;
+        }
         return (tiles + Q - 1) / Q;
     };
     auto part_begin = [&](int tiles, int nparts, int Q, bool coop, int p) {

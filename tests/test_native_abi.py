@@ -360,7 +360,9 @@ def test_planner_mixed_step_partitions_on_the_c2_shape():
     """The C2 mixed step (4 chunks of 512 on priors U[0,2048] + 28 decodes of
     U[64,4096], bf16 D 64): the narrow partition is raised to the smallest
     power of two that keeps wide items within the target (32 tiles), because
-    both classes share one launch, and the wide partition is twice that."""
+    both classes share one launch, and the wide partition is twice that: each
+    chunk's key range is cut into as many partitions as 64-tile strides give,
+    in strides of equal length."""
     g = torch.Generator().manual_seed(0)
     prior = torch.randint(0, 2049, (4,), generator=g).tolist()
     dctx = torch.randint(64, 4097, (28,), generator=g).tolist()
@@ -370,12 +372,20 @@ def test_planner_mixed_step_partitions_on_the_c2_shape():
     p = _plan(cu, kv, hq=15, hkv=5, d=64)
     wide = p.items_host[p.n_narrow:]
     live = wide[wide[:, 3] > 0]
-    assert int((live[:, 5] - live[:, 4]).max()) == 64
+    for e in range(4):
+        tiles = (kv[e] + 15) // 16
+        starts = sorted({int(x) for x in live[live[:, 0] == e, 4]})
+        assert len(starts) == -(-tiles // 64)
+        lengths = np.diff(starts + [tiles])
+        # equal strides; the last one short by less than one tile per partition
+        assert len(set(lengths[:-1].tolist())) <= 1 and lengths[0] <= 64
+        assert 0 <= lengths[0] - lengths[-1] < len(lengths)
     assert _partition_of(p.items_host[: p.n_narrow]) == 32
-    # the same chunks with no decodes: one class, the wide partition kept
+    # the same chunks with no decodes: one class, 32-tile partitions
     pre = _plan(cu[:5], kv[:4], hq=15, hkv=5, d=64)
     live = pre.items_host[pre.items_host[:, 3] > 0]
-    assert pre.n_narrow == 0 and int((live[:, 5] - live[:, 4]).max()) == 32
+    assert pre.n_narrow == 0 and int((live[:, 5] - live[:, 4]).max()) <= 32
+    assert len({(int(r[0]), int(r[4])) for r in live}) == sum(-(-((c + 15) // 16) // 32) for c in kv[:4])
     # decode rows alone keep the estimate's own pick
     alone = _plan(list(range(29)), dctx, hq=15, hkv=5, d=64)
     assert _partition_of(alone.items_host[: alone.n_narrow]) == 16
