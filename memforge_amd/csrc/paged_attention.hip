@@ -66,8 +66,8 @@ constexpr int kMaxItemTiles = MF_MAX_ITEM_TILES;  // key tiles per work item (tw
 #ifndef MF_WIDE_PRIO
 #define MF_WIDE_PRIO 1
 #endif
-// XCD-local order of the wide workgroups in plans without single-tile items
-// (1). The dispatcher sends workgroup b of a launch to XCD b mod 8, so the
+// XCD-local order of the wide workgroups (1). The dispatcher sends
+// workgroup b of a launch to XCD b mod 8, so the
 // consecutive wide workgroups of one key range (the column groups of one
 // sequence, kv head and key partition, which read the same K/V tiles) land on
 // eight XCDs whose L2s each fetch the tiles. The planner instead deals whole
@@ -75,10 +75,12 @@ constexpr int kMaxItemTiles = MF_MAX_ITEM_TILES;  // key tiles per work item (tw
 // workgroup 8k + x comes from queue x and a range stays on one XCD; each
 // queue runs its workgroups most causal work first. Measured on the C2
 // prefill items alone: 38.2-38.8 us -> 35.1-35.5 us between events, PMC
-// FETCH 74 MB -> 24 MB (1.4x the K/V and query bytes). Beside single-tile
-// items (one mixed launch) the same order was slower (C2 engine layer 49.2
-// -> 50.2 us; the causal-work order alone 51.2 us), so mixed plans keep the
-// range-length order.
+// FETCH 74 MB -> 24 MB (1.4x the K/V and query bytes). In a mixed launch the
+// wide workgroups follow the single-tile ones, which only rotates the XCDs
+// (a range still shares one). There, at 32-tile wide partitions, the order
+// was slower (C2 engine layer 49.2 -> 50.2 us); at the mixed plans' doubled,
+// equal-stride partitions it is faster: 45.71-45.75 against 45.85-45.94 us,
+// and the mixed plan's prefill items alone 34.7-34.9 against 39.6-39.8 us.
 #ifndef MF_WIDE_XCD
 #define MF_WIDE_XCD 1
 #endif
@@ -2258,7 +2260,7 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
         for (int w = 0; w < U; ++w) l = std::max(l, item_work(u[w]));
         return l;
     };
-    if (MF_WIDE_XCD && n_narrow == 0) {
+    if (MF_WIDE_XCD) {
         // Runs of workgroups on one key range, most work first, are dealt
         // to the queue with the least work so far; each queue then runs its
         // workgroups most work first, and the queues are interleaved.
