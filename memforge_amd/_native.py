@@ -11,6 +11,7 @@ runs on the MI355X or not at all.
 from __future__ import annotations
 
 import ctypes
+from collections import OrderedDict
 from dataclasses import dataclass
 from pathlib import Path
 from typing import List, Optional, Sequence, Tuple
@@ -439,11 +440,25 @@ def plan_slices_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_he
     return slices, merges[:n_merges], counts
 
 
+_DEVICE_CUS = {}
+
+
 def device_cus(device) -> int:
     """Compute units of ``device`` (a slice plan's size is set by it)."""
     dev = torch.device(device)
-    return torch.cuda.get_device_properties(dev.index if dev.index is not None
-                                            else torch.cuda.current_device()).multi_processor_count
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    cus = _DEVICE_CUS.get(index)
+    if cus is None:
+        cus = _DEVICE_CUS[index] = torch.cuda.get_device_properties(index).multi_processor_count
+    return cus
+
+
+# plan_host results by their inputs, most recent last. The planners are pure
+# functions of them, and a model that calls the attention operator once per
+# layer asks for the same plan in every layer of a step. The arrays are handed
+# out read-only, so no caller can change what a later hit returns.
+_PLAN_CACHE: "OrderedDict[tuple, tuple]" = OrderedDict()
+PLAN_CACHE_SIZE = 64
 
 
 def plan_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int, num_kv_heads: int,
@@ -454,13 +469,26 @@ def plan_host(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: in
     blocks, no row map and no in-flight keys) a decode step large enough to
     fill the GPU on ``device`` more than once gets a slice plan; every other
     call, and an explicit ``partition_tiles``, the per-range plan."""
-    if decode_slices and partition_tiles <= 0 and device is not None and torch.device(device).type == "cuda":
-        made = plan_slices_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim, dtype,
-                                device_cus(device))
-        if made is not None:
-            return (*made, True)
-    return (*plan_attention_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim, dtype,
-                                 partition_tiles), False)
+    slices = decode_slices and partition_tiles <= 0 and device is not None and torch.device(device).type == "cuda"
+    cus = device_cus(device) if slices else 0
+    key = (tuple(int(x) for x in cu_seqlens), tuple(int(x) for x in kv_lens), num_q_heads, num_kv_heads,
+           head_dim, dtype, partition_tiles, cus)
+    hit = _PLAN_CACHE.get(key)
+    if hit is not None:
+        _PLAN_CACHE.move_to_end(key)
+        return hit
+    made = plan_slices_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim, dtype, cus) if slices else None
+    if made is not None:
+        out = (*made, True)
+    else:
+        out = (*plan_attention_host(cu_seqlens, kv_lens, num_q_heads, num_kv_heads, head_dim, dtype,
+                                    partition_tiles), False)
+    for a in out[:3]:
+        a.flags.writeable = False
+    _PLAN_CACHE[key] = out
+    if len(_PLAN_CACHE) > PLAN_CACHE_SIZE:
+        _PLAN_CACHE.popitem(last=False)
+    return out
 
 
 def plan_attention(cu_seqlens: Sequence[int], kv_lens: Sequence[int], num_q_heads: int,

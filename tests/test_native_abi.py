@@ -513,3 +513,26 @@ def test_noalloc_refuses_a_plan_whose_slots_reach_past_its_array():
         q = torch.zeros((2, 40, 128), dtype=torch.bfloat16)
         with pytest.raises(nat.MemforgeHipError, match="workspace"):
             nat.paged_attention_noalloc(q, q.clone(), None, None, None, None, None, bad, 0.1, 8)
+
+
+def test_plan_host_cache_returns_read_only_plans_and_stays_bounded():
+    """plan_host hands back the same read-only arrays for the same inputs
+    (the planners are pure functions of them), a different plan for any
+    changed input, and keeps at most PLAN_CACHE_SIZE plans."""
+    a = nat.plan_host([0, 1, 2], [300, 40], 15, 5, 64, torch.float32, "cpu")
+    b = nat.plan_host([0, 1, 2], [300, 40], 15, 5, 64, torch.float32, "cpu")
+    assert a[0] is b[0] and a[1] is b[1] and a[2] is b[2] and a[3] is False and b[3] is False
+    for arr in a[:3]:
+        assert not arr.flags.writeable
+        with pytest.raises(ValueError):
+            arr[...] = 0
+    fresh = nat.plan_attention_host([0, 1, 2], [300, 40], 15, 5, 64, torch.float32)
+    assert all(np.array_equal(x, y) for x, y in zip(a[:3], fresh))
+    for other in (([0, 1, 2], [300, 41], 15, 5, 64, torch.float32), ([0, 1, 2], [300, 40], 15, 5, 64, torch.bfloat16),
+                  ([0, 2, 3], [300, 40], 15, 5, 64, torch.float32), ([0, 1, 2], [300, 40], 16, 4, 64, torch.float32)):
+        c = nat.plan_host(*other, "cpu")
+        want = nat.plan_attention_host(*other)
+        assert c[0] is not a[0] and all(np.array_equal(x, y) for x, y in zip(c[:3], want))
+    for n in range(nat.PLAN_CACHE_SIZE + 10):
+        nat.plan_host([0, 1], [17 + n], 8, 2, 64, torch.float32, "cpu")
+    assert len(nat._PLAN_CACHE) == nat.PLAN_CACHE_SIZE
