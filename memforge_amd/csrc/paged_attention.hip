@@ -78,9 +78,11 @@ constexpr int kMaxItemTiles = MF_MAX_ITEM_TILES;  // key tiles per work item (tw
 // FETCH 74 MB -> 24 MB (1.4x the K/V and query bytes). In a mixed launch the
 // wide workgroups follow the single-tile ones, which only rotates the XCDs
 // (a range still shares one). There, at 32-tile wide partitions, the order
-// was slower (C2 engine layer 49.2 -> 50.2 us); at the mixed plans' doubled,
-// equal-stride partitions it is faster: 45.71-45.75 against 45.85-45.94 us,
-// and the mixed plan's prefill items alone 34.7-34.9 against 39.6-39.8 us.
+// was slower (C2 engine layer 49.2 -> 50.2 us); at 64-tile equal-stride
+// partitions it was faster: 45.71-45.75 against 45.85-45.94 us, and the mixed
+// plan's prefill items alone 34.7-34.9 against 39.6-39.8 us. Mixed plans now
+// cut each column quad on its own (quad partitions, in the planner) and keep
+// a (sequence, kv head)'s workgroups on one XCD.
 #ifndef MF_WIDE_XCD
 #define MF_WIDE_XCD 1
 #endif
@@ -1999,6 +2001,7 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     }
     int P = std::min(partition_tiles, mf::kMaxItemTiles);
     int PW = P;
+    bool mixed = false;  // a shared launch of narrow and wide items (quad partitions below)
     if (P <= 0) {
         const int64_t target_items = MF_NARROW_ITEMS;
         int64_t want = (work + target_items - 1) / target_items;
@@ -2032,16 +2035,9 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
             // classes run as separate launches, where the raised partition
             // only lengthens the narrow launch's chains (no effect on
             // results, which do not depend on the partition).
-            // The wide partition is then doubled: in the shared launch the
-            // wide chains run beside the narrow ones, and half the partitions
-            // halve the split-K partials and the merge's reads. C2 step,
-            // graph replays: PW 32 49.0-49.1 us per layer, PW 64 47.1-47.2
-            // (merge 12.2 -> 9.7 us), PW 128 64.6. A plan of wide items only
-            // keeps PW (there the prefill items alone take 35.5 us at PW 32
-            // against 41 at 64).
             if (MF_MIXED_LAUNCH && WT > 1 && dtype != MF_F32 && head_dim == DP && narrow_units > 0) {
                 P = std::max(P, PW);
-                PW = std::min(2 * PW, (int)mf::kMaxItemTiles);
+                mixed = true;
             }
         }
     }
@@ -2065,9 +2061,9 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     // key partitions of sequence s: count, and the start of partition p
     // (narrow cooperative ranges are balanced; the rest are Q-tile strides).
     // A wide range takes as many partitions as PW-tile strides would give,
-    // in strides of equal length: on the C2 step 46.0-46.9 us per layer
-    // against 47.1-47.6 with PW strides (a short last partition), and the
-    // same chunks planned prefill-only 34.9-35.3 against 36.3-36.6 us.
+    // in strides of equal length: the C2 chunks planned prefill-only
+    // 34.9-35.3 us against 36.3-36.6 with PW strides (a short last
+    // partition).
     auto partitions = [&](int s, bool narrow, int& Q, bool& coop) {
         const int tiles = (kv_lens[s] + 15) / 16;
         coop = narrow && tiles > P;
@@ -2080,6 +2076,48 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
     };
     auto part_begin = [&](int tiles, int nparts, int Q, bool coop, int p) {
         return coop ? (int)((int64_t)p * tiles / nparts) : std::min(tiles, p * Q);
+    };
+    // Quad partitions (mixed plans). A sequence whose wide items fill whole
+    // workgroups runs as column quads: the kWaves column groups one
+    // workgroup holds, over one key range. In a mixed plan each quad takes
+    // its own partitions: the tiles its last column sees, cut into
+    // round(visible / W) equal ranges, W chosen so that the launch's wide
+    // workgroups carry about two rounds' worth per compute unit (the total
+    // visible work over 2 x 256 CUs, at least PW). Every wide workgroup then
+    // holds about the same work, and each compute unit about two of them
+    // beside the narrow ones, all in one resident round. C2 step, engine
+    // layer as graph replays: 44.1-44.2 us against 45.8-46.0 with the ranges'
+    // partitions (PW 64 strides); 1.5 workgroups per CU 49.3-49.6, 2.5
+    // 47.1-47.4, 3 47.5-48.0, 4 53.3-53.5. Plans of wide items only keep the
+    // ranges' partitions (there two per CU took the prefill items from 35.1
+    // to 37.9 us). The XCD queues below take a (sequence, kv head)'s quads
+    // as one run: the launch fetches 1.09x its algorithmic reads, against
+    // 1.65x with each (quad, kv head) dealt alone (0.3 us faster).
+    constexpr int kPlanCUs = 256;  // compute units of an MI355X
+    auto quads = [&](int s) -> int {  // column quads of s, 0 if s is not a shared wide sequence
+        const int nct = col_tiles(s);
+        if (!mixed || !nct || nct == 1 || WT == 1) return 0;
+        const int ngroups = (nct + WT - 1) / WT;
+        return ngroups >= U ? (int)(round_up(ngroups) / U) : 0;
+    };
+    auto quad_visible = [&](int s, int qd) -> int {
+        const int rows = cu_seqlens[s + 1] - cu_seqlens[s];
+        const int end_ct = std::min(col_tiles(s), (qd + 1) * U * WT);
+        const int last_col = std::min(end_ct * 16, rows * G) - 1;
+        const int last_pos = kv_lens[s] - rows + last_col / G;
+        return std::max(1, std::min((kv_lens[s] + 15) / 16, last_pos / 16 + 1));
+    };
+    double quad_w = 1.0;
+    if (mixed) {
+        int64_t visible = 0;
+        for (int s = 0; s < num_seqs; ++s)
+            for (int qd = 0, nq = quads(s); qd < nq; ++qd) visible += (int64_t)Hkv * quad_visible(s, qd);
+        quad_w = std::max((double)std::max(PW, 1), (double)visible / (2.0 * kPlanCUs));
+    }
+    auto quad_parts = [&](int s, int qd) {
+        const int v = quad_visible(s, qd);
+        const int n = std::max(1, (int)std::lround(v / quad_w));
+        return std::max(n, (v + mf::kMaxItemTiles - 1) / mf::kMaxItemTiles);
     };
 
     // First walk: sizes only.
@@ -2096,6 +2134,17 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
         if (narrow) {
             if (coop) n_coop += (int64_t)U * nparts * Hkv * ngroups;
             else n_single += (int64_t)nparts * Hkv * ngroups;
+        } else if (const int nq = quads(s)) {
+            for (int qd = 0; qd < nq; ++qd) {
+                const int n = quad_parts(s, qd);
+                const int cols = std::min(nct, (qd + 1) * U * WT) - qd * U * WT;
+                n_wide += (int64_t)Hkv * n * U;
+                if (n > 1) {
+                    n_slots += (int64_t)Hkv * n * cols;
+                    n_merges += (int64_t)Hkv * cols;
+                }
+            }
+            continue;
         } else if (ngroups >= U) {
             n_wide += (int64_t)nparts * Hkv * round_up(ngroups);
         } else {
@@ -2134,6 +2183,65 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
         const int nparts = partitions(s, narrow, Q, coop);
         const int width = narrow ? 1 : WT;
         const int ngroups = (nct + width - 1) / width;
+        if (const int nq = narrow ? 0 : quads(s)) {
+            // quad partitions: per (kv head, quad), each column group owns
+            // n * w consecutive slots (partition-major) and w merge records;
+            // a kv head's workgroups are consecutive (one XCD run)
+            for (int h = 0; h < Hkv; ++h) {
+                for (int qd = 0; qd < nq; ++qd) {
+                    const int n = quad_parts(s, qd);
+                    const int v = quad_visible(s, qd);
+                    int64_t gslot[mf::kWaves], grec[mf::kWaves];
+                    for (int k = 0; k < U; ++k) {
+                        const int gi = qd * U + k;
+                        gslot[k] = grec[k] = -1;
+                        if (gi >= ngroups || n <= 1) continue;
+                        const int w = std::min(WT, nct - gi * WT);
+                        gslot[k] = slots;
+                        slots += (int64_t)n * w;
+                        grec[k] = wm;
+                        for (int o2 = 0; o2 < w; ++o2, ++wm) {
+                            int32_t* o = merges + wm * MF_PLAN_MERGE_INTS;
+                            o[0] = s;
+                            o[1] = h;
+                            o[2] = gi * WT + o2;
+                            o[3] = n;
+                            o[4] = (int32_t)(gslot[k] + o2);
+                            o[5] = w;
+                            o[6] = cu_seqlens[s];
+                            o[7] = cu_seqlens[s + 1] - cu_seqlens[s];
+                        }
+                    }
+                    for (int p = 0; p < n; ++p) {
+                        const int k0 = (int)((int64_t)p * v / n), k1 = (int)((int64_t)(p + 1) * v / n);
+                        for (int k = 0; k < U; ++k) {
+                            const int gi = qd * U + k;
+                            Item o{};
+                            o[0] = s;
+                            o[1] = h;
+                            o[4] = k0;
+                            o[5] = k1;
+                            o[8] = cu_seqlens[s];
+                            o[9] = cu_seqlens[s + 1] - cu_seqlens[s];
+                            o[10] = kv_lens[s];
+                            if (gi < ngroups) {
+                                const int w = std::min(WT, nct - gi * WT);
+                                o[2] = gi * WT;
+                                o[3] = w;
+                                o[6] = n > 1 ? (int32_t)(gslot[k] + (int64_t)p * w) : -1;
+                                o[7] = n > 1 ? (int32_t)grec[k] : -1;
+                            } else {  // padding: same keys, no columns, no partial slot
+                                o[2] = (ngroups - 1) * WT;
+                                o[6] = -1;
+                                o[7] = -1;
+                            }
+                            shared_items.push_back(o);
+                        }
+                    }
+                }
+            }
+            continue;
+        }
         const int64_t slot0 = slots, merge0 = wm;
         auto make = [&](int gi, int p, int h, int k0, int k1) {
             const int cg0 = gi * width;
@@ -2271,7 +2379,9 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
         auto same_range = [&](size_t x, size_t y) {
             const Item& a = wunits[x][0];
             const Item& b = wunits[y][0];
-            return a[0] == b[0] && a[1] == b[1] && a[4] == b[4] && a[5] == b[5];
+            // one key range; in a mixed plan one (sequence, kv head), whose
+            // quads' ranges overlap
+            return a[0] == b[0] && a[1] == b[1] && (mixed || (a[4] == b[4] && a[5] == b[5]));
         };
         // run r holds units [run_begin[r], run_begin[r + 1])
         std::vector<size_t> run_begin;

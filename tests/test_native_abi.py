@@ -109,16 +109,19 @@ def _check_plan_cover(q_lens, kv, hq, hkv, d, dtype, pt):
                     continue
                 assert sl not in slots
                 slots[sl] = (s, h, c)
+    # every key tile a column tile's last column can see is planned (once,
+    # above); a plan may also cover tiles past that, which the kernel masks
     for s, (q, n) in enumerate(zip(q_lens, kv)):
         if q == 0 or n == 0:
             continue
         nct = (q * G + 15) // 16
         for h in range(hkv):
             for c in range(nct):
-                for kt in range((n + 15) // 16):
-                    assert (s, h, c, kt) in cover
-    assert len(cover) == sum(hkv * ((q * G + 15) // 16) * ((n + 15) // 16)
-                             for q, n in zip(q_lens, kv) if q and n)
+                last_row = (min((c + 1) * 16, q * G) - 1) // G
+                for kt in range(min((n + 15) // 16, (n - q + last_row) // 16 + 1)):
+                    assert (s, h, c, kt) in cover, f"visible tile {(s, h, c, kt)} not planned"
+    for s, h, c, kt in cover:
+        assert kt < (kv[s] + 15) // 16, "a tile past the sequence's keys"
     # each merge record reads exactly the partial slots of its (s, h, column)
     seen = set()
     for m in merges:
@@ -162,9 +165,10 @@ def test_prefill_only_plans_of_any_shape_cover_every_tile_once(q_lens, kv):
 @pytest.mark.parametrize("decodes", [0, 12])
 @pytest.mark.parametrize("hq,hkv,d", [(15, 5, 64), (8, 2, 128), (16, 4, 32)])
 def test_plan_keeps_each_key_range_on_one_xcd(hq, hkv, d, decodes):
-    """The wide workgroups of one key range sit at wide positions of one
-    residue mod 8 (the XCD the dispatcher sends them to; in a mixed launch
-    the single-tile workgroups before them only rotate the residues), the
+    """The wide workgroups of one key range (in a mixed plan, of one
+    sequence and kv head) sit at wide positions of one residue mod 8 (the
+    XCD the dispatcher sends them to; in a mixed launch the single-tile
+    workgroups before them only rotate the residues), the
     eight residue classes carry near-equal causal work, and each class runs
     its workgroups most work first. With and without decode rows."""
     rng = np.random.default_rng(d)
@@ -181,6 +185,8 @@ def test_plan_keeps_each_key_range_on_one_xcd(hq, hkv, d, decodes):
         keys = {(int(it[0]), int(it[1]), int(it[4]), int(it[5])) for it in u}
         if len(keys) == 1:
             key = keys.pop()
+            if decodes:  # a mixed plan's quads of one (sequence, kv head) read overlapping ranges
+                key = key[:2]
             ranges.setdefault(key, set()).add(w % 8)
             run_work[key] = run_work.get(key, 0) + work[w]
     # a run split between two queues (at most one per queue but the last)
@@ -368,35 +374,47 @@ def test_planner_mixed_step_partitions_on_the_c2_shape():
     """The C2 mixed step (4 chunks of 512 on priors U[0,2048] + 28 decodes of
     U[64,4096], bf16 D 64): the narrow partition is raised to the smallest
     power of two that keeps wide items within the target (32 tiles), because
-    both classes share one launch, and the wide partition is twice that: each
-    chunk's key range is cut into as many partitions as 64-tile strides give,
-    in strides of equal length."""
+    both classes share one launch. Each column quad (the four column groups
+    of one wide workgroup) cuts the tiles its last column sees into
+    round(visible / W) equal ranges, W = the visible work over 2 x 256 compute
+    units: every wide workgroup holds about the same work, about 512 of
+    them."""
     g = torch.Generator().manual_seed(0)
     prior = torch.randint(0, 2049, (4,), generator=g).tolist()
     dctx = torch.randint(64, 4097, (28,), generator=g).tolist()
     q_lens = [512] * 4 + [1] * 28
     kv = [p + 512 for p in prior] + dctx
     cu = np.concatenate([[0], np.cumsum(q_lens)]).tolist()
-    p = _plan(cu, kv, hq=15, hkv=5, d=64)
+    p = _check_plan_cover(q_lens, kv, 15, 5, 64, torch.bfloat16, 0)
+    G, hkv = 3, 5
     wide = p.items_host[p.n_narrow:]
-    live = wide[wide[:, 3] > 0]
+    units = [wide[u:u + 4] for u in range(0, p.n_wide, 4)]
+    visible = {}
     for e in range(4):
-        tiles = (kv[e] + 15) // 16
-        starts = sorted({int(x) for x in live[live[:, 0] == e, 4]})
-        assert len(starts) == -(-tiles // 64)
-        lengths = np.diff(starts + [tiles])
-        # equal strides; the last one short by less than one tile per partition
-        assert len(set(lengths[:-1].tolist())) <= 1 and lengths[0] <= 64
-        assert 0 <= lengths[0] - lengths[-1] < len(lengths)
+        for qd in range(12):  # 96 column tiles, 8 per quad
+            last_row = (min((qd + 1) * 128, 512 * G) - 1) // G
+            visible[(e, qd)] = min((kv[e] + 15) // 16, (kv[e] - 512 + last_row) // 16 + 1)
+    W = hkv * sum(visible.values()) / 512
+    parts = {}
+    for u in units:
+        s, h, c0, _, k0, k1 = (int(x) for x in u[0][:6])
+        assert {(int(x[0]), int(x[1]), int(x[4]), int(x[5])) for x in u} == {(s, h, k0, k1)}
+        parts.setdefault((s, h, c0 // 8), []).append((k0, k1))
+    for (s, h, qd), ranges in parts.items():
+        ranges.sort()
+        v = visible[(s, qd)]
+        n = max(1, round(v / W))
+        assert ranges == [(i * v // n, (i + 1) * v // n) for i in range(n)], (s, h, qd, ranges)
+    assert 480 <= len(units) <= 544, len(units)
     assert _partition_of(p.items_host[: p.n_narrow]) == 32
-    # the same chunks with no decodes: one class, 32-tile partitions
+    # decode rows alone keep the estimate's own pick
+    alone = _plan(list(range(29)), dctx, hq=15, hkv=5, d=64)
+    assert _partition_of(alone.items_host[: alone.n_narrow]) == 16
+    # the same chunks with no decodes: one class, 32-tile partitions in equal strides
     pre = _plan(cu[:5], kv[:4], hq=15, hkv=5, d=64)
     live = pre.items_host[pre.items_host[:, 3] > 0]
     assert pre.n_narrow == 0 and int((live[:, 5] - live[:, 4]).max()) <= 32
     assert len({(int(r[0]), int(r[4])) for r in live}) == sum(-(-((c + 15) // 16) // 32) for c in kv[:4])
-    # decode rows alone keep the estimate's own pick
-    alone = _plan(list(range(29)), dctx, hq=15, hkv=5, d=64)
-    assert _partition_of(alone.items_host[: alone.n_narrow]) == 16
 
 
 @pytest.mark.parametrize("bs", [8, 16, 32])
