@@ -523,3 +523,45 @@ def test_operator_takes_slices_for_a_large_decode_batch(device, monkeypatch):
     _varlen.run_varlen(q[:2], small, pool, tables[:2], [0, 1], [c - 1 for c in ctx[:2]], None, hkv)
     assert seen == [True, False]
     assert float((small.float() - ref[:2].float()).abs().max()) <= 1e-2
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(40, 8, 128), (15, 5, 64), (32, 4, 64)])
+def test_mixed_step_quad_partitions_at_other_shapes(device, hq, hkv, d):
+    """Long prefill chunks on long priors beside decodes (one mixed launch):
+    the chunks' column quads take their own, split and merged, key
+    partitions. Sampled chunk rows (first, last, random) and every decode row
+    against the fp64 oracle, bf16."""
+    from memforge_amd import _native as nat
+
+    gen = torch.Generator().manual_seed(hq + d)
+    bs = 16
+    prefill = [(3000, 256), (700, 384), (0, 128)]   # (prior, chunk)
+    decodes = [int(x) for x in torch.randint(64, 6000, (20,), generator=gen)]
+    lengths = [p + c for p, c in prefill] + decodes
+    tables = random_tables(gen, sum((x + bs - 1) // bs for x in lengths) + 2, lengths, bs)
+    kp, vp = _pool(gen, max(max(t) for t in tables) + 1, bs, hkv, d, torch.bfloat16, device)
+    seq_ids, positions = [], []
+    for s, (p, c) in enumerate(prefill):
+        seq_ids += [s] * c
+        positions += list(range(p, p + c))
+    for i, c in enumerate(decodes):
+        seq_ids.append(len(prefill) + i)
+        positions.append(c - 1)
+    cu = [0]
+    for _, c in prefill:
+        cu.append(cu[-1] + c)
+    for _ in decodes:
+        cu.append(cu[-1] + 1)
+    plan = nat.plan_attention(cu, lengths, hq, hkv, d, torch.bfloat16, device)
+    assert plan.n_narrow and plan.n_wide and plan.n_merges  # one mixed launch, split quads merged
+    q = torch.randn((hq, len(seq_ids), d), generator=gen).to(torch.bfloat16).to(device)
+    got = to_np64(gpu_varlen(q, kp, vp, tables, seq_ids, positions))
+    rng = np.random.default_rng(d)
+    rows, start = [], 0
+    for _, c in prefill:
+        rows += sorted({start, start + c - 1} | set((start + rng.choice(c, 12, replace=False)).tolist()))
+        start += c
+    rows += list(range(start, len(seq_ids)))
+    want = oatt.varlen_attention(to_np64(q[:, rows]), to_np64(kp), to_np64(vp), tables,
+                                 [seq_ids[r] for r in rows], [positions[r] for r in rows], bs)
+    _check(got[:, rows], want, torch.bfloat16)

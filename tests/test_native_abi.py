@@ -147,6 +147,26 @@ def _wide_work(it, G):
     return max(0, min(kt1, last_pos // 16 + 1) - kt0)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_mixed_plans_of_random_shapes_cover_every_visible_tile_once(seed):
+    """Decode rows beside prefill chunks (one mixed launch, quad partitions
+    for the chunks): every key tile a column can see planned exactly once,
+    partial slots owned once and every merge record reading exactly its
+    column's slots, across GQA ratios, head sizes, dtypes, chunk lengths
+    (one column group up to many quads) and contexts up to 40,000 keys."""
+    rng = np.random.default_rng(100 + seed)
+    for hq, hkv, d, dtype in ((15, 5, 64, torch.bfloat16), (8, 2, 128, torch.bfloat16), (16, 4, 32, torch.float16),
+                              (8, 8, 64, torch.bfloat16), (32, 2, 64, torch.float16)):
+        chunks = [int(x) for x in rng.integers(2, 900, int(rng.integers(1, 6)))]
+        decodes = int(rng.integers(1, 40))
+        q_lens = chunks + [1] * decodes
+        kv = [q + int(x) for q, x in zip(chunks, rng.integers(0, 4000, len(chunks)))]
+        kv += [int(x) for x in rng.integers(1, 40000 if seed % 2 else 3000, decodes)]
+        order = rng.permutation(len(q_lens))
+        p = _check_plan_cover([q_lens[i] for i in order], [kv[i] for i in order], hq, hkv, d, dtype, 0)
+        assert p.n_narrow > 0
+
+
 @pytest.mark.parametrize("q_lens,kv", [
     ([40], [40]),                      # one short run: fewer workgroups than XCDs
     ([20, 33, 70], [20, 900, 3000]),   # pooled (loose) wide items beside shared runs
