@@ -326,7 +326,14 @@ int mf_paged_attention_noalloc(const void* q, int64_t q_stride_row, int64_t q_st
  * four or more column groups over one (sequence, kv head, key range) fills
  * whole workgroups, which then share each K/V tile through LDS (the last one
  * padded with items that have no column tiles and no partial slot); shorter
- * runs are packed four to a workgroup. counts receives
+ * runs are packed four to a workgroup. With partition_tiles 0 and both item
+ * kinds in the plan (one mixed launch), each such workgroup's four column
+ * groups (a column quad) take partitions of their own: the tiles the quad's
+ * last column can see, cut into equal ranges sized so that the wide
+ * workgroups carry about two per compute unit; tiles no column of the quad
+ * sees are not planned. The wide workgroups of one key range (in that case,
+ * of one sequence and kv head) are placed at grid positions of one residue
+ * mod 8, so they run on one XCD and share its L2. counts receives
  * [num_items_narrow, num_items_wide, num_merges, partials_floats].
  * A plan is valid for the dtype and head_dim it was made for and carries the
  * sequences' first rows, row counts and kv lengths: the cu_seqlens / kv_lens
