@@ -321,6 +321,38 @@ def upload_packed(parts: Sequence[np.ndarray], device) -> Tuple[torch.Tensor, Li
     return buf, offs
 
 
+# upload_packed_cached: device buffers by their exact contents, device and
+# stream, most recent last
+_UPLOAD_CACHE: "OrderedDict[tuple, Tuple[torch.Tensor, List[int]]]" = OrderedDict()
+UPLOAD_CACHE_SIZE = 64
+UPLOAD_CACHE_MAX_WORDS = 1 << 18  # 1 MiB: at most 64 MiB of device memory held
+
+
+def upload_packed_cached(parts: Sequence[np.ndarray], device) -> Tuple[torch.Tensor, List[int]]:
+    """``upload_packed`` that hands back the buffer an earlier call made from
+    the same bytes on the same device and stream (a model calling the
+    attention operator once per layer sends the same tables, plan and
+    positions for every layer of a step). The kernels only read these
+    buffers, so sharing one between launches on its stream is safe; the key
+    holds the stream, so no buffer is read on a stream its upload was not
+    ordered before."""
+    dev = torch.device(device)
+    arrs, offs, words = _layout(parts)
+    if words > UPLOAD_CACHE_MAX_WORDS:  # a large launch amortises its own upload
+        return upload_packed(arrs, dev)
+    key = (dev.type, dev.index, _stream(dev) if dev.type == "cuda" else 0,
+           tuple((a.dtype.str, a.shape) for a in arrs), b"".join(a.tobytes() for a in arrs))
+    hit = _UPLOAD_CACHE.get(key)
+    if hit is not None:
+        _UPLOAD_CACHE.move_to_end(key)
+        return hit
+    made = upload_packed(arrs, dev)
+    _UPLOAD_CACHE[key] = made
+    if len(_UPLOAD_CACHE) > UPLOAD_CACHE_SIZE:
+        _UPLOAD_CACHE.popitem(last=False)
+    return made
+
+
 def upload(parts: Sequence[np.ndarray], device) -> List[torch.Tensor]:
     """Move int32 / int64 host arrays to ``device`` with ONE host-to-device
     copy: they are packed into a pinned buffer (each part on an 8-byte

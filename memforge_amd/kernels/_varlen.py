@@ -81,8 +81,8 @@ def run_varlen(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: nat.PoolView,
     items, merges, counts, sliced = nat.plan_host(cu, kvl, hq, num_kv_heads, d, q_rows.dtype, dev,
                                                   decode_slices=sliceable)
     # tables, plan, cu/kv lengths, positions, row map and pool lengths cross
-    # to the device in one copy, and the launch addresses them inside that
-    # one buffer
+    # to the device in one copy (none when the same bytes crossed before on
+    # this stream), and the launch addresses them inside that one buffer
     tables_host = padded_tables_host([tables[s] for s in order])
     parts = [tables_host, *nat.plan_upload_parts(items, merges),
              np.asarray(cu + kvl, dtype=np.int32), np.asarray(list(positions), dtype=np.int64)]
@@ -90,7 +90,7 @@ def run_varlen(q_rows: torch.Tensor, out_rows: torch.Tensor, pool: nat.PoolView,
         parts.append(np.asarray(row_map, dtype=np.int32))
     if pool_lens is not None:
         parts.append(np.asarray([pool_lens[s] for s in order], dtype=np.int32))
-    buf, offsets = nat.upload_packed(parts, dev)
+    buf, offsets = nat.upload_packed_cached(parts, dev)
     nat.paged_attention_packed(
         q_rows, out_rows, pool, buf, offsets, len(order), tables_host.shape[1], counts,
         scale if scale is not None else 1.0 / math.sqrt(d), num_kv_heads,

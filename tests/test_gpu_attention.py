@@ -565,3 +565,45 @@ def test_mixed_step_quad_partitions_at_other_shapes(device, hq, hkv, d):
     want = oatt.varlen_attention(to_np64(q[:, rows]), to_np64(kp), to_np64(vp), tables,
                                  [seq_ids[r] for r in rows], [positions[r] for r in rows], bs)
     _check(got[:, rows], want, torch.bfloat16)
+
+
+def test_repeated_calls_reuse_only_identical_index_buffers(device):
+    """run_varlen keeps uploaded index buffers (tables, plan, lengths,
+    positions) by their exact bytes, device and stream. A repeated call gives
+    the same output; a call whose table, context or stream differs gets its
+    own buffer and its own result, each against the fp64 oracle."""
+    from memforge_amd import _native as nat
+    from memforge_amd.kernels import _varlen
+
+    gen = torch.Generator().manual_seed(11)
+    bs, hq, hkv, d = 16, 15, 5, 64
+    kp, vp = _pool(gen, 64, bs, hkv, d, torch.float32, device)
+    pool = nat.PoolView.from_bshd(kp, vp)
+    q = torch.randn((3, hq, d), generator=gen).to(device)
+    table = list(range(10, 30))
+
+    def run(tab, ctx, stream=None):
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
+            out = torch.full_like(q, float("nan"))
+            _varlen.run_varlen(q, out, pool, [tab], [0, 0, 0], [ctx - 3, ctx - 2, ctx - 1], None, hkv,
+                               kv_lens=[ctx])
+        torch.cuda.synchronize()
+        want = oatt.varlen_attention(to_np64(q.permute(1, 0, 2)), to_np64(kp), to_np64(vp), [tab], [0, 0, 0],
+                                     [ctx - 3, ctx - 2, ctx - 1], bs)
+        _check(to_np64(out.permute(1, 0, 2)), want, torch.float32)
+        return out
+
+    nat._UPLOAD_CACHE.clear()
+    a = run(table, 300)
+    b = run(table, 300)
+    assert torch.equal(a, b) and len(nat._UPLOAD_CACHE) == 1
+    other = list(table)
+    other[5] = 50  # one block id differs: another buffer, another result
+    c = run(other, 300)
+    assert len(nat._UPLOAD_CACHE) == 2 and not torch.equal(a, c)
+    run(table, 301)
+    assert len(nat._UPLOAD_CACHE) == 3
+    side = torch.cuda.Stream()
+    run(table, 300, side)
+    assert len(nat._UPLOAD_CACHE) == 4
