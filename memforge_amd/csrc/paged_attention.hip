@@ -1365,6 +1365,25 @@ void attn_kernel(AttnArgs a) {
     }
 }
 
+// In a mixed launch the single-tile (decode) waves start their loads after a
+// short sleep, about the time the dispatcher takes to hand out the launch's
+// workgroups. Per-workgroup timestamps of the C2 launch showed a prefill
+// workgroup beside a decode workgroup spend 14.6 us (median) from its start
+// to its first staged tile, against 6.1 us on a CU without one: its setup
+// loads (block table, Q, the first K/V stages) queued behind the decode
+// waves' streams, while the decode workgroups themselves finished at 14 us
+// and the prefill ones at 34-41 us. With the decode waves held back by one
+// s_sleep(32) (2,048 cycles) the prefill setup loads go out first: C2 engine
+// layer 43.0-43.6 us against 44.6-45.1 (graph replays, alternating builds);
+// two to four sleeps gave 43.3-44.1, six 44.9-45.1, nine 46.0-46.4.
+#ifndef MF_MIXED_NARROW_SLEEPS
+#define MF_MIXED_NARROW_SLEEPS 1
+#endif
+__device__ __forceinline__ void narrow_start_delay() {
+#pragma unroll
+    for (int i = 0; i < MF_MIXED_NARROW_SLEEPS; ++i) __builtin_amdgcn_s_sleep(32);
+}
+
 // Single-tile and wide items of one plan in one launch: the first
 // workgroups run the single-tile items (decode rows: chains of dependent
 // loads, latency-bound), the last `wide_blocks` the wide ones (prefill rows:
@@ -1394,8 +1413,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(mixed_waves
 void attn_mixed_kernel(AttnArgs narrow, AttnArgs wide, int wide_blocks) {
     const int b = blockIdx.x;
     const int narrow_blocks = (int)gridDim.x - wide_blocks;
-    if (b < narrow_blocks) attn_body<DT, DP, 1, true>(narrow, b);
-    else attn_body<DT, DP, NTW, true>(wide, b - narrow_blocks);
+    if (b < narrow_blocks) {
+        narrow_start_delay();
+        attn_body<DT, DP, 1, true>(narrow, b);
+    } else {
+        attn_body<DT, DP, NTW, true>(wide, b - narrow_blocks);
+    }
 }
 
 // The written-in-flight form: the copy workgroups first, then the narrow and
@@ -1410,6 +1433,7 @@ void attn_mixed_tail_kernel(AttnArgs a, const int32_t* wide_items, int wide_num_
     if (b < 0) {
         write_new_rows<DT>(a, blockIdx.x);
     } else if (b < narrow_blocks) {
+        narrow_start_delay();
         attn_body<DT, DP, 1, true, true>(a, b);
     } else {
         AttnArgs w = a;
