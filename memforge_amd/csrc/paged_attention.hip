@@ -724,13 +724,28 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     bool wg_shared = false;
     if constexpr (FAST && DT != MF_F32 && NT > 1) {
         if ((block + 1) * kWaves <= num_items) {
+            // The four items' (sequence, kv head, key range) are loaded
+            // together and compared without short-circuit: chained && made
+            // the compiler issue one load per comparison, each behind a full
+            // wait -- twelve round trips before the first K/V fetch, which
+            // beside a decode workgroup's streams took 12.7 us of a prefill
+            // workgroup's setup (4.0 us alone).
             const int32_t* i0 = a.items + (int64_t)block * kWaves * MF_PLAN_ITEM_INTS;
-            wg_shared = true;
+            int32_t key[kWaves][4];
 #pragma unroll
-            for (int w = 1; w < kWaves; ++w) {
+            for (int w = 0; w < kWaves; ++w) {
                 const int32_t* iw = i0 + w * MF_PLAN_ITEM_INTS;
-                wg_shared = wg_shared && iw[0] == i0[0] && iw[1] == i0[1] && iw[4] == i0[4] && iw[5] == i0[5];
+                key[w][0] = iw[0];
+                key[w][1] = iw[1];
+                key[w][2] = iw[4];
+                key[w][3] = iw[5];
             }
+            bool same = true;
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w)
+                same = same & (key[w][0] == key[0][0]) & (key[w][1] == key[0][1]) & (key[w][2] == key[0][2]) &
+                       (key[w][3] == key[0][3]);
+            wg_shared = same;
         }
     }
     const bool shared_inflight = TAIL && wg_shared;
@@ -2138,11 +2153,45 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
             for (int qd = 0, nq = quads(s); qd < nq; ++qd) visible += (int64_t)Hkv * quad_visible(s, qd);
         quad_w = std::max((double)std::max(PW, 1), (double)visible / (2.0 * kPlanCUs));
     }
-    auto quad_parts = [&](int s, int qd) {
-        const int v = quad_visible(s, qd);
-        const int n = std::max(1, (int)std::lround(v / quad_w));
-        return std::max(n, (v + mf::kMaxItemTiles - 1) / mf::kMaxItemTiles);
-    };
+    // Partition counts per (sequence, quad), then at most two wide
+    // workgroups per CU: rounding can leave a few more, and with every CU
+    // holding two, those few land as a third on some CU, which then finishes
+    // last. Partitions are merged, one at a time, in the quad whose ranges
+    // grow the least. C2: 530 -> 510 workgroups, engine layer 42.1-42.3 us
+    // against 42.7-42.9.
+    std::vector<std::vector<int>> qparts(num_seqs);
+    if (mixed) {
+        int64_t total = 0;
+        for (int s = 0; s < num_seqs; ++s) {
+            const int nq = quads(s);
+            qparts[s].resize(nq);
+            for (int qd = 0; qd < nq; ++qd) {
+                const int v = quad_visible(s, qd);
+                const int n = std::max(1, (int)std::lround(v / quad_w));
+                qparts[s][qd] = std::max(n, (v + mf::kMaxItemTiles - 1) / mf::kMaxItemTiles);
+                total += (int64_t)Hkv * qparts[s][qd];
+            }
+        }
+        while (total > 2 * kPlanCUs) {
+            int bs = -1, bq = -1;
+            double best = 1e300;
+            for (int s = 0; s < num_seqs; ++s)
+                for (int qd = 0; qd < (int)qparts[s].size(); ++qd) {
+                    const int n = qparts[s][qd], v = quad_visible(s, qd);
+                    if (n <= 1 || (v + n - 2) / (n - 1) > mf::kMaxItemTiles) continue;
+                    const double grown = (double)v / (n - 1);
+                    if (grown < best) {
+                        best = grown;
+                        bs = s;
+                        bq = qd;
+                    }
+                }
+            if (bs < 0) break;  // every quad is down to one range (or at the item limit)
+            --qparts[bs][bq];
+            total -= Hkv;
+        }
+    }
+    auto quad_parts = [&](int s, int qd) { return qparts[s][qd]; };
 
     // First walk: sizes only.
     int64_t n_single = 0, n_coop = 0, n_wide = 0, n_loose = 0, n_merges = 0, n_slots = 0;

@@ -397,8 +397,9 @@ def test_planner_mixed_step_partitions_on_the_c2_shape():
     both classes share one launch. Each column quad (the four column groups
     of one wide workgroup) cuts the tiles its last column sees into
     round(visible / W) equal ranges, W = the visible work over 2 x 256 compute
-    units: every wide workgroup holds about the same work, about 512 of
-    them."""
+    units, and partitions are merged until at most 512 wide workgroups (two
+    per compute unit) remain: every wide workgroup holds about the same
+    work."""
     g = torch.Generator().manual_seed(0)
     prior = torch.randint(0, 2049, (4,), generator=g).tolist()
     dctx = torch.randint(64, 4097, (28,), generator=g).tolist()
@@ -420,12 +421,21 @@ def test_planner_mixed_step_partitions_on_the_c2_shape():
         s, h, c0, _, k0, k1 = (int(x) for x in u[0][:6])
         assert {(int(x[0]), int(x[1]), int(x[4]), int(x[5])) for x in u} == {(s, h, k0, k1)}
         parts.setdefault((s, h, c0 // 8), []).append((k0, k1))
+    counts = {}
     for (s, h, qd), ranges in parts.items():
         ranges.sort()
         v = visible[(s, qd)]
-        n = max(1, round(v / W))
+        n = len(ranges)
+        # equal ranges; round(visible / W) of them, or fewer where the cap
+        # below merged partitions
         assert ranges == [(i * v // n, (i + 1) * v // n) for i in range(n)], (s, h, qd, ranges)
-    assert 480 <= len(units) <= 544, len(units)
+        assert 1 <= n <= max(1, round(v / W)), (s, qd, n, v / W)
+        counts[(s, qd)] = n
+    # every kv head of a quad is cut alike; at most two wide workgroups per CU
+    assert len(parts) == hkv * len(counts)
+    assert len(units) <= 512 and len(units) == hkv * sum(counts.values())
+    merged = sum(max(1, round(v / W)) for v in visible.values()) - sum(counts.values())
+    assert 0 < merged <= 5 and len(units) > 512 - hkv, (merged, len(units))
     assert _partition_of(p.items_host[: p.n_narrow]) == 32
     # decode rows alone keep the estimate's own pick
     alone = _plan(list(range(29)), dctx, hq=15, hkv=5, d=64)
