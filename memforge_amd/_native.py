@@ -312,9 +312,21 @@ def _pack_host(parts: Sequence[np.ndarray], pinned: bool) -> Tuple[torch.Tensor,
     return host, arrs, offs
 
 
+def _refuse_capture(device: torch.device) -> None:
+    """Uploads stage through a temporary pinned buffer that a captured copy
+    would read again on every replay, after torch's host allocator has handed
+    it out again; torch's pinned allocation is not permitted under capture
+    anyway. Captured steps stage through buffers of their own
+    (GraphedPagedDecoder, CountedPlan)."""
+    if device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+        raise MemforgeHipError("host arrays cannot be uploaded under graph capture: stage them through "
+                               "persistent buffers (GraphedPagedDecoder, CountedPlan) and capture those")
+
+
 def upload_packed(parts: Sequence[np.ndarray], device) -> Tuple[torch.Tensor, List[int]]:
     """``upload`` without the per-part views: the device int32 buffer and each
     part's word offset in it (for callers that pass addresses to the C ABI)."""
+    _refuse_capture(torch.device(device))
     host, _, offs = _pack_host(parts, True)
     buf = torch.empty(host.numel(), dtype=torch.int32, device=device)
     buf.copy_(host, non_blocking=True)
@@ -335,9 +347,10 @@ def upload_packed_cached(parts: Sequence[np.ndarray], device) -> Tuple[torch.Ten
     positions for every layer of a step). The kernels only read these
     buffers, so sharing one between launches on its stream is safe; the key
     holds the stream, so no buffer is read on a stream its upload was not
-    ordered before."""
+    ordered before. Refused under graph capture, like every upload."""
     dev = torch.device(device)
     arrs, offs, words = _layout(parts)
+    _refuse_capture(dev)  # a cached buffer could be evicted while a graph still replays
     if words > UPLOAD_CACHE_MAX_WORDS:  # a large launch amortises its own upload
         return upload_packed(arrs, dev)
     key = (dev.type, dev.index, _stream(dev) if dev.type == "cuda" else 0,
@@ -362,6 +375,7 @@ def upload(parts: Sequence[np.ndarray], device) -> List[torch.Tensor]:
     hand it out again before the copy has completed, so the host never waits
     for the GPU here."""
     dev = torch.device(device)
+    _refuse_capture(dev)
     pinned = dev.type == "cuda"
     host, arrs, offs = _pack_host(parts, pinned)
     if not pinned:

@@ -607,3 +607,4 @@ def test_repeated_calls_reuse_only_identical_index_buffers(device):
     side = torch.cuda.Stream()
     run(table, 300, side)
     assert len(nat._UPLOAD_CACHE) == 4
+

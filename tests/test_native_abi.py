@@ -584,3 +584,17 @@ def test_plan_host_cache_returns_read_only_plans_and_stays_bounded():
     for n in range(nat.PLAN_CACHE_SIZE + 10):
         nat.plan_host([0, 1], [17 + n], 8, 2, 64, torch.float32, "cpu")
     assert len(nat._PLAN_CACHE) == nat.PLAN_CACHE_SIZE
+
+
+def test_uploads_refuse_graph_capture(monkeypatch):
+    """Host-array uploads stage through a temporary pinned buffer, which a
+    captured copy would read again on every replay: under capture they raise
+    before any allocation (captured steps stage through buffers of their own)."""
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    parts = [np.arange(4, dtype=np.int32)]
+    for call in (lambda: nat.upload(parts, "cuda"), lambda: nat.upload_packed(parts, "cuda"),
+                 lambda: nat.upload_packed_cached(parts, "cuda")):
+        with pytest.raises(nat.MemforgeHipError, match="graph capture"):
+            call()
+    # a CPU destination is never captured
+    assert nat.upload(parts, "cpu")[0].tolist() == [0, 1, 2, 3]
