@@ -606,7 +606,12 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // Per-key loads of tile kt (the verify boundary and in-flight tiles, and
     // every tile off the fast path). On the fast path a tile's pool keys all
     // lie in one block, whose entry is already in tbl.
-    auto load_general = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
+    // has_map: the launch has a row map (a compile-time copy of each case:
+    // with the map read behind a runtime test, the five row lookups below
+    // each ended in a wait for every load in flight, row map or not -- on a
+    // verify pass the boundary tile's wave then started its key loop 2.3 us
+    // after the others and held up its cooperative unit)
+    auto load_general_m = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD], auto has_map) {
         int phys = 0;
         if constexpr (FAST) phys = kt < tbl_end ? tbl_at(kt - tbl_base) : 0;
         auto row = [&](const char* pool, const char* inflight, int key) -> const char* {
@@ -615,7 +620,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                 if (key < pool_len)
                     return pool + ((int64_t)phys * a.p_sb + (int64_t)(key & 15) * a.p_ss + (int64_t)h * a.p_sh) * ES;
                 int nr = row0 + (key - pool_len);
-                if (a.row_map) nr = a.row_map[nr];
+                if constexpr (decltype(has_map)::value) nr = a.row_map[nr];
                 return inflight + ((int64_t)nr * a.n_sr + (int64_t)h * a.n_sh) * ES;
             } else {
                 return key_row(pool, inflight, key);
@@ -637,6 +642,10 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                 for (int w = 0; w < VWD; ++w) vf[r][w] = 0;
             }
         }
+    };
+    auto load_general = [&](int kt, uint4 (&kf)[NL], uint32_t (&vf)[4][VWD]) {
+        if (FAST && a.row_map) load_general_m(kt, kf, vf, std::true_type{});
+        else load_general_m(kt, kf, vf, std::false_type{});
     };
     // Lane byte offsets of the V rows 4g..4g+3 inside a block, computed once.
     uint32_t v_off[4];
