@@ -608,3 +608,47 @@ def test_repeated_calls_reuse_only_identical_index_buffers(device):
     run(table, 300, side)
     assert len(nat._UPLOAD_CACHE) == 4
 
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_verify_pass_without_a_row_map(device, dtype):
+    """A verify pass (lookahead + 1 rows per sequence, candidates attended in
+    flight) launched without a row map, as the engine's binding launches it:
+    against the fp64 oracle, and bit-identical to the same launch with an
+    identity row map (the boundary tile's loads take the other code path)."""
+    from memforge_amd import _native as nat
+
+    dt = DT[dtype]
+    gen = torch.Generator().manual_seed(21)
+    bs, hq, hkv, d, B, K = 16, 15, 5, 64, 16, 4
+    ctx = torch.randint(100, 1200, (B,), generator=gen).tolist()
+    kvl = [c + K + 1 for c in ctx]
+    tables = random_tables(gen, sum((c + bs - 1) // bs for c in kvl) + 2, kvl, bs)
+    kp, vp = _pool(gen, max(max(t) for t in tables) + 1, bs, hkv, d, dt, device)
+    T = B * (K + 1)
+    q = torch.randn((T, hq, d), generator=gen).to(dt).to(device)
+    nk = torch.randn((T, hkv, d), generator=gen).to(dt).to(device)
+    nv = torch.randn((T, hkv, d), generator=gen).to(dt).to(device)
+    cu = [b * (K + 1) for b in range(B + 1)]
+    positions = [c + j for c in ctx for j in range(K + 1)]
+    seq_ids = [b for b in range(B) for _ in range(K + 1)]
+    bt = torch.zeros((B, max(len(t) for t in tables)), dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    bt = bt.to(device)
+    plan = nat.plan_attention(cu, kvl, hq, hkv, d, dt, device)
+    pool = nat.PoolView.from_bshd(kp, vp)
+    args = (pool, bt, torch.tensor(cu, dtype=torch.int32, device=device),
+            torch.tensor(kvl, dtype=torch.int32, device=device),
+            torch.tensor(positions, dtype=torch.int64, device=device), plan, 1.0 / math.sqrt(d), hkv)
+    pl = torch.tensor(ctx, dtype=torch.int32, device=device)
+    plain = torch.full_like(q, float("nan"))
+    nat.paged_attention(q, plain, *args, pool_lens=pl, new_k_rows=nk, new_v_rows=nv)
+    mapped = torch.full_like(q, float("nan"))
+    nat.paged_attention(q, mapped, *args, row_map=torch.arange(T, dtype=torch.int32, device=device),
+                        pool_lens=pl, new_k_rows=nk, new_v_rows=nv)
+    torch.cuda.synchronize()
+    assert torch.equal(plain, mapped)
+    want = oatt.varlen_attention(to_np64(q.permute(1, 0, 2)), to_np64(kp), to_np64(vp), tables, seq_ids, positions,
+                                 bs, pool_lens=ctx, new_k=to_np64(nk), new_v=to_np64(nv),
+                                 new_rows=[list(range(cu[b], cu[b + 1])) for b in range(B)])
+    _check(to_np64(plain.permute(1, 0, 2)), want, dt)
