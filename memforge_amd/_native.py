@@ -139,7 +139,7 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 def require_device(*tensors: Optional[torch.Tensor]) -> None:
     for t in tensors:
-        if t is not None and t.device.type != "cuda":
+        if t is not None and not t.is_cuda:
             raise ValueError(
                 f"memforge_amd runs on the GPU; got a tensor on {t.device} "
                 "(there is no CPU path)"
@@ -612,10 +612,11 @@ class Workspace:
             self._partials[key] = buf
         return buf
 
-    def verify(self, nbytes: int, device) -> torch.Tensor:
-        """mf_spec_verify's scratch, kept between calls."""
-        dev = torch.device(device)
-        key = (dev.index, _stream(dev))
+    def verify(self, nbytes: int, device, stream: Optional[int] = None) -> torch.Tensor:
+        """mf_spec_verify's scratch, kept between calls (``stream``: the raw
+        handle of the device's current stream, when the caller has it)."""
+        dev = device if isinstance(device, torch.device) else torch.device(device)
+        key = (dev.index, _stream(dev) if stream is None else stream)
         buf = self._verify.get(key)
         if buf is None or buf.numel() < nbytes:
             buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
@@ -1041,30 +1042,35 @@ def spec_verify(draft_tokens: torch.Tensor, draft_probs: torch.Tensor, target_lo
         raise ValueError(f"target logits {tuple(target_logits.shape)} do not cover ({B}, {K + 1}, {V})")
     if target_logits.stride(-1) != 1 or draft_probs.stride(-1) != 1 or exp_noise.stride(-1) != 1:
         raise ValueError("vocabulary axes must be contiguous")
-    draft_tokens = draft_tokens.to(torch.int32).contiguous()
-    u_accept = u_accept.to(torch.float32).contiguous()
+    if draft_tokens.dtype != torch.int32 or not draft_tokens.is_contiguous():
+        draft_tokens = draft_tokens.to(torch.int32).contiguous()
+    if u_accept.dtype != torch.float32 or not u_accept.is_contiguous():
+        u_accept = u_accept.to(torch.float32).contiguous()
     dev = target_logits.device
     # one allocation for the four outputs (only the first count[b] entries of
-    # each row are written); is_draft is bytes of its int32 tail
+    # each row are written); is_draft is bytes of its int32 tail. The kernels
+    # are queued first and the views built after, so no view is made on the
+    # way to the launch.
     n = B * (K + 1)
     out = torch.empty(n + 2 * B + (n + 3) // 4, dtype=torch.int32, device=dev)
-    res = VerifyResult(
+    base = out.data_ptr()
+    L = lib()
+    ws_bytes = _VERIFY_WS_BYTES.get((B, K))
+    if ws_bytes is None:
+        ws_bytes = _VERIFY_WS_BYTES[(B, K)] = int(L.mf_spec_verify_workspace_size(B, K))
+    stream = _stream(dev)
+    ws = _WORKSPACE.verify(ws_bytes, dev, stream)
+    _check(L.mf_spec_verify(
+        B, K, V, draft_tokens.data_ptr(), draft_probs.data_ptr(),
+        draft_probs.stride(0) if K > 0 else 0, draft_probs.stride(1) if K > 0 else 0,
+        target_logits.data_ptr(), dtype_code(target_logits.dtype), target_logits.stride(0),
+        target_logits.stride(1), float(temperature), int(bool(target_is_probs)), u_accept.data_ptr(),
+        exp_noise.data_ptr(), exp_noise.stride(0), base, base + 4 * (n + 2 * B), base + 4 * n,
+        base + 4 * (n + B), ws.data_ptr(), ws_bytes, stream,
+    ), "mf_spec_verify")
+    return VerifyResult(
         tokens=out[:n].view(B, K + 1),
         is_draft=out[n + 2 * B:].view(torch.uint8)[:n].view(B, K + 1),
         count=out[n:n + B],
         num_accepted=out[n + B:n + 2 * B],
     )
-    L = lib()
-    ws_bytes = _VERIFY_WS_BYTES.get((B, K))
-    if ws_bytes is None:
-        ws_bytes = _VERIFY_WS_BYTES[(B, K)] = int(L.mf_spec_verify_workspace_size(B, K))
-    ws = _WORKSPACE.verify(ws_bytes, dev)
-    _check(L.mf_spec_verify(
-        B, K, V, _ptr(draft_tokens), _ptr(draft_probs),
-        draft_probs.stride(0) if K > 0 else 0, draft_probs.stride(1) if K > 0 else 0,
-        _ptr(target_logits), dtype_code(target_logits.dtype), target_logits.stride(0),
-        target_logits.stride(1), float(temperature), int(bool(target_is_probs)), _ptr(u_accept), _ptr(exp_noise),
-        exp_noise.stride(0), _ptr(res.tokens), _ptr(res.is_draft), _ptr(res.count),
-        _ptr(res.num_accepted), _ptr(ws), ws_bytes, _stream(),
-    ), "mf_spec_verify")
-    return res

@@ -195,3 +195,14 @@ def test_repeated_calls_on_one_workspace_and_a_large_batch(device):
         assert (count == first[0]).all() and (nacc == first[1]).all()
     draft, target, tokens, u, noise = _inputs(22, 1100, 2, 96, agree=0.5)
     _run_both(device, draft, target, tokens, u, noise, 0.9)
+
+
+@pytest.mark.parametrize("V", [65537, 131080])
+def test_vocabularies_past_one_batch_of_chunk_statistics(device, V):
+    """Vocabularies over 8 x 8,192 entries: the accept walk combines each
+    position's chunk statistics over several batches of loads (the batch past
+    the last chunk clamped and masked). A round that rejects and one that
+    accepts every candidate both match the oracle."""
+    for agree, seed in ((0.0, 31), (1.0, 32)):
+        draft, target, tokens, u, noise = _inputs(seed, 3, 3, V, agree=agree)
+        _run_both(device, draft, target, tokens, u, noise, 1.0)
