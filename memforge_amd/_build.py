@@ -34,6 +34,13 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # a kernel's leading scalar / pointer arguments (up to two) arrive in
+    # scalar registers instead of being loaded from the argument block: the
+    # attention and merge kernels take their work lists first so the first
+    # load of a wave does not wait on that block (LLVM's AMDGPU kernel
+    # argument preloading; the code object keeps a load path for firmware
+    # that does not preload)
+    "-mllvm", "-amdgpu-kernarg-preload-count=2",
 ]
 
 

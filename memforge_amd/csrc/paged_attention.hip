@@ -488,26 +488,47 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int item = block * kWaves + wave;
-    const int num_items = a.dev_count ? *a.dev_count : a.num_items;
-    if (item >= num_items) return;
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4;  // 16-lane group: MFMA k-group / output row group
-    const int j = lane & 15;  // MFMA column (query column) and A-row (key) index
-
     // The item carries its sequence's first row, row count and kv length (the
     // planner's copies of cu_seqlens / kv_lens), so nothing waits on loading
     // them before the row positions and block table are fetched.
     const int32_t* it = a.items + (int64_t)item * MF_PLAN_ITEM_INTS;
-    const int s = it[0], h = it[1], c0 = it[2], nct = it[3];
-    const int kt0 = it[4], kt1 = it[5], pslot = it[6];
-    const int row0 = it[8];
-    const int ncols = it[9] * a.G;
-    const int kv_len = it[10];
+    int4 iv0, iv1, iv2;
+    if constexpr (NT == 1) {
+        // Single-tile items load their item before the count check, together
+        // with the argument block that the check reads (the item list's
+        // address needs no argument load when it is preloaded), instead of
+        // one round trip after it. The item is in bounds past the live count:
+        // plans fill whole workgroups and counted launches size the list by
+        // its capacity. The empty asm keeps the loads ahead of the check.
+        // Wide items keep the order below: their setup issues the item with
+        // the workgroup's other items' keys in one batch after the check.
+        iv0 = *(const int4*)it;
+        iv1 = *(const int4*)(it + 4);
+        iv2 = *(const int4*)(it + 8);
+        asm volatile("" ::"s"(iv0.x), "s"(iv0.y), "s"(iv0.z), "s"(iv0.w), "s"(iv1.x), "s"(iv1.y), "s"(iv1.z),
+                     "s"(iv1.w), "s"(iv2.x), "s"(iv2.y), "s"(iv2.z), "s"(iv2.w));
+    }
+    const int num_items = a.dev_count ? *a.dev_count : a.num_items;
+    if (item >= num_items) return;
+    if constexpr (NT != 1) {
+        iv0 = make_int4(it[0], it[1], it[2], it[3]);
+        iv1 = make_int4(it[4], it[5], it[6], it[7]);
+        iv2 = make_int4(it[8], it[9], it[10], it[11]);
+    }
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;  // 16-lane group: MFMA k-group / output row group
+    const int j = lane & 15;  // MFMA column (query column) and A-row (key) index
+
+    const int s = iv0.x, h = iv0.y, c0 = iv0.z, nct = iv0.w;
+    const int kt0 = iv1.x, kt1 = iv1.y, pslot = iv1.z;
+    const int row0 = iv2.x;
+    const int ncols = iv2.y * a.G;
+    const int kv_len = iv2.z;
     // Keys below pool_len are in the pool; the rest are in-flight rows of the
     // sequence's own new tokens (a verify pass: pool_lens; a written-in-flight
     // step: everything past the keys before the sequence's rows).
     const bool inflight = TAIL || a.pool_lens != nullptr;
-    const int pool_len = TAIL ? kv_len - it[9] : (a.pool_lens != nullptr ? a.pool_lens[s] : kv_len);
+    const int pool_len = TAIL ? kv_len - iv2.y : (a.pool_lens != nullptr ? a.pool_lens[s] : kv_len);
     const int D = a.head_dim;
 
     // The loads that need nothing but the item go out together -- block-table
@@ -1251,7 +1272,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // the elements with r == w across the four waves and stores them -- the
     // normalised output, or one partial of a longer split.
     if constexpr (NT == 1) {
-        if (it[11] != 0) {  // the planner flags all four items of a cooperative workgroup
+        if (iv2.w != 0) {  // the planner flags all four items of a cooperative workgroup
             static_assert(coop_lds_bytes<DP>() == (kWaves * 4 * VCH * 64 + 2 * kWaves * 16) * 4, "LDS arena layout");
             auto s_acc = reinterpret_cast<float (*)[4 * VCH][64]>(attn_lds);
             auto s_m = reinterpret_cast<float (*)[16]>(attn_lds + kWaves * 4 * VCH * 64 * 4);
@@ -1306,7 +1327,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                 __threadfence();
                 __syncthreads();
                 if (wave == 0) {
-                    const int m0 = it[7];
+                    const int m0 = iv1.w;
                     int prev = 0;
                     if (lane == 0) prev = atomicAdd(a.counters + m0, 1);
                     prev = __shfl(prev, 0, 64);
@@ -1361,7 +1382,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     // arrival acquire everyone else's partials and reset the counter for the
     // next call. Every wave runs to the end; nothing waits on another wave.
     if (pslot >= 0 && a.counters != nullptr) {
-        const int m0 = it[7];
+        const int m0 = iv1.w;
         __threadfence();
         int prev = 0;
         if (lane == 0) prev = atomicAdd(a.counters + m0, 1);
@@ -1375,9 +1396,13 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
     }
 }
 
+// The item list comes as a separate first argument, which the build has the
+// hardware preload into scalar registers: a wave's first item load then
+// needs no load of the argument block (see attn_body).
 template <int DT, int DP, int NT, bool FAST, bool TAIL = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<DT, DP, NT>())))
-void attn_kernel(AttnArgs a) {
+void attn_kernel(const int32_t* items, AttnArgs a) {
+    a.items = items;
     if constexpr (TAIL) {
         // the copy workgroups first (measured on the C2 step: 53.7 us per
         // layer against 55.7 with them last)
@@ -1752,21 +1777,36 @@ void attn_slice_kernel(AttnArgs a, int num_slices, int hkv) {
 }
 
 // --------------------------------------------------------------- merge kernel
+// A merge launch's record mi, loaded before its count check (record
+// min(mi, num_merges - 1): in bounds for every workgroup of the grid), so the
+// load goes out with the argument block's instead of one round trip after it;
+// the record list's address and num_merges are the preloaded first arguments.
+// The empty asm keeps the loads ahead of the check.
+__device__ __forceinline__ void load_merge_record(const int32_t* merges, int mi, int num_merges,
+                                                  int32_t (&mg)[MF_PLAN_MERGE_INTS]) {
+    const int32_t* rec = merges + (int64_t)min(mi, num_merges - 1) * MF_PLAN_MERGE_INTS;
+    const int4 r0 = *(const int4*)rec, r1 = *(const int4*)(rec + 4);
+    asm volatile("" ::"s"(r0.x), "s"(r0.y), "s"(r0.z), "s"(r0.w), "s"(r1.x), "s"(r1.y), "s"(r1.z), "s"(r1.w));
+    mg[0] = r0.x; mg[1] = r0.y; mg[2] = r0.z; mg[3] = r0.w;
+    mg[4] = r1.x; mg[5] = r1.y; mg[6] = r1.z; mg[7] = r1.w;
+}
+
 // One workgroup per merge record: wave w merges partitions w, w+4, ... and the
 // four partial results are combined through LDS by wave 0.
 template <int DT, int DP>
-__global__ __launch_bounds__(256) void merge_kernel(AttnArgs a, const int32_t* merges, int num_merges) {
+__global__ __launch_bounds__(256) void merge_kernel(const int32_t* merges, int num_merges, AttnArgs a) {
     constexpr int VCH = DP / 16;
     constexpr int ES = DT == MF_F32 ? 4 : 2;
     constexpr float kNegInf = -__builtin_huge_valf();
     __shared__ float s_m[kWaves][16], s_l[kWaves][16];
     __shared__ float s_o[kWaves][16][DP];
     const int mi = blockIdx.x;
+    int32_t mg[MF_PLAN_MERGE_INTS];
+    load_merge_record(merges, mi, num_merges, mg);
     if (mi >= (a.dev_count ? *a.dev_count : num_merges)) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15;
-    const int32_t* mg = merges + (int64_t)mi * MF_PLAN_MERGE_INTS;
     int prow = 0, qhead = 0;
     const int dbase = 4 * g * VCH;
     const bool active = merge_column(a, mg, j, prow, qhead) && dbase < a.head_dim;
@@ -1806,12 +1846,14 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnArgs a, const int32_t* m
 // record's partitions four at a time (merge_range) and writes the output
 // directly, with no LDS combine or barrier.
 template <int DT, int DP>
-__global__ __launch_bounds__(256) void merge_wave_kernel(AttnArgs a, const int32_t* merges, int num_merges) {
+__global__ __launch_bounds__(256) void merge_wave_kernel(const int32_t* merges, int num_merges, AttnArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int mi = blockIdx.x * kWaves + wave;
+    int32_t mg[MF_PLAN_MERGE_INTS];
+    load_merge_record(merges, mi, num_merges, mg);
     if (mi >= (a.dev_count ? *a.dev_count : num_merges)) return;
     const int lane = threadIdx.x & 63;
-    merge_tile<DT, DP>(a, merges + (int64_t)mi * MF_PLAN_MERGE_INTS, lane >> 4, lane & 15);
+    merge_tile<DT, DP>(a, mg, lane >> 4, lane & 15);
 }
 
 // The split-K merge launch: one wave per record for large launches, one
@@ -1820,10 +1862,10 @@ template <int DT, int DP>
 int launch_merge(const AttnArgs& a, const int32_t* merges, int64_t n_merges, hipStream_t stream) {
     if (n_merges >= MF_MERGE_WAVE_MIN) {
         const dim3 grid((unsigned)((n_merges + kWaves - 1) / kWaves));
-        hipLaunchKernelGGL((merge_wave_kernel<DT, DP>), grid, dim3(256), 0, stream, a, merges, (int)n_merges);
+        hipLaunchKernelGGL((merge_wave_kernel<DT, DP>), grid, dim3(256), 0, stream, merges, (int)n_merges, a);
     } else {
         const dim3 grid((unsigned)n_merges);
-        hipLaunchKernelGGL((merge_kernel<DT, DP>), grid, dim3(256), 0, stream, a, merges, (int)n_merges);
+        hipLaunchKernelGGL((merge_kernel<DT, DP>), grid, dim3(256), 0, stream, merges, (int)n_merges, a);
     }
     return check_launch();
 }
@@ -1847,7 +1889,7 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
             aw.num_items = 0;
             aw.dev_count = nullptr;
             hipLaunchKernelGGL((attn_kernel<DT, DP, 1, true, true>), dim3((unsigned)a.w_blocks), dim3(256),
-                               (attn_lds_bytes<DT, DP, 1, true>()), stream, aw);
+                               (attn_lds_bytes<DT, DP, 1, true>()), stream, aw.items, aw);
             if (int st = check_launch()) return st;
         }
     } else {
@@ -1886,10 +1928,10 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
         const dim3 grid((unsigned)(a.w_blocks + (n_narrow + kWaves - 1) / kWaves));
         if (fast)
             hipLaunchKernelGGL((attn_kernel<DT, DP, 1, true, TAIL>), grid, dim3(256),
-                               (attn_lds_bytes<DT, DP, 1, true>()), stream, a);
+                               (attn_lds_bytes<DT, DP, 1, true>()), stream, a.items, a);
         else if constexpr (!TAIL)
             hipLaunchKernelGGL((attn_kernel<DT, DP, 1, false>), grid, dim3(256), (attn_lds_bytes<DT, DP, 1, false>()),
-                               stream, a);
+                               stream, a.items, a);
         if (int st = check_launch()) return st;
         a.w_blocks = 0;
     }
@@ -1901,10 +1943,10 @@ int launch_attention(AttnArgs a, const int32_t* items, int64_t n_narrow, int64_t
             const dim3 grid((unsigned)(a.w_blocks + (n_wide + kWaves - 1) / kWaves));
             if (fast)
                 hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, true, TAIL>), grid, dim3(256),
-                                   (attn_lds_bytes<DT, DP, NTW, true>()), stream, a);
+                                   (attn_lds_bytes<DT, DP, NTW, true>()), stream, a.items, a);
             else if constexpr (!TAIL)
                 hipLaunchKernelGGL((attn_kernel<DT, DP, NTW, false>), grid, dim3(256),
-                                   (attn_lds_bytes<DT, DP, NTW, false>()), stream, a);
+                                   (attn_lds_bytes<DT, DP, NTW, false>()), stream, a.items, a);
             if (int st = check_launch()) return st;
         }
     } else {
@@ -1931,8 +1973,7 @@ int launch_slices(AttnArgs a, const int32_t* slices, int64_t n_slices, int hkv, 
     }
     if (n_merges > 0) {
 #if MF_SLICE_MERGE_WG
-        hipLaunchKernelGGL((merge_kernel<DT, DP>), dim3((unsigned)n_merges), dim3(256), 0, stream, a, merges,
-                           (int)n_merges);
+        hipLaunchKernelGGL((merge_kernel<DT, DP>), dim3((unsigned)n_merges), dim3(256), 0, stream, merges, (int)n_merges, a);
         if (int st = check_launch()) return st;
 #else
         if (int st = launch_merge<DT, DP>(a, merges, n_merges, stream)) return st;
