@@ -507,6 +507,11 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
         iv2 = *(const int4*)(it + 8);
         asm volatile("" ::"s"(iv0.x), "s"(iv0.y), "s"(iv0.z), "s"(iv0.w), "s"(iv1.x), "s"(iv1.y), "s"(iv1.z),
                      "s"(iv1.w), "s"(iv2.x), "s"(iv2.y), "s"(iv2.z), "s"(iv2.w));
+        // ... and so do the argument fields the next batch of loads (block
+        // table, row positions, Q) is addressed from, which otherwise come
+        // from argument cache lines fetched after the check
+        asm volatile("" ::"s"(a.block_tables), "s"(a.bt_stride), "s"(a.positions), "s"(a.pool_lens), "s"(a.q),
+                     "s"(a.q_sr), "s"(a.q_sh), "s"(a.G), "s"(a.row_map), "s"(a.q_sign));
     }
     const int num_items = a.dev_count ? *a.dev_count : a.num_items;
     if (item >= num_items) return;
