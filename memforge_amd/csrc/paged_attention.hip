@@ -1786,12 +1786,16 @@ void attn_slice_kernel(AttnArgs a, int num_slices, int hkv) {
 // min(mi, num_merges - 1): in bounds for every workgroup of the grid), so the
 // load goes out with the argument block's instead of one round trip after it;
 // the record list's address and num_merges are the preloaded first arguments.
-// The empty asm keeps the loads ahead of the check.
-__device__ __forceinline__ void load_merge_record(const int32_t* merges, int mi, int num_merges,
+// The argument fields the merge addresses its partials, row map and output
+// from are loaded in the same batch. The empty asm keeps the loads ahead of
+// the check.
+__device__ __forceinline__ void load_merge_record(const AttnArgs& a, const int32_t* merges, int mi, int num_merges,
                                                   int32_t (&mg)[MF_PLAN_MERGE_INTS]) {
     const int32_t* rec = merges + (int64_t)min(mi, num_merges - 1) * MF_PLAN_MERGE_INTS;
     const int4 r0 = *(const int4*)rec, r1 = *(const int4*)(rec + 4);
     asm volatile("" ::"s"(r0.x), "s"(r0.y), "s"(r0.z), "s"(r0.w), "s"(r1.x), "s"(r1.y), "s"(r1.z), "s"(r1.w));
+    asm volatile("" ::"s"(a.G), "s"(a.out), "s"(a.o_sr), "s"(a.o_sh), "s"(a.row_map), "s"(a.partials),
+                 "s"(a.part_dstride), "s"(a.head_dim));
     mg[0] = r0.x; mg[1] = r0.y; mg[2] = r0.z; mg[3] = r0.w;
     mg[4] = r1.x; mg[5] = r1.y; mg[6] = r1.z; mg[7] = r1.w;
 }
@@ -1807,7 +1811,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const int32_t* merges, int n
     __shared__ float s_o[kWaves][16][DP];
     const int mi = blockIdx.x;
     int32_t mg[MF_PLAN_MERGE_INTS];
-    load_merge_record(merges, mi, num_merges, mg);
+    load_merge_record(a, merges, mi, num_merges, mg);
     if (mi >= (a.dev_count ? *a.dev_count : num_merges)) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -1855,7 +1859,7 @@ __global__ __launch_bounds__(256) void merge_wave_kernel(const int32_t* merges, 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int mi = blockIdx.x * kWaves + wave;
     int32_t mg[MF_PLAN_MERGE_INTS];
-    load_merge_record(merges, mi, num_merges, mg);
+    load_merge_record(a, merges, mi, num_merges, mg);
     if (mi >= (a.dev_count ? *a.dev_count : num_merges)) return;
     const int lane = threadIdx.x & 63;
     merge_tile<DT, DP>(a, mg, lane >> 4, lane & 15);
