@@ -429,6 +429,17 @@ constexpr int attn_waves_per_eu() {
 #define MF_SLICE_MERGE_WG 0
 #endif
 
+// Tiles of extra work the planner charges to the last wave of a cooperative
+// unit that holds a multi-row sequence's last tile. Measured on C3's verify
+// layer (graph replays): 0 13.2 us, 2 12.96-12.99, 4 12.93-12.94, 6
+// 12.36-12.37, 8 12.34-12.37, 10 13.22-13.24, 12 13.18-13.19, 16 13.0. In an
+// instrumented build's timeline those waves started their key loop 1.1 us
+// after the unit's other waves and ran the boundary and in-flight tiles after
+// it, while the others waited at the combine.
+#ifndef MF_TAIL_WAVE_TILES
+#define MF_TAIL_WAVE_TILES 6
+#endif
+
 #ifndef MF_NARROW_DEPTH
 #define MF_NARROW_DEPTH 3
 #endif
@@ -2404,10 +2415,21 @@ extern "C" int mf_attention_plan(int num_seqs, const int32_t* cu_seqlens, const 
                             singles.push_back(make(gi, p, h, k0, k1));
                             continue;
                         }
-                        // four waves on consecutive quarters of [k0, k1)
+                        // four waves on consecutive quarters of [k0, k1). In
+                        // the unit holding a multi-row sequence's last tile (a
+                        // verify pass: the boundary tile and the in-flight
+                        // candidates, loaded key by key), the last wave counts
+                        // MF_TAIL_WAVE_TILES more tiles than it has, so the
+                        // others take them and the unit's waves reach its
+                        // LDS combine together.
                         const int n = k1 - k0;
+                        const int rows = cu_seqlens[s + 1] - cu_seqlens[s];
+                        const int extra = (k1 == tiles && rows > 1) ? MF_TAIL_WAVE_TILES : 0;
+                        auto cut = [&](int w) {
+                            return w >= U ? k1 : std::min(k1, k0 + (int)((int64_t)w * (n + extra) / U));
+                        };
                         for (int w = 0; w < U; ++w) {
-                            Item o = make(gi, p, h, k0 + (int)((int64_t)w * n / U), k0 + (int)((int64_t)(w + 1) * n / U));
+                            Item o = make(gi, p, h, cut(w), cut(w + 1));
                             o[11] = 1;
                             coop_items.push_back(o);
                         }

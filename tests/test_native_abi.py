@@ -598,3 +598,28 @@ def test_uploads_refuse_graph_capture(monkeypatch):
             call()
     # a CPU destination is never captured
     assert nat.upload(parts, "cpu")[0].tolist() == [0, 1, 2, 3]
+
+
+def test_plan_verify_units_give_the_last_wave_fewer_tiles():
+    """In the cooperative unit that holds a multi-row sequence's last tile (a
+    verify pass: boundary and in-flight tiles), the last wave's quarter is
+    shorter than the others'; the quarters still tile the unit's range. Single
+    rows (decodes) keep even quarters."""
+    P = 8
+    kv = [32 * 16, 32 * 16]
+    verify = _plan([0, 5, 6], kv, hq=8, hkv=2, pt=P)     # 5 rows, then 1 row
+    items = verify.items_host[: verify.n_narrow]
+    units = {}
+    for u in range(0, items.shape[0], 4):
+        unit = items[u:u + 4]
+        if int(unit[0][11]) == 1:
+            units.setdefault(int(unit[0][0]), []).append(unit)
+    for s, us in units.items():
+        for unit in us:
+            assert all(int(unit[w][5]) == int(unit[w + 1][4]) for w in range(3))
+            lens = [int(unit[w][5] - unit[w][4]) for w in range(4)]
+            assert int(unit[0][4]) == 0 and int(unit[3][5]) == 32 and sum(lens) == 32
+            if s == 0:
+                assert lens[3] < min(lens[:3]), lens
+            else:
+                assert max(lens) - min(lens) <= 1, lens
