@@ -304,43 +304,56 @@ __device__ __forceinline__ void store_out_chunk(char* p, const float* vals) {
 
 // ------------------------------------------------------------- split-K merge
 // Partials of one 16-column tile (merge record `mg`) live in slots
-// slot0 + p*sstride, p < np; each slot holds [16 columns][part_dstride] fp32
-// unnormalised outputs followed by 16 running maxima and 16 sums. The merged
-// output is sum_p w_p acc_p / sum_p w_p l_p with w_p = 2^(m_p - max_p m_p).
-//
+// slot0 + p*sstride, p < np. A slot holds, per column, the partition's
+// normalised output o_p / l_p in the launch's element type (column c at
+// element c*part_dstride), then 16 running maxima m_p and 16 sums l_p (fp32,
+// at float 16*part_dstride). The merged output is
+// sum_p w_p l_p (o_p / l_p) / sum_p w_p l_p with w_p = 2^(m_p - max_p m_p).
+// A normalised output is a convex combination of V rows, so it keeps the
+// output type's range; 16-bit partials halve the bytes written and merged
+// against fp32 ones, for one more rounding to that type.
+template <int DT>
+__device__ __forceinline__ char* partial_out(const AttnArgs& a, int64_t slot, int col, int elem) {
+    constexpr int ES = DT == MF_F32 ? 4 : 2;
+    return (char*)(a.partials + slot * (16 * (int64_t)(a.part_dstride + 2))) +
+           ((int64_t)col * a.part_dstride + elem) * ES;
+}
+__device__ __forceinline__ float* partial_ml(const AttnArgs& a, int64_t slot) {
+    return a.partials + slot * (16 * (int64_t)(a.part_dstride + 2)) + 16 * a.part_dstride;
+}
+
 // merge_range accumulates partitions p0, p0+pinc, ... relative to their own
 // maximum `mx` (lane (g, j): column j, head_dim range [4g*VCH, 4g*VCH+4*VCH)).
 // Partitions go four at a time with every load of a batch issued before any
 // is used (a batch past the last partition loads only what exists; the
 // condition is wave-uniform), and the running maximum moves batch to batch:
 // a merge of n partitions per wave costs ceil(n/4) memory round trips.
-template <int DP>
+template <int DT, int DP>
 __device__ __forceinline__ void merge_range(const AttnArgs& a, const int32_t* mg, int p0, int pinc, int j,
                                             int dbase, float& mx, float& L, float (&o)[DP / 4]) {
     constexpr int VCH = DP / 16;
     constexpr int B = 4;
+    constexpr int ES = DT == MF_F32 ? 4 : 2;
+    constexpr int NW = 4 * VCH * ES / 4;  // words of the lane's chunk
     const int np = mg[3], slot0 = mg[4], sstride = mg[5];
-    const int64_t stride = 16 * (int64_t)(a.part_dstride + 2);
-    const float* base = a.partials + (int64_t)slot0 * stride;
-    const int64_t pstep = (int64_t)sstride * stride;
-    const int moff = 16 * a.part_dstride + j;
     mx = kMinM;
     L = 0.f;
 #pragma unroll
     for (int e = 0; e < 4 * VCH; ++e) o[e] = 0.f;
     for (int p = p0; p < np; p += B * pinc) {
-        uint32_t raw[B][4 * VCH];
+        uint32_t raw[B][NW];
         float mb[B], lb[B];
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             if (p + b * pinc < np) {
-                const float* q = base + (int64_t)(p + b * pinc) * pstep;
-                ld_words<16 * VCH>((const char*)(q + j * a.part_dstride + dbase), raw[b]);
-                mb[b] = q[moff];
-                lb[b] = q[moff + 16];
+                const int64_t slot = slot0 + (int64_t)(p + b * pinc) * sstride;
+                ld_words<4 * VCH * ES>(partial_out<DT>(a, slot, j, dbase), raw[b]);
+                const float* ml = partial_ml(a, slot);
+                mb[b] = ml[j];
+                lb[b] = ml[16 + j];
             } else {
 #pragma unroll
-                for (int e = 0; e < 4 * VCH; ++e) raw[b][e] = 0u;
+                for (int e = 0; e < NW; ++e) raw[b][e] = 0u;
                 mb[b] = kMinM;
                 lb[b] = 0.f;
             }
@@ -354,10 +367,15 @@ __device__ __forceinline__ void merge_range(const AttnArgs& a, const int32_t* mg
         for (int e = 0; e < 4 * VCH; ++e) o[e] *= keep;
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const float w = __builtin_amdgcn_exp2f(mb[b] - bm);
-            L += lb[b] * w;
+            const float wl = __builtin_amdgcn_exp2f(mb[b] - bm) * lb[b];
+            L += wl;
 #pragma unroll
-            for (int e = 0; e < 4 * VCH; ++e) o[e] += w * __uint_as_float(raw[b][e]);
+            for (int e = 0; e < 4 * VCH; ++e) {
+                float v;
+                if constexpr (DT == MF_F32) v = __uint_as_float(raw[b][e]);
+                else v = bits_to_f32<DT>((raw[b][e >> 1] >> (16 * (e & 1))) & 0xffffu);
+                o[e] += wl * v;
+            }
         }
         mx = bm;
     }
@@ -388,7 +406,7 @@ __device__ __forceinline__ void merge_tile(const AttnArgs& a, const int32_t* mg,
     const int dbase = 4 * g * VCH;
     if (!merge_column(a, mg, j, prow, qhead) || dbase >= a.head_dim) return;
     float mx, L, o[4 * VCH];
-    merge_range<DP>(a, mg, 0, 1, j, dbase, mx, L, o);
+    merge_range<DT, DP>(a, mg, 0, 1, j, dbase, mx, L, o);
     const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
     for (int e = 0; e < 4 * VCH; ++e) o[e] *= inv;
@@ -1329,11 +1347,14 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                         store_elems<DT, VCH>(a.out + ((int64_t)prow[0] * a.o_sr + (int64_t)qhead[0] * a.o_sh + d0) * ES, o);
                     }
                 } else {
-                    float* ps = a.partials + (int64_t)pslot * (16 * (a.part_dstride + 2));
-                    store_elems<MF_F32, VCH>((char*)(ps + j * a.part_dstride + d0), o);
+                    const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+                    for (int c = 0; c < VCH; ++c) o[c] *= inv;
+                    store_elems<DT, VCH>(partial_out<DT>(a, pslot, j, d0), o);
                     if (g == 0 && wave == 0) {
-                        ps[16 * a.part_dstride + j] = M;
-                        ps[16 * a.part_dstride + 16 + j] = L;
+                        float* ml = partial_ml(a, pslot);
+                        ml[j] = M;
+                        ml[16 + j] = L;
                     }
                 }
             }
@@ -1378,16 +1399,17 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a, const int block) {
                 store_out_chunk<DT, VCH>(op, vals);
             }
         } else {
-            float* ps = a.partials + (int64_t)(pslot + nt) * (16 * (a.part_dstride + 2));
+            const float inv = lt > 0.f ? 1.f / lt : 0.f;
             float vals[4 * VCH];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int c = 0; c < VCH; ++c) vals[r * VCH + c] = acc[nt][c][r];
-            store_out_chunk<MF_F32, VCH>((char*)(ps + j * a.part_dstride + dbase), vals);
+                for (int c = 0; c < VCH; ++c) vals[r * VCH + c] = acc[nt][c][r] * inv;
+            store_out_chunk<DT, VCH>(partial_out<DT>(a, pslot + nt, j, dbase), vals);
             if (g == 0) {
-                ps[16 * a.part_dstride + j] = m[nt];
-                ps[16 * a.part_dstride + 16 + j] = lt;
+                float* ml = partial_ml(a, pslot + nt);
+                ml[j] = m[nt];
+                ml[16 + j] = lt;
             }
         }
     }
@@ -1776,16 +1798,17 @@ void attn_slice_kernel(AttnArgs a, int num_slices, int hkv) {
                 store_out_chunk<DT, VCH>(a.out + ((int64_t)row * a.o_sr + (int64_t)qhead * a.o_sh + dbase) * ES, vals);
             } else {
                 const int pslot = slot0 + h * __builtin_amdgcn_readlane(r1.z, si) + __builtin_amdgcn_readlane(r1.w, si);
-                float* ps = a.partials + (int64_t)pslot * (16 * (a.part_dstride + 2));
+                const float inv = lt > 0.f ? 1.f / lt : 0.f;
                 float vals[4 * VCH];
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
-                    for (int c = 0; c < VCH; ++c) vals[r * VCH + c] = acc[c][r];
-                store_out_chunk<MF_F32, VCH>((char*)(ps + j * a.part_dstride + dbase), vals);
+                    for (int c = 0; c < VCH; ++c) vals[r * VCH + c] = acc[c][r] * inv;
+                store_out_chunk<DT, VCH>(partial_out<DT>(a, pslot, j, dbase), vals);
                 if (g == 0) {
-                    ps[16 * a.part_dstride + j] = m;
-                    ps[16 * a.part_dstride + 16 + j] = lt;
+                    float* ml = partial_ml(a, pslot);
+                    ml[j] = m;
+                    ml[16 + j] = lt;
                 }
             }
         }
@@ -1833,7 +1856,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const int32_t* merges, int n
     float mx = kNegInf, L = 0.f, o[4 * VCH];
 #pragma unroll
     for (int e = 0; e < 4 * VCH; ++e) o[e] = 0.f;
-    if (active) merge_range<DP>(a, mg, wave, kWaves, j, dbase, mx, L, o);
+    if (active) merge_range<DT, DP>(a, mg, wave, kWaves, j, dbase, mx, L, o);
     if (g == 0) {
         s_m[wave][j] = mx;
         s_l[wave][j] = L;
