@@ -430,21 +430,8 @@ constexpr int attn_waves_per_eu() {
 // and three fit the two-waves-per-SIMD budget.
 // One launch for plans holding both single-tile and wide items (see
 // attn_mixed_kernel); 0 launches them one after the other.
-// Merge launches of at least this many records run one wave per record
-// (merge_wave_kernel); smaller ones one workgroup per record (merge_kernel),
-// whose four waves split the record's partitions. Measured on MI355X: C2
-// (2,045 records) 12.2 us against 13.4 us, C5 (136 records) 7.9 against
-// 8.5 us; C3 (75 records, 19 workgroups in the wave form) 0.35 us slower.
-#ifndef MF_MERGE_WAVE_MIN
-#define MF_MERGE_WAVE_MIN 128
-#endif
-
 #ifndef MF_MIXED_LAUNCH
 #define MF_MIXED_LAUNCH 1
-#endif
-
-#ifndef MF_SLICE_MERGE_WG
-#define MF_SLICE_MERGE_WG 0
 #endif
 
 // Tiles of extra work the planner charges to the last wave of a cooperative
@@ -1834,64 +1821,16 @@ __device__ __forceinline__ void load_merge_record(const AttnArgs& a, const int32
     mg[4] = r1.x; mg[5] = r1.y; mg[6] = r1.z; mg[7] = r1.w;
 }
 
-// One workgroup per merge record: wave w merges partitions w, w+4, ... and the
-// four partial results are combined through LDS by wave 0.
+// One wave per merge record, each record a workgroup of its own: the wave
+// loads its record's partitions four at a time (merge_range) and writes the
+// output directly, with no LDS combine or barrier. Measured on MI355X against
+// the two earlier forms (four waves per record splitting its partitions and
+// combining them in LDS below 128 records, four records per workgroup above):
+// C3's verify layer (75 records) 11.36-11.38 us against 12.29-12.40, the C2
+// layer (1,955 records) 37.9-38.1 against 38.2-38.3, C5 (824) the same.
 template <int DT, int DP>
-__global__ __launch_bounds__(256) void merge_kernel(const int32_t* merges, int num_merges, AttnArgs a) {
-    constexpr int VCH = DP / 16;
-    constexpr int ES = DT == MF_F32 ? 4 : 2;
-    constexpr float kNegInf = -__builtin_huge_valf();
-    __shared__ float s_m[kWaves][16], s_l[kWaves][16];
-    __shared__ float s_o[kWaves][16][DP];
+__global__ __launch_bounds__(64) void merge_kernel(const int32_t* merges, int num_merges, AttnArgs a) {
     const int mi = blockIdx.x;
-    int32_t mg[MF_PLAN_MERGE_INTS];
-    load_merge_record(a, merges, mi, num_merges, mg);
-    if (mi >= (a.dev_count ? *a.dev_count : num_merges)) return;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4, j = lane & 15;
-    int prow = 0, qhead = 0;
-    const int dbase = 4 * g * VCH;
-    const bool active = merge_column(a, mg, j, prow, qhead) && dbase < a.head_dim;
-    float mx = kNegInf, L = 0.f, o[4 * VCH];
-#pragma unroll
-    for (int e = 0; e < 4 * VCH; ++e) o[e] = 0.f;
-    if (active) merge_range<DT, DP>(a, mg, wave, kWaves, j, dbase, mx, L, o);
-    if (g == 0) {
-        s_m[wave][j] = mx;
-        s_l[wave][j] = L;
-    }
-#pragma unroll
-    for (int e = 0; e < 4 * VCH; ++e) s_o[wave][j][dbase + e] = o[e];
-    __syncthreads();
-    if (wave != 0 || !active) return;
-    float gm = kNegInf;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) gm = fmaxf(gm, s_m[w][j]);
-    float tot = 0.f, res[4 * VCH];
-#pragma unroll
-    for (int e = 0; e < 4 * VCH; ++e) res[e] = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-        const float mw = s_m[w][j];
-        const float sc = (mw == kNegInf) ? 0.f : exp2f(mw - gm);
-        tot += s_l[w][j] * sc;
-#pragma unroll
-        for (int e = 0; e < 4 * VCH; ++e) res[e] += s_o[w][j][dbase + e] * sc;
-    }
-    const float inv = tot > 0.f ? 1.f / tot : 0.f;
-#pragma unroll
-    for (int e = 0; e < 4 * VCH; ++e) res[e] *= inv;
-    store_out_chunk<DT, VCH>(a.out + ((int64_t)prow * a.o_sr + (int64_t)qhead * a.o_sh + dbase) * ES, res);
-}
-
-// One wave per merge record, four records per workgroup: the wave loads its
-// record's partitions four at a time (merge_range) and writes the output
-// directly, with no LDS combine or barrier.
-template <int DT, int DP>
-__global__ __launch_bounds__(256) void merge_wave_kernel(const int32_t* merges, int num_merges, AttnArgs a) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int mi = blockIdx.x * kWaves + wave;
     int32_t mg[MF_PLAN_MERGE_INTS];
     load_merge_record(a, merges, mi, num_merges, mg);
     if (mi >= (a.dev_count ? *a.dev_count : num_merges)) return;
@@ -1899,17 +1838,11 @@ __global__ __launch_bounds__(256) void merge_wave_kernel(const int32_t* merges, 
     merge_tile<DT, DP>(a, mg, lane >> 4, lane & 15);
 }
 
-// The split-K merge launch: one wave per record for large launches, one
-// workgroup per record (four waves splitting its partitions) for small ones.
+// The split-K merge launch: one single-wave workgroup per record.
 template <int DT, int DP>
 int launch_merge(const AttnArgs& a, const int32_t* merges, int64_t n_merges, hipStream_t stream) {
-    if (n_merges >= MF_MERGE_WAVE_MIN) {
-        const dim3 grid((unsigned)((n_merges + kWaves - 1) / kWaves));
-        hipLaunchKernelGGL((merge_wave_kernel<DT, DP>), grid, dim3(256), 0, stream, merges, (int)n_merges, a);
-    } else {
-        const dim3 grid((unsigned)n_merges);
-        hipLaunchKernelGGL((merge_kernel<DT, DP>), grid, dim3(256), 0, stream, merges, (int)n_merges, a);
-    }
+    hipLaunchKernelGGL((merge_kernel<DT, DP>), dim3((unsigned)n_merges), dim3(64), 0, stream, merges, (int)n_merges,
+                       a);
     return check_launch();
 }
 
@@ -2015,12 +1948,7 @@ int launch_slices(AttnArgs a, const int32_t* slices, int64_t n_slices, int hkv, 
         if (int st = check_launch()) return st;
     }
     if (n_merges > 0) {
-#if MF_SLICE_MERGE_WG
-        hipLaunchKernelGGL((merge_kernel<DT, DP>), dim3((unsigned)n_merges), dim3(256), 0, stream, merges, (int)n_merges, a);
-        if (int st = check_launch()) return st;
-#else
         if (int st = launch_merge<DT, DP>(a, merges, n_merges, stream)) return st;
-#endif
     }
     return MF_OK;
 }
