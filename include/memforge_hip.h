@@ -178,7 +178,9 @@ int mf_ragged_pack(const int32_t* entries, int num_entries,
  * zero one gives uniform weights), a NaN or infinite one is MF_ERR_ARG.
  * Softmax accumulates in fp32; out is written in `dtype` (the q/K/V dtype).
  * Work is described by a plan from mf_attention_plan (device copy of its
- * items/merges); `partials` is fp32 scratch of at least the planned size.
+ * items/merges; num_items_narrow and num_items_wide are multiples of four, as
+ * the planner makes them, else MF_ERR_ARG); `partials` is fp32 scratch of at
+ * least the planned size.
  * merge_counters (device int32[num_merges], all-zero on entry and again on
  * exit) lets the attention kernel merge split-K partitions itself: the last
  * partition of a group to finish merges it. With merge_counters NULL a
@@ -215,7 +217,8 @@ int mf_paged_attention(const void* q, int64_t q_stride_row, int64_t q_stride_hea
  * caller that captures the launch in a HIP graph and replays it with a new
  * plan each step. No counterpart in the reference: it serves callers that
  * capture the decode step (the grid must be fixed at capture time).
- * The grids are sized by the capacities: plan_items holds capacity_narrow
+ * The grids are sized by the capacities (multiples of four, else MF_ERR_ARG):
+ * plan_items holds capacity_narrow
  * narrow items followed by capacity_wide wide items (wide items always start
  * at plan_items + capacity_narrow * MF_PLAN_ITEM_INTS), plan_merges holds
  * capacity_merges records, and device_counts (device, int32[3]) gives the

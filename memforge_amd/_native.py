@@ -552,11 +552,14 @@ class CountedPlan:
     (mf_paged_attention_counted): the shapes and addresses a captured HIP
     graph recorded stay valid while ``update`` swaps in each step's plan.
 
-    Items hold ``cap_narrow`` narrow then ``cap_wide`` wide rows; ``update``
-    raises if a plan does not fit. Host staging is pinned; each update waits
-    for the previous one's copies before reusing it."""
+    Items hold ``cap_narrow`` narrow then ``cap_wide`` wide rows, each
+    capacity rounded up to whole workgroups of four (the launch's grid, whose
+    waves read their items before the live-count check); ``update`` raises if
+    a plan does not fit. Host staging is pinned; each update waits for the
+    previous one's copies before reusing it."""
 
     def __init__(self, cap_narrow: int, cap_wide: int, cap_merges: int, partials_floats: int, device):
+        cap_narrow, cap_wide = -(-cap_narrow // 4) * 4, -(-cap_wide // 4) * 4
         self.cap_narrow, self.cap_wide, self.cap_merges = cap_narrow, cap_wide, cap_merges
         rows = max(cap_narrow + cap_wide, 1)
         self.items = torch.zeros((rows, PLAN_ITEM_INTS), dtype=torch.int32, device=device)

@@ -2728,6 +2728,10 @@ int paged_attention_impl(
     if (!q || !out || !k_pool || !v_pool || !block_tables || !cu_seqlens || !kv_lens || !positions)
         return MF_ERR_ARG;
     if (num_items_narrow + num_items_wide > 0 && !plan_items) return MF_ERR_ARG;
+    // Range-plan items run in workgroups of four and a wave loads its item
+    // before its count check: both counts are whole workgroups, as plans make
+    // them (a slice plan's counts are slices and segments).
+    if (!sliced && ((num_items_narrow % kWaves) || (num_items_wide % kWaves))) return MF_ERR_ARG;
     if (pool_lens && (!new_k || !new_v)) return MF_ERR_ARG;
     if (num_merges > 0 && (!plan_merges || !partials || partials_floats <= 0)) return MF_ERR_WORKSPACE;
     // 16-byte row loads need 16-byte aligned rows.

@@ -652,3 +652,35 @@ def test_verify_pass_without_a_row_map(device, dtype):
                                  bs, pool_lens=ctx, new_k=to_np64(nk), new_v=to_np64(nv),
                                  new_rows=[list(range(cu[b], cu[b + 1])) for b in range(B)])
     _check(to_np64(plain.permute(1, 0, 2)), want, dt)
+
+
+def test_item_counts_are_whole_workgroups(device):
+    """A wave reads its item before its count check, so a range plan's item
+    counts must be whole workgroups of four: a call with any other count is
+    refused before launch, and counted plans round their capacities up."""
+    from memforge_amd import _native as nat
+
+    gen = torch.Generator().manual_seed(3)
+    bs, hq, hkv, d = 16, 8, 2, 64
+    kvl = [40, 300, 700]
+    tables = random_tables(gen, sum((c + bs - 1) // bs for c in kvl) + 1, kvl, bs)
+    kp, vp = _pool(gen, max(max(t) for t in tables) + 1, bs, hkv, d, torch.bfloat16, device)
+    q = torch.randn((3, hq, d), generator=gen).to(torch.bfloat16).to(device)
+    bt = torch.zeros((3, max(len(t) for t in tables)), dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    cu = [0, 1, 2, 3]
+    plan = nat.plan_attention(cu, kvl, hq, hkv, d, torch.bfloat16, device)
+    assert plan.n_narrow % 4 == 0 and plan.n_narrow >= 4
+    args = (nat.PoolView.from_bshd(kp, vp), bt.to(device), torch.tensor(cu, dtype=torch.int32, device=device),
+            torch.tensor(kvl, dtype=torch.int32, device=device),
+            torch.tensor([c - 1 for c in kvl], dtype=torch.int64, device=device))
+    out = torch.empty_like(q)
+    nat.paged_attention(q, out, *args, plan, 0.125, hkv)
+    odd = nat.AttentionPlan(plan.items, plan.merges, plan.n_narrow - 1, plan.n_wide, plan.n_merges,
+                            plan.partials_floats, plan.items_host, plan.merges_host)
+    with pytest.raises(nat.MemforgeHipError, match="invalid argument"):
+        nat.paged_attention(q, out, *args, odd, 0.125, hkv)
+    counted = nat.CountedPlan(5, 3, 1, 1024, device)
+    assert (counted.cap_narrow, counted.cap_wide) == (8, 4)
+    assert counted.items.shape[0] == 12
