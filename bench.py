@@ -44,7 +44,7 @@ B, HQ, HKV, D, BS, LAYERS = 256, 40, 8, 128, 16, 48
 # WRITE_SIZE all (x1.0). None: not measured for that kernel yet.
 PMC_DEFAULT = {
     "ranges": {"fetch_kib": 1619051.2, "write_kib": 3210.7, "fetch_scale": 2.0, "write_scale": 1.0},
-    "slices": {"fetch_kib": 1609361.8, "write_kib": 6224.9, "fetch_scale": 2.0, "write_scale": 1.0},
+    "slices": {"fetch_kib": 1609298.0, "write_kib": 3934.5, "fetch_scale": 2.0, "write_scale": 1.0},
 }
 
 
