@@ -184,20 +184,6 @@ __device__ float block_sum(float v, float* sh) {
 }
 
 template <int NW>
-__device__ float block_max(float v, float* sh) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) sh[w] = v;
-    __syncthreads();
-    float t = sh[0];
-#pragma unroll
-    for (int k = 1; k < NW; ++k) t = fmaxf(t, sh[k]);
-    return t;
-}
-
-template <int NW>
 __device__ void block_argmax(float& v, int& i, float* shv, int* shi) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -262,7 +248,10 @@ __global__ __launch_bounds__(kStatThreads) void row_stats_kernel(VerifyArgs a) {
                 }
             }
         }
-        const float gm = block_max<4>(m, shv);
+        // the chunk's max of x / T is its max raw logit (the argmax above,
+        // every thread holding it) divided once: division by T > 0 is
+        // monotone, so no second max reduction is needed
+        const float gm = am == kNegInf ? kNegInf : (unit ? am : am / T);
         const float scaled = (m == kNegInf) ? 0.f : s * expf(m - gm);
         const float tot = block_sum<4>(scaled, shs);
         if (threadIdx.x == 0) {
@@ -401,8 +390,6 @@ __device__ __forceinline__ void accept_row(const VerifyArgs& a, int b, float* s_
 // rejected), and the chunk's "has mass" bits.
 template <int DT>
 __global__ __launch_bounds__(kPassThreads) void draw_kernel(VerifyArgs a) {
-    __shared__ float shv[kPassThreads / 64];
-    __shared__ int shi[kPassThreads / 64];
     __shared__ float s_max[kMaxPositions], s_sum[kMaxPositions];
     __shared__ int s_arg[kMaxPositions];
     __shared__ int s_stop, s_reject;
@@ -465,24 +452,47 @@ __global__ __launch_bounds__(kPassThreads) void draw_kernel(VerifyArgs a) {
         }
     const int64_t po = (int64_t)b * a.npass + c;
     const int64_t fam = (int64_t)a.B * a.npass;
+    // the three families' winners and the mass bits: each wave's by
+    // shuffles, then the waves' through LDS in one round (the first-index
+    // argmax order is total, so any combining order gives the same winner)
+    constexpr int NW = kPassThreads / 64;
+    __shared__ float s_best[3][NW];
+    __shared__ int s_best_i[3][NW], s_any[NW];
 #pragma unroll
-    for (int f = 0; f < 3; ++f) {
-        block_argmax<kPassThreads / 64>(best[f], best_i[f], shv, shi);
-        if (threadIdx.x == 0) {
-            a.part_best[f * fam + po] = best[f];
-            a.part_best_i[f * fam + po] = best_i[f];
+    for (int off = 32; off >= 1; off >>= 1) {
+        any |= __shfl_xor(any, off, 64);
+#pragma unroll
+        for (int f = 0; f < 3; ++f) {
+            const float ov = __shfl_xor(best[f], off, 64);
+            const int oi = __shfl_xor(best_i[f], off, 64);
+            argmax_merge(best[f], best_i[f], ov, oi);
         }
     }
-    // OR of the lanes' bits, through the argmax scratch
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) any |= __shfl_xor(any, off, 64);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) shi[threadIdx.x >> 6] = any;
+        for (int f = 0; f < 3; ++f) {
+            s_best[f][w] = best[f];
+            s_best_i[f][w] = best_i[f];
+        }
+        s_any[w] = any;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
         int t = 0;
 #pragma unroll
-        for (int w = 0; w < kPassThreads / 64; ++w) t |= shi[w];
+        for (int k = 0; k < NW; ++k) {
+            t |= s_any[k];
+            if (k > 0) {
+#pragma unroll
+                for (int f = 0; f < 3; ++f) argmax_merge(best[f], best_i[f], s_best[f][k], s_best_i[f][k]);
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < 3; ++f) {
+            a.part_best[f * fam + po] = best[f];
+            a.part_best_i[f * fam + po] = best_i[f];
+        }
         a.part_any[po] = t;
     }
 }
