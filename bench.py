@@ -1019,7 +1019,8 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "bench.py measures one GPU: every box in this run has a single "
-                                   "MI355X and the data path is per-GPU (see DESIGN.md for sharding)"}))
+                                   "MI355X, and the data path is per GPU (across GPUs it shards by "
+                                   "request, each GPU with its own pool)"}))
         sys.exit(2)
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no HIP device"}))
